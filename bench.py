@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantised decode GEMV on one MI355X.
+
+Headline (`value`): gncx_xfold_universal_matvec on Q4_K 4096 -> 14336 (the
+gate/up GEMV of Llama-3-8B / Qwen3-8B-sized models) with weights, x and y
+resident in HBM, as whole-job throughput in GB/s of algorithmic bytes
+(weights once + fp32 x + fp32 y per step).  One step is one matvec call
+(activation quantisation and the GEMV run in one kernel).  Weight copies are
+rotated so the working set (> 512 MB) cannot sit in the 256 MB Infinity Cache.
+
+Also reported: `roofline` of that kernel (HIP-event durations on the
+library's stream), `cpu_baseline` (the reference library compiled from its
+own source, timed on this host on a bounded sample), and `extra` figures for
+the other decode GEMV shapes and the decode-attention step.
+
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-extra]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+HBM_PEAK_GBPS = 8000.0
+METRIC = "Q4_K GEMV HBM GB/s (% of peak); decode tok/s, Qwen3-8B-shaped, 1 GPU"
+
+
+def import_pkg():
+    import importlib.util
+    root = ROOT / "gnc-x_amd"
+    if "gncx_amd" not in sys.modules:
+        spec = importlib.util.spec_from_file_location("gncx_amd", root / "__init__.py",
+                                                      submodule_search_locations=[str(root)])
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules["gncx_amd"] = mod
+        spec.loader.exec_module(mod)
+    import gncx_amd.synth  # noqa: F401
+    return sys.modules["gncx_amd"]
+
+
+class HipEvents:
+    """hipEvent pairs recorded on the library's stream."""
+
+    def __init__(self, stream: int):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+
+    def create(self, n: int):
+        evs = []
+        for _ in range(n):
+            e = C.c_void_p()
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+            evs.append(e)
+        return evs
+
+    def record(self, e):
+        assert self.hip.hipEventRecord(e, self.stream) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = C.c_float()
+        assert self.hip.hipEventSynchronize(b) == 0
+        assert self.hip.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+
+
+def gemv_bytes(pkg, t: int, k: int, n: int) -> int:
+    return pkg.row_bytes(t, k) * n + 4 * k + 4 * n
+
+
+def time_gemv(pkg, lib, torch, t, k, n, steps, warmup, copies, seed=1):
+    """Returns dict: wall ms/step, mean/median kernel us (events), GB/s."""
+    w_host = pkg.synth.make_weights(t, n, k, seed=seed)
+    x_host = pkg.synth.make_activations(1, k, seed=seed + 1)
+    ws = [torch.from_numpy(w_host).cuda() for _ in range(copies)]
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.zeros(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    fn = lib.gncx_xfold_universal_matvec
+    wp = [w.data_ptr() for w in ws]
+    xp, yp = x.data_ptr(), y.data_ptr()
+    for i in range(warmup):
+        fn(wp[i % copies], 0, t, xp, None, k, n, yp, None)
+    torch.cuda.synchronize()
+    pkg.check(lib)
+    # wall-clock pass: K back-to-back steps
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(wp[i % copies], 0, t, xp, None, k, n, yp, None)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    pkg.check(lib)
+    # event pass: one event pair around every launch on the library stream
+    ev = HipEvents(lib.gncx_hip_get_stream() or 0)
+    evs = ev.create(2 * steps)
+    for i in range(steps):
+        ev.record(evs[2 * i])
+        fn(wp[i % copies], 0, t, xp, None, k, n, yp, None)
+        ev.record(evs[2 * i + 1])
+    torch.cuda.synchronize()
+    dur = np.array([ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]) * 1e3
+    ev.destroy(evs)
+    nbytes = gemv_bytes(pkg, t, k, n)
+    del ws
+    torch.cuda.empty_cache()
+    return {
+        "bytes": nbytes,
+        "wall_ms": wall_ms,
+        "kernel_us_mean": float(dur.mean()),
+        "kernel_us_median": float(np.median(dur)),
+        "gbps_wall": nbytes / (wall_ms * 1e-3) / 1e9,
+        "gbps_kernel": nbytes / (dur.mean() * 1e-6) / 1e9,
+        "w_host": w_host,
+        "x_host": x_host,
+    }
+
+
+def time_attention(lib, torch, H, KV, hd, ctx, sw, steps, copies):
+    """Device-resident KV caches (N(0,1)), one step at pos = ctx - 1."""
+    g = torch.Generator(device="cuda").manual_seed(ctx + sw + KV)
+    kcs = [torch.randn(ctx, KV * hd, device="cuda", generator=g) for _ in range(copies)]
+    vcs = [torch.randn(ctx, KV * hd, device="cuda", generator=g) for _ in range(copies)]
+    q = torch.randn(H * hd, device="cuda", generator=g)
+    kn = torch.randn(KV * hd, device="cuda", generator=g)
+    vn = torch.randn(KV * hd, device="cuda", generator=g)
+    out = torch.zeros(H * hd, device="cuda")
+    torch.cuda.synchronize()
+    fn = lib.gncx_mqa_attention_step_ext
+    args = lambda i: (q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kcs[i % copies].data_ptr(),  # noqa: E731
+                      vcs[i % copies].data_ptr(), ctx - 1, H, KV, hd, 1.0 / np.sqrt(hd), sw, 1, out.data_ptr())
+    for i in range(5):
+        fn(*args(i))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(*args(i))
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) * 1e6 / steps
+    win = min(ctx, sw) if sw > 0 else ctx
+    nbytes = 2 * 4 * KV * hd * win + 4 * (2 * H * hd + 2 * KV * hd)
+    del kcs, vcs
+    torch.cuda.empty_cache()
+    return {"us_per_step": wall_us, "bytes": nbytes, "gbps": nbytes / (wall_us * 1e-6) / 1e9}
+
+
+def cpu_baseline(pkg, t, k, n, w_host, x_host, seconds=10.0):
+    """The reference's own matvec (compiled from its source) on this host's
+    cores with its default pool size, clamp(hardware threads, 2, 12)
+    (csrc/gncx_llm_kernels.cpp:139-141); the oracle restatement (1 thread)
+    if the reference build is absent."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle
+    nbytes = gemv_bytes(pkg, t, k, n)
+    try:
+        impl, kind = pyoracle.Reference(), "reference"
+        cores = min(max(os.cpu_count() or 1, 2), 12)
+    except FileNotFoundError:
+        impl, kind, cores = pyoracle.Oracle(), "port", 1
+    for _ in range(3):
+        impl.matvec(t, w_host, x_host, k, n)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        impl.matvec(t, w_host, x_host, k, n)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    cpu = platform.processor() or ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"{len(times)} calls of the same Q4_K {k}->{n} matvec (median {med * 1e3:.2f} ms), "
+                      f"{sum(times):.1f} s of CPU work, host '{cpu}', os.cpu_count()={os.cpu_count()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=16, help="weight copies rotated to defeat the MALL")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    pkg = import_pkg()
+    lib = pkg.load()
+    assert lib.gncx_hip_init(0) == 0, lib.gncx_hip_last_error()
+    lib.gncx_hip_set_stream(C.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+    t, k, n = pkg.Q4_K, 4096, 14336
+    head = time_gemv(pkg, lib, torch, t, k, n, args.steps, args.warmup, args.copies)
+    achieved = head["bytes"] / (head["kernel_us_mean"] * 1e-6) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "traffic_gemv_q4k_4096x14336.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+
+    extra = {}
+    if not args.no_extra:
+        gem = {}
+        for name, (tt, kk, nn, cp) in {
+            "q6k_14336x4096": (pkg.Q6_K, 14336, 4096, 12),
+            "q8_0_4096x4096": (pkg.Q8_0, 4096, 4096, 32),
+            "q4_0_4096x4096": (pkg.Q4_0, 4096, 4096, 64),
+            "q6k_4096x128256_lm_head": (pkg.Q6_K, 4096, 128256, 2),
+            "q4k_4096x4096": (pkg.Q4_K, 4096, 4096, 64),
+        }.items():
+            r = time_gemv(pkg, lib, torch, tt, kk, nn, max(50, args.steps // 2), 10, cp, seed=7)
+            gem[name] = {"gbps_wall": round(r["gbps_wall"], 1), "gbps_kernel": round(r["gbps_kernel"], 1),
+                         "kernel_us": round(r["kernel_us_mean"], 2), "frac_kernel": round(r["gbps_kernel"] / HBM_PEAK_GBPS, 4)}
+        extra["gemv"] = gem
+        att = {}
+        for name, (H, KV, hd, ctx, sw, cp) in {
+            "gqa32x8_ctx512": (32, 8, 128, 512, 0, 160), "gqa32x8_ctx4096": (32, 8, 128, 4096, 0, 16),
+            "gqa32x8_ctx32768": (32, 8, 128, 32768, 0, 3), "gqa32x8_swa1024": (32, 8, 128, 2048, 1024, 64),
+            "mqa32x1_ctx32768": (32, 1, 128, 32768, 0, 16),
+        }.items():
+            r = time_attention(lib, torch, H, KV, hd, ctx, sw, 50, cp)
+            att[name] = {"us_per_step": round(r["us_per_step"], 2), "gbps": round(r["gbps"], 1)}
+        extra["attention"] = att
+
+    cpu = None if args.no_cpu else cpu_baseline(pkg, t, k, n, head["w_host"], head["x_host"], args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbps_wall"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded GGUF Q4_K blocks, x ~ N(0,1))",
+        "config": {"workload": "gncx_matvec Q4_K 4096->14336 (gate/up decode GEMV)", "in_dim": k, "out_dim": n,
+                   "bytes_per_step": head["bytes"], "weight_copies_rotated": args.copies,
+                   "inputs": "resident in HBM (device pointers through the reference C-ABI)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel_us_mean": round(head["kernel_us_mean"], 3),
+                     "kernel_us_median": round(head["kernel_us_median"], 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

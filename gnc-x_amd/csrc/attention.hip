@@ -1,0 +1,357 @@
+// attention.hip -- GQA/MQA/SWA decode attention step for gfx950.
+//
+// Semantics of the reference's gncx_mqa_attention_step_ext
+// (csrc/gncx_llm_kernels.cpp:1887-1994): optionally store k_new/v_new at row
+// `pos` of the layer's KV cache, then for every query head h (KV head
+// h / (n_heads / n_kv_heads)) softmax((q . k_t) * scale) over the window
+// [max(0, pos - sw + 1), pos] and o = sum_t p_t v_t with the reference's
+// normaliser 1 / (sum + 1e-12).
+//
+// MI355X design (flash-decoding): the window is cut into chunks; one
+// work-group owns (KV head, chunk) and serves all query heads of its group, so
+// each KV row is read from HBM once (the reference re-reads it per query
+// head).  A token row of one KV head is read by hd/16 lanes with coalesced
+// 16-byte loads; scores go to LDS, each wave reduces one head's max/sum, the
+// V pass accumulates in registers and the waves combine through LDS.  A
+// second small kernel merges the chunk partials with the log-sum-exp rule.
+//
+// Optional fused prologue (cpp:895-953 per-head RMSNorm, then cpp:1797-1862
+// NEOX RoPE with a host-computed cos/sin table) is applied to q and k_new in
+// LDS before the scan, with the same arithmetic as the stand-alone kernels.
+#include <hip/hip_runtime.h>
+
+#include "gncx_device.h"
+#include "gncx_launch.h"
+
+namespace gncx {
+namespace {
+
+using namespace dev;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kHeadBlock = 4;     // query heads handled per pass (one wave each in the softmax)
+constexpr int kMaxChunk = 1024;   // tokens per work-group
+constexpr int kTargetGroups = 1024;
+
+struct AttnParams {
+    const float* q;
+    const float* k_new;
+    const float* v_new;
+    float* k_cache;
+    float* v_cache;
+    float* part_o;  // [n_split][n_heads][hd]
+    float* part_ml; // [n_split][n_heads][2]  (max, sum)
+    float* q_out;
+    float* k_out;
+    const float* q_gamma;
+    const float* k_gamma;
+    int32_t pos, n_heads, n_kv, t0, t1, chunk, use_new, norm_qk, has_rope;
+    float scale, eps;
+    RopeTable rope;
+};
+
+// Per-head RMSNorm then RoPE of one head held in LDS; one wave.
+template <int HD>
+__device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope, float eps,
+                              const RopeTable& t, int lane) {
+    if (norm) {
+        const float inv = head_inv_rms(v, HD, eps, lane);
+        for (int i = lane; i < HD; i += 64) {
+            const float x = __fmul_rn(v[i], inv);
+            v[i] = gamma ? __fmul_rn(x, gamma[i]) : x;
+        }
+    }
+    if (rope) {
+        constexpr int H = HD / 2;
+        for (int i = lane; i < H; i += 64) {
+            const float x1 = v[i], x2 = v[i + H];
+            v[i] = __fsub_rn(__fmul_rn(x1, t.c[i]), __fmul_rn(x2, t.s[i]));
+            v[i + H] = __fadd_rn(__fmul_rn(x2, t.c[i]), __fmul_rn(x1, t.s[i]));
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
+    constexpr int LPT = HD / 16;          // lanes per token row (16 dims each)
+    constexpr int TPP = kThreads / LPT;   // tokens per pass
+    extern __shared__ __align__(16) float smem[];
+    const int G = p.n_heads / p.n_kv;
+    float* sc = smem;                                   // [kHeadBlock][chunk]
+    float* red = sc + kHeadBlock * p.chunk;             // [kWaves][kHeadBlock][HD]
+    float* qs = red + kWaves * kHeadBlock * HD;         // [G][HD]  (prologue result)
+    float* ks = qs + G * HD;                            // [HD]
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int hk = blockIdx.x;
+    const int split = blockIdx.y;
+    const int ta = p.t0 + split * p.chunk;
+    const int tb = min(p.t1, ta + p.chunk);
+    const int j = tid % LPT;       // 16-dim slice of the row
+    const int ts = tid / LPT;      // token slot within a pass
+    const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
+
+    // ---- q (and k_new) into LDS, with the optional prologue ----
+    const float* qg = p.q + static_cast<size_t>(hk) * G * HD;
+    for (int i = tid; i < G * HD; i += kThreads) qs[i] = qg[i];
+    const bool have_new = p.use_new != 0;
+    if (have_new)
+        for (int i = tid; i < HD; i += kThreads) ks[i] = p.k_new[static_cast<size_t>(hk) * HD + i];
+    __syncthreads();
+    if (p.norm_qk || p.has_rope) {
+        for (int h = wv; h < G + (have_new ? 1 : 0); h += kWaves) {
+            if (h < G) prologue_head<HD>(qs + h * HD, p.q_gamma, p.norm_qk, p.has_rope, p.eps, p.rope, lane);
+            else prologue_head<HD>(ks, p.k_gamma, p.norm_qk, p.has_rope, p.eps, p.rope, lane);
+        }
+        __syncthreads();
+        if (split == 0) {
+            if (p.q_out)
+                for (int i = tid; i < G * HD; i += kThreads) p.q_out[static_cast<size_t>(hk) * G * HD + i] = qs[i];
+            if (p.k_out && have_new)
+                for (int i = tid; i < HD; i += kThreads) p.k_out[static_cast<size_t>(hk) * HD + i] = ks[i];
+        }
+    }
+    // the work-group whose chunk holds `pos` stores the new K/V row of its head
+    if (have_new && p.pos >= ta && p.pos < tb) {
+        float* kd = p.k_cache + static_cast<size_t>(p.pos) * kv_dim + static_cast<size_t>(hk) * HD;
+        float* vd = p.v_cache + static_cast<size_t>(p.pos) * kv_dim + static_cast<size_t>(hk) * HD;
+        const float* vn = p.v_new + static_cast<size_t>(hk) * HD;
+        for (int i = tid; i < HD; i += kThreads) {
+            kd[i] = ks[i];
+            vd[i] = vn[i];
+        }
+    }
+
+    for (int hb = 0; hb < G; hb += kHeadBlock) {
+        const int nh = min(kHeadBlock, G - hb);
+        // q slices of this lane
+        float4 qf[kHeadBlock][4];
+#pragma unroll
+        for (int h = 0; h < kHeadBlock; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                qf[h][c] = h < nh ? *reinterpret_cast<const float4*>(qs + (hb + h) * HD + 4 * (j + LPT * c))
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+
+        // ---- pass 1: scores ----
+        for (int t = ta; t < tb; t += TPP) {
+            const int tok = t + ts;
+            const bool valid = tok < tb;
+            float4 kf[4];
+            if (valid) {
+                const float* src = (have_new && tok == p.pos)
+                                       ? ks
+                                       : p.k_cache + static_cast<size_t>(tok) * kv_dim + static_cast<size_t>(hk) * HD;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kf[c] = *reinterpret_cast<const float4*>(src + 4 * (j + LPT * c));
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kf[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int h = 0; h < kHeadBlock; ++h) {
+                float s = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    s += qf[h][c].x * kf[c].x + qf[h][c].y * kf[c].y + qf[h][c].z * kf[c].z + qf[h][c].w * kf[c].w;
+#pragma unroll
+                for (int o = 1; o < LPT; o <<= 1) s += __shfl_xor(s, o, 64);
+                if (valid && j == 0 && h < nh) sc[h * p.chunk + (tok - ta)] = s * p.scale;
+            }
+        }
+        __syncthreads();
+
+        // ---- per-head max / exp / sum: wave h owns head h ----
+        const int len = tb - ta;
+        float mx = -1e30f, sum = 0.0f;
+        if (wv < nh) {
+            float* row = sc + wv * p.chunk;
+            for (int i = lane; i < len; i += 64) mx = fmaxf(mx, row[i]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            for (int i = lane; i < len; i += 64) {
+                const float e = expf(row[i] - mx);
+                row[i] = e;
+                sum += e;
+            }
+            sum = wave_sum(sum);
+        }
+        __syncthreads();
+
+        // ---- pass 2: o = sum_t e_t v_t ----
+        float4 of[kHeadBlock][4];
+#pragma unroll
+        for (int h = 0; h < kHeadBlock; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) of[h][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int t = ta; t < tb; t += TPP) {
+            const int tok = t + ts;
+            if (tok < tb) {
+                const float* src = (have_new && tok == p.pos)
+                                       ? p.v_new + static_cast<size_t>(hk) * HD
+                                       : p.v_cache + static_cast<size_t>(tok) * kv_dim + static_cast<size_t>(hk) * HD;
+                float4 vf[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) vf[c] = *reinterpret_cast<const float4*>(src + 4 * (j + LPT * c));
+#pragma unroll
+                for (int h = 0; h < kHeadBlock; ++h) {
+                    const float w = h < nh ? sc[h * p.chunk + (tok - ta)] : 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        of[h][c].x += w * vf[c].x;
+                        of[h][c].y += w * vf[c].y;
+                        of[h][c].z += w * vf[c].z;
+                        of[h][c].w += w * vf[c].w;
+                    }
+                }
+            }
+        }
+        // reduce over the token slots of this wave (lanes with equal j)
+#pragma unroll
+        for (int h = 0; h < kHeadBlock; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int o = LPT; o < 64; o <<= 1) {
+                    of[h][c].x += __shfl_xor(of[h][c].x, o, 64);
+                    of[h][c].y += __shfl_xor(of[h][c].y, o, 64);
+                    of[h][c].z += __shfl_xor(of[h][c].z, o, 64);
+                    of[h][c].w += __shfl_xor(of[h][c].w, o, 64);
+                }
+        if (lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < kHeadBlock; ++h)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    *reinterpret_cast<float4*>(red + (wv * kHeadBlock + h) * HD + 4 * (j + LPT * c)) = of[h][c];
+        }
+        // per-head (max, sum) from the owning wave
+        if (wv < nh && lane == 0) {
+            float* ml = p.part_ml + (static_cast<size_t>(split) * p.n_heads + hk * G + hb + wv) * 2;
+            ml[0] = mx;
+            ml[1] = sum;
+        }
+        __syncthreads();
+        for (int i = tid; i < nh * HD; i += kThreads) {
+            const int h = i / HD, d = i % HD;
+            float acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) acc += red[(w * kHeadBlock + h) * HD + d];
+            p.part_o[(static_cast<size_t>(split) * p.n_heads + hk * G + hb + h) * HD + d] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12)
+__global__ void attn_merge_kernel(const float* __restrict part_o, const float* __restrict part_ml,
+                                  int32_t n_split, int32_t n_heads, int32_t hd, float* __restrict out) {
+    const int h = blockIdx.x;
+    float M = -1e30f;
+    for (int s = 0; s < n_split; ++s) M = fmaxf(M, part_ml[(static_cast<size_t>(s) * n_heads + h) * 2]);
+    float L = 0.0f;
+    for (int s = 0; s < n_split; ++s) {
+        const float* ml = part_ml + (static_cast<size_t>(s) * n_heads + h) * 2;
+        L += ml[1] * expf(ml[0] - M);
+    }
+    const float inv = __fdiv_rn(1.0f, L + 1e-12f);
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float acc = 0.0f;
+        for (int s = 0; s < n_split; ++s) {
+            const float m = part_ml[(static_cast<size_t>(s) * n_heads + h) * 2];
+            acc += part_o[(static_cast<size_t>(s) * n_heads + h) * hd + d] * expf(m - M);
+        }
+        out[static_cast<size_t>(h) * hd + d] = acc * inv;
+    }
+}
+
+struct Plan {
+    int32_t t0, t1, chunk, n_split;
+};
+
+Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv) {
+    Plan pl;
+    pl.t0 = sw > 0 ? (pos - sw + 1 > 0 ? pos - sw + 1 : 0) : 0;
+    pl.t1 = pos + 1;
+    const int32_t win = pl.t1 - pl.t0;
+    int32_t want = kTargetGroups / (n_kv > 0 ? n_kv : 1);
+    if (want < 1) want = 1;
+    int32_t chunk = (win + want - 1) / want;
+    chunk = ((chunk + 31) / 32) * 32;
+    if (chunk < 32) chunk = 32;
+    if (chunk > kMaxChunk) chunk = kMaxChunk;
+    pl.chunk = chunk;
+    pl.n_split = (win + chunk - 1) / chunk;
+    return pl;
+}
+
+template <int HD>
+hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* part_ml, hipStream_t stream) {
+    AttnParams p;
+    p.q = a.q;
+    p.k_new = a.k_new;
+    p.v_new = a.v_new;
+    p.k_cache = a.k_cache;
+    p.v_cache = a.v_cache;
+    p.part_o = part_o;
+    p.part_ml = part_ml;
+    p.q_out = a.q_out;
+    p.k_out = a.k_out;
+    p.q_gamma = a.q_gamma;
+    p.k_gamma = a.k_gamma;
+    p.pos = a.pos;
+    p.n_heads = a.n_heads;
+    p.n_kv = a.n_kv_heads;
+    p.t0 = pl.t0;
+    p.t1 = pl.t1;
+    p.chunk = pl.chunk;
+    p.use_new = (a.write_kv && a.k_new && a.v_new) ? 1 : 0;
+    p.norm_qk = a.norm_qk;
+    p.has_rope = a.rope ? 1 : 0;
+    p.scale = a.scale;
+    p.eps = a.eps;
+    if (a.rope) p.rope = *a.rope;
+    else p.rope.half = 0;
+    const int G = a.n_heads / a.n_kv_heads;
+    const size_t lds = sizeof(float) * (static_cast<size_t>(kHeadBlock) * pl.chunk + kWaves * kHeadBlock * HD +
+                                        static_cast<size_t>(G) * HD + HD);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_chunk_kernel<HD>, dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), lds, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, stream, part_o, part_ml,
+                       pl.n_split, a.n_heads, HD, a.out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window) {
+    // upper bound over n_kv: the smallest chunk is 32 tokens
+    const int32_t n_split = (window + 31) / 32;
+    return sizeof(float) * static_cast<size_t>(n_split) * n_heads * (head_dim + 2) + 256;
+}
+
+hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (a.n_heads <= 0 || a.n_kv_heads <= 0 || a.pos < 0) return hipErrorInvalidValue;
+    if (a.n_heads % a.n_kv_heads != 0) return hipErrorInvalidValue;
+    if (a.rope && a.rope->half * 2 != a.head_dim) return hipErrorInvalidValue;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k_cache) |
+                         reinterpret_cast<uintptr_t>(a.v_cache) | reinterpret_cast<uintptr_t>(a.out);
+    if (al & 15u) return hipErrorInvalidValue;
+    const Plan pl = make_plan(a.pos, a.sliding_window, a.n_kv_heads);
+    const size_t need_o = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * a.head_dim;
+    const size_t need_ml = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * 2;
+    if (need_o + need_ml > workspace_bytes) return hipErrorInvalidValue;
+    float* part_o = static_cast<float*>(workspace);
+    float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + need_o);
+    switch (a.head_dim) {
+    case 64: return launch_hd<64>(a, pl, part_o, part_ml, stream);
+    case 128: return launch_hd<128>(a, pl, part_o, part_ml, stream);
+    case 256: return launch_hd<256>(a, pl, part_o, part_ml, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace gncx

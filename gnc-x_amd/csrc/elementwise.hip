@@ -1,0 +1,206 @@
+// elementwise.hip -- the small per-token kernels around the hot path, plus
+// the block dequantiser used to prove the decoders bit-exact.
+//   per-head RMSNorm      cpp:895-953    RMSNorm (fast path)  cpp:789-833
+//   NEOX RoPE             cpp:1797-1862  SwiGLU               cpp:2038-2052
+//   lm_head softcap       cpp:1726-1731  embedding row fetch  cpp:693-780
+//   block decoders        cpp:85-112, 707-714, 734-759 and the dots' implicit
+//                         Q4_0/Q4_K decoders (cpp:1023-1030, 1127-1178)
+#include <hip/hip_runtime.h>
+
+#include "gncx_device.h"
+#include "gncx_launch.h"
+
+namespace gncx {
+namespace {
+
+using namespace dev;
+
+// one wave per head; values stay in global memory (hd <= a few hundred)
+__global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict v, const float* __restrict g,
+                                                            int32_t n_heads, int32_t hd, float eps) {
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (h >= n_heads) return;
+    float* x = v + static_cast<size_t>(h) * hd;
+    const float inv = head_inv_rms(x, hd, eps, lane);
+    for (int i = lane; i < hd; i += 64) {
+        const float y = __fmul_rn(x[i], inv);
+        x[i] = g ? __fmul_rn(y, g[i]) : y;
+    }
+}
+
+// one work-group per row; fp32 per-thread partials, combined in double
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict x, const float* __restrict g,
+                                                      int32_t dim, float eps, float* __restrict out) {
+    __shared__ double part[4];
+    const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
+    float* yr = out + static_cast<size_t>(blockIdx.x) * dim;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < dim; i += 256) s = __fadd_rn(s, __fmul_rn(xr[i], xr[i]));
+    double d = static_cast<double>(s);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = d;
+    __syncthreads();
+    const double tot = part[0] + part[1] + part[2] + part[3];
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / dim), eps)));
+    for (int i = threadIdx.x; i < dim; i += 256) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), g[i]);
+}
+
+__global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable t, int32_t n_heads,
+                            int32_t n_kv, int32_t hd) {
+    const int half = hd / 2;
+    const int total = (n_heads + n_kv) * half;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int h = idx / half, i = idx % half;
+        float* v = h < n_heads ? (q ? q + static_cast<size_t>(h) * hd : nullptr)
+                               : (k ? k + static_cast<size_t>(h - n_heads) * hd : nullptr);
+        if (!v) continue;
+        const float x1 = v[i], x2 = v[i + half];
+        v[i] = __fsub_rn(__fmul_rn(x1, t.c[i]), __fmul_rn(x2, t.s[i]));
+        v[i + half] = __fadd_rn(__fmul_rn(x2, t.c[i]), __fmul_rn(x1, t.s[i]));
+    }
+}
+
+__global__ void swiglu_kernel(const float* __restrict g, const float* __restrict u, int32_t n,
+                              float* __restrict out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float x = g[i];
+        out[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), u[i]);
+    }
+}
+
+__global__ void softcap_kernel(float* __restrict y, int32_t n, float cap) {
+    const float inv = __fdiv_rn(1.0f, cap);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        y[i] = __fmul_rn(tanhf(__fmul_rn(y[i], inv)), cap);
+}
+
+// Decode element e of a row (all decoders are exact: every product below is
+// representable in fp32, except where the reference also rounds).
+__device__ __forceinline__ float decode_elem(int32_t type, const uint8_t* __restrict row, int32_t e, float scale) {
+    if (type == kQ4_0) {
+        const uint8_t* blk = row + static_cast<size_t>(e / 32) * 18;
+        const int j = e % 32;
+        const float d = half_bits_to_float(ld_u16(blk));
+        const int b = blk[2 + (j & 15)];
+        const int qv = (j < 16 ? (b & 15) : (b >> 4)) - 8;
+        return __fmul_rn(d, static_cast<float>(qv));
+    }
+    if (type == kQ8_0) {
+        const uint8_t* blk = row + static_cast<size_t>(e / 32) * 34;
+        const float d = __fmul_rn(half_bits_to_float(ld_u16(blk)), scale);
+        return __fmul_rn(static_cast<float>(static_cast<int8_t>(blk[2 + e % 32])), d);
+    }
+    if (type == kQ4_K) {
+        const uint8_t* blk = row + static_cast<size_t>(e / 256) * 144;
+        const int r = e % 256, c = r / 64, hi = (r % 64) / 32, l = r % 32;
+        const uint32_t s0 = blk[4] | (blk[5] << 8) | (blk[6] << 16) | (static_cast<uint32_t>(blk[7]) << 24);
+        const uint32_t s1 = blk[8] | (blk[9] << 8) | (blk[10] << 16) | (static_cast<uint32_t>(blk[11]) << 24);
+        const uint32_t s2 = blk[12] | (blk[13] << 8) | (blk[14] << 16) | (static_cast<uint32_t>(blk[15]) << 24);
+        int sc, mn;
+        k4_scale_min(2 * c + hi, s0, s1, s2, sc, mn);
+        const float d = half_bits_to_float(ld_u16(blk)), dmin = half_bits_to_float(ld_u16(blk + 2));
+        const int b = blk[16 + 32 * c + l];
+        const int qv = hi ? (b >> 4) : (b & 15);
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, static_cast<float>(sc)), static_cast<float>(qv)),
+                         __fmul_rn(dmin, static_cast<float>(mn)));
+    }
+    if (type == kQ6_K) {
+        const uint8_t* blk = row + static_cast<size_t>(e / 256) * 210;
+        const int r = e % 256, h = r / 128, rr = r % 128, grp = rr / 32, l = rr % 32;
+        const uint8_t* ql = blk + 64 * h;
+        const uint8_t* qh = blk + 128 + 32 * h;
+        const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * h);
+        const int lo4 = (grp & 1) ? ql[l + 32] : ql[l];
+        const int low = (grp >= 2) ? (lo4 >> 4) : (lo4 & 15);
+        const int qv = (low | (((qh[l] >> (2 * grp)) & 3) << 4)) - 32;
+        const float d = __fmul_rn(half_bits_to_float(ld_u16(blk + 208)), scale);
+        return __fmul_rn(__fmul_rn(d, static_cast<float>(sc[l / 16 + 2 * grp])), static_cast<float>(qv));
+    }
+    // BF16
+    return __fmul_rn(__uint_as_float(ld_u16(row + static_cast<size_t>(e) * 2) << 16), scale);
+}
+
+__global__ void dequant_kernel(int32_t type, const uint8_t* __restrict w, size_t rb, int32_t k, int32_t n,
+                               float* __restrict out) {
+    const size_t total = static_cast<size_t>(k) * n;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int32_t r = static_cast<int32_t>(i / k), e = static_cast<int32_t>(i % k);
+        out[i] = decode_elem(type, w + static_cast<size_t>(r) * rb, e, 1.0f);
+    }
+}
+
+__global__ void fetch_embedding_kernel(int32_t type, const uint8_t* __restrict row, int32_t dim, float scale,
+                                       float* __restrict out) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < dim; e += gridDim.x * blockDim.x)
+        out[e] = decode_elem(type, row, e, scale);
+}
+
+int grid_for(size_t n, int threads) {
+    size_t g = (n + threads - 1) / threads;
+    if (g > 4096) g = 4096;
+    return g < 1 ? 1 : static_cast<int>(g);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_heads(float* v, const float* gamma, int32_t n_heads, int32_t head_dim, float eps,
+                                hipStream_t stream) {
+    if (n_heads <= 0 || head_dim <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_heads_kernel, dim3((n_heads + 3) / 4), dim3(256), 0, stream, v, gamma, n_heads,
+                       head_dim, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int32_t dim, float eps, float* out,
+                          hipStream_t stream) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, gamma, dim, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, hipStream_t stream) {
+    if (head_dim / 2 > kMaxRopeHalf || table.half * 2 != head_dim) return hipErrorInvalidValue;
+    const size_t work = static_cast<size_t>(n_heads + n_kv_heads) * (head_dim / 2);
+    if (work == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(work, 256)), dim3(256), 0, stream, q, k, table, n_heads,
+                       n_kv_heads, head_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, gate, up, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_softcap(float* y, int32_t n, float softcap, hipStream_t stream) {
+    if (n <= 0 || !(softcap > 0.0f)) return hipSuccess;
+    hipLaunchKernelGGL(softcap_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, y, n, softcap);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant(int32_t type, const uint8_t* w, int32_t k, int32_t n, float* out, hipStream_t stream) {
+    if (!type_supported(type)) return hipErrorInvalidValue;
+    if (k <= 0 || n <= 0) return hipSuccess;
+    if (k % block_elems(type) != 0 || (reinterpret_cast<uintptr_t>(w) & 1u)) return hipErrorInvalidValue;
+    const size_t total = static_cast<size_t>(k) * n;
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid_for(total, 256)), dim3(256), 0, stream, type, w,
+                       row_bytes(type, k), k, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim, float scale,
+                                  float* out, hipStream_t stream) {
+    if (type != kQ8_0 && type != kQ6_K && type != kBF16) return hipErrorInvalidValue;
+    if (dim <= 0) return hipSuccess;
+    const uint8_t* row = table + static_cast<size_t>(token) * row_bytes(type, dim);
+    hipLaunchKernelGGL(fetch_embedding_kernel, dim3(grid_for(dim, 256)), dim3(256), 0, stream, type, row, dim,
+                       scale, out);
+    return hipGetLastError();
+}
+
+}  // namespace gncx

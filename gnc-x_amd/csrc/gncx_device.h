@@ -1,0 +1,141 @@
+// gncx_device.h -- device helpers shared by the HIP kernels (gfx950).
+//
+// Loads: GGUF blocks other than Q4_K are only 2-byte aligned (18, 34 and 210
+// byte blocks).  A 16-byte field at a 2-aligned address is read as one
+// dword-aligned dwordx4 plus one extra 16-bit load, and realigned with
+// v_alignbyte_b32; no load ever reaches outside the block it belongs to.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gncx_formats.h"
+
+namespace gncx {
+namespace dev {
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+__device__ __forceinline__ uint4 ld16_aligned(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+// 16 bytes at a 2-aligned address p.  Reads [p - sh, p - sh + 16) and
+// [p + 14, p + 16) with sh = p mod 4 in {0, 2}: nothing past the field, and
+// the 2 bytes before p only when p is not 4-aligned (then p - 2 is still
+// inside a tensor whose base is 4-aligned).
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t* p) {
+    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint8_t* a = p - sh;
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(a);
+    const uint32_t tail = ld_u16(p + 14);  // == a[16], a[17] when sh == 2
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(tail, v.w, sh);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    // v_cvt_f32_f16: exact IEEE conversion (subnormal halves are normal floats)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Q4_K 6-bit (scale, min) of sub-block j (reference cpp:1112-1120) from the
+// three little-endian dwords of the 12 scale bytes.
+__device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             int& sc, int& mn) {
+    const int jj = j & 3;
+    const uint32_t a = byte_of(s0, jj), b = byte_of(s1, jj), c = byte_of(s2, jj);
+    if (j < 4) {
+        sc = static_cast<int>(a & 63u);
+        mn = static_cast<int>(b & 63u);
+    } else {
+        sc = static_cast<int>((c & 15u) | ((a >> 6) << 4));
+        mn = static_cast<int>((c >> 4) | ((b >> 6) << 4));
+    }
+}
+
+// 1/rms of one head of hd values, formed as the reference does
+// (cpp:905-926): four fp32 lane sums over i mod 4 for the multiple-of-4
+// prefix, the lanes added in double, a double tail, then
+// 1 / sqrtf((float)(sum/hd) + eps).  No contraction, IEEE div/sqrt.
+// Called by a whole wave; every lane returns the same value.
+__device__ __forceinline__ float head_inv_rms(const float* v, int hd, float eps, int lane) {
+    const int full = hd & ~3;
+    float part = 0.0f;
+    if (lane < 4)
+        for (int i = lane; i < full; i += 4) part = __fadd_rn(part, __fmul_rn(v[i], v[i]));
+    const float p0 = __shfl(part, 0, 64), p1 = __shfl(part, 1, 64);
+    const float p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
+    double s = static_cast<double>(p0) + static_cast<double>(p1) + static_cast<double>(p2) + static_cast<double>(p3);
+    for (int i = full; i < hd; ++i) s += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+    const float mean = static_cast<float>(s / static_cast<double>(hd));
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+}
+
+// Per-32 Q8 quantisation of x[k] (reference cpp:955-995), done by the whole
+// work-group: 8 lanes per 32-block, 4 values per lane.  Writes int8 values
+// to q[k] and one ActMeta per block.  blockDim.x must be a multiple of 64.
+// Bit-exact with the reference: IEEE 127/amax and amax/127, one rounding for
+// x*inv, round-half-even.
+__device__ __forceinline__ void quantize_block8(const float* __restrict x, int32_t nb, int tid,
+                                                int nthr, int8_t* __restrict q,
+                                                ActMeta* __restrict meta) {
+    const int32_t ntask = nb * 8;
+    for (int32_t task = tid; task < ntask; task += nthr) {
+        const int32_t b = task >> 3;
+        const int j = task & 7;
+        const float4 v = *reinterpret_cast<const float4*>(x + static_cast<size_t>(b) * 32 + j * 4);
+        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        a = fmaxf(a, __shfl_xor(a, 1, 8));
+        a = fmaxf(a, __shfl_xor(a, 2, 8));
+        a = fmaxf(a, __shfl_xor(a, 4, 8));
+        int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+        float d = 0.0f;
+        if (a != 0.0f) {
+            const float inv = __fdiv_rn(127.0f, a);
+            d = __fdiv_rn(a, 127.0f);
+            q0 = static_cast<int>(rintf(v.x * inv));
+            q1 = static_cast<int>(rintf(v.y * inv));
+            q2 = static_cast<int>(rintf(v.z * inv));
+            q3 = static_cast<int>(rintf(v.w * inv));
+        }
+        const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
+                                ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
+        *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * 32 + j * 4) = packed;
+        int s = q0 + q1 + q2 + q3;
+        s += __shfl_xor(s, 1, 8);
+        s += __shfl_xor(s, 2, 8);  // lanes 0-3: sum of q[0:16]; lanes 4-7: q[16:32]
+        const int other = __shfl_xor(s, 4, 8);
+        if (j == 0) {
+            ActMeta m;
+            m.d = d;
+            m.sum_lo16 = s;
+            m.sum_hi16 = other;
+            m.sum = s + other;
+            meta[b] = m;
+        }
+    }
+}
+
+}  // namespace dev
+}  // namespace gncx

@@ -1,0 +1,92 @@
+// gncx_launch.h -- host-callable launchers for the HIP kernels.
+//
+// Every launcher takes device pointers only, enqueues on `stream` and returns
+// hipSuccess or the error of the failed check/launch; none synchronises.  The
+// host shim (gncx_shim.cpp) owns pointer classification, staging and the
+// reference-compatible C-ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "gncx_formats.h"
+
+namespace gncx {
+
+// Largest in_dim the fused GEMV accepts (its quantised activations live in LDS).
+constexpr int32_t kMaxGemvK = 40960;
+
+// y[n] = W[n x k] . Q8(x[k])   (BF16: fp32 x)  -- quantises x inside the kernel.
+hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n,
+                       float* y, hipStream_t stream);
+
+// Per-32 Q8 quantisation of `rows` rows of k floats into q[rows*k] and
+// meta[rows*k/32] (used by matbatch and the dequant tests).
+hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, ActMeta* meta,
+                            hipStream_t stream);
+
+// Dequantise n rows of k weights to fp32 (bit-exact block decoders).
+hipError_t launch_dequant(int32_t type, const uint8_t* w, int32_t k, int32_t n, float* out,
+                          hipStream_t stream);
+
+// Y[b x n] = Q8(X[b x k]) . W^T  (per-row activation quantisation).
+size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k);
+hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k,
+                           int32_t n, float* y, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+// cos/sin of one RoPE position, computed on the host with the C library's
+// powf/cosf/sinf exactly as the reference does (cpp:1779-1796), passed to
+// the kernels by value.
+constexpr int32_t kMaxRopeHalf = 256;
+struct RopeTable {
+    int32_t half;  // head_dim / 2
+    float c[kMaxRopeHalf];
+    float s[kMaxRopeHalf];
+};
+
+// Decode attention step (reference cpp:1887-1994) with split-K softmax.
+struct AttnArgs {
+    const float* q;        // [n_heads*hd]
+    const float* k_new;    // [n_kv*hd] or null
+    const float* v_new;    // [n_kv*hd] or null
+    float* k_cache;        // [rows*n_kv*hd]
+    float* v_cache;
+    float* out;            // [n_heads*hd]
+    int32_t pos, n_heads, n_kv_heads, head_dim;
+    float scale;
+    int32_t sliding_window, write_kv;
+    // optional fused prologue applied to q and k_new before the scan:
+    // per-head RMSNorm (cpp:895-953) then NEOX RoPE (cpp:1797-1862)
+    int32_t norm_qk;          // 1 = RMSNorm q and k_new per head
+    const float* q_gamma;     // may be null (no weight)
+    const float* k_gamma;
+    float eps;
+    const RopeTable* rope;    // host table, null = no rotation
+    float* q_out;             // prologue result for q written back (optional)
+    float* k_out;             // prologue result for k_new written back (optional)
+};
+size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window);
+hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+// Per-head RMSNorm in place (reference cpp:895-953); gamma may be null.
+hipError_t launch_rmsnorm_heads(float* v, const float* gamma, int32_t n_heads, int32_t head_dim,
+                                float eps, hipStream_t stream);
+// RMSNorm of `rows` vectors of dim (reference cpp:789-833).
+hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int32_t dim, float eps,
+                          float* out, hipStream_t stream);
+// NEOX RoPE with a host-computed cos/sin table (reference cpp:1797-1862).
+hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_heads,
+                       int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
+// SiLU(gate)*up (reference cpp:2038-2052).
+hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* out,
+                         hipStream_t stream);
+// tanh softcap in place (reference cpp:1726-1731).
+hipError_t launch_softcap(float* y, int32_t n, float softcap, hipStream_t stream);
+// One embedding row (reference cpp:693-780), scale folded like the reference.
+hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim,
+                                  float scale, float* out, hipStream_t stream);
+
+}  // namespace gncx

@@ -1,0 +1,996 @@
+// gncx_shim.cpp -- C++20 host shim: the reference's C-ABI on top of HIP.
+//
+// Every exported name and signature is the one csrc/gncx_llm_kernels.cpp of
+// the reference exports (cited per function), so this library drops in for
+// bin/gncx_llm_core.so under the LuaJIT FFI (lua/gncx_streamer.lua:16-252).
+//
+// Pointers crossing the ABI may be host memory (the reference contract: the
+// LuaJIT caller passes mmap'ed / RAM-pinned weights and host scratch) or HIP
+// device memory (callers that keep activations in HBM).  The shim classifies
+// each pointer with hipPointerGetAttributes:
+//   * weights (base + offset) living on the host are uploaded once, in their
+//     native GGUF block layout, into a registry keyed by host address and
+//     reused for the life of the process (weights are immutable, the
+//     reference's own convention); a cheap content signature guards against a
+//     freed-and-reused host address;
+//   * host activations are staged through device scratch and host outputs are
+//     copied back before the call returns (the reference is synchronous);
+//     device activations/outputs are used in place and the call is only
+//     stream-ordered (no host synchronisation);
+//   * a host KV cache gets a device twin that is kept coherent: rows the
+//     library writes go to both copies, rows it has not seen are uploaded on
+//     first use.
+// Calls are serialised with one mutex (the reference is not re-entrant
+// either).  On any failure the call prints one line to stderr, records the
+// error for gncx_hip_last_error(), and leaves its outputs untouched; there
+// is no CPU fallback.  GNCX_ABORT_ON_ERROR=1 turns failures into abort().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "gncx_formats.h"
+#include "gncx_launch.h"
+
+#define GNCX_API extern "C" __attribute__((visibility("default")))
+
+#pragma pack(push, 1)
+// cpp:267-271
+struct GNCXCompactToken {
+    uint8_t phase_2bit;
+    uint8_t diag_d;
+    uint16_t abs_delta;
+};
+// cpp:308-313
+struct GNCXTelemetryStats {
+    uint64_t total_macs_equivalent;
+    uint64_t zero_origin_cancellations;
+    uint64_t zero_weight_skips;
+    uint64_t xfold_bucket_merges;
+};
+#pragma pack(pop)
+
+namespace {
+
+using namespace gncx;
+
+std::mutex g_mu;
+std::string g_last_error;
+int g_last_code = 0;
+
+void set_error(const char* where, const char* what, int code) {
+    g_last_error = std::string(where) + ": " + what;
+    g_last_code = code ? code : -1;
+    std::fprintf(stderr, "gncx_llm_core: %s\n", g_last_error.c_str());
+    const char* ab = std::getenv("GNCX_ABORT_ON_ERROR");
+    if (ab && ab[0] == '1') std::abort();
+}
+
+bool check(hipError_t e, const char* where) {
+    if (e == hipSuccess) return true;
+    set_error(where, hipGetErrorString(e), static_cast<int>(e));
+    return false;
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---- runtime state ----------------------------------------------------
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    bool ensure(size_t bytes, const char* where) {
+        if (bytes <= cap && p) return true;
+        if (p) {
+            (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+        }
+        const size_t c = round_up(std::max<size_t>(bytes, 4096), 1 << 16);
+        if (!check(hipMalloc(&p, c), where)) return false;
+        cap = c;
+        return true;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+struct DevWeight {
+    uint8_t* d = nullptr;
+    size_t bytes = 0;
+    uint64_t sig = 0;
+};
+
+struct KVTwin {
+    float* d = nullptr;
+    int32_t cap_rows = 0;
+    int32_t kv_dim = 0;
+    int32_t valid_rows = 0;
+    std::array<float, 8> row0{};  // first values of host row 0 when last synced
+};
+
+struct Runtime {
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;  // null stream unless the caller sets one
+    DevBuf x, y, q, k, v, o, ws, aux;
+    std::unordered_map<uintptr_t, DevWeight> weights;
+    std::unordered_map<uintptr_t, KVTwin> kv;
+};
+
+Runtime g_rt;
+
+bool ensure_runtime(const char* where) {
+    if (g_rt.ready) return true;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        set_error(where, "no HIP device is visible (this library has no CPU path)", e ? static_cast<int>(e) : -1);
+        return false;
+    }
+    const char* dv = std::getenv("GNCX_DEVICE");
+    g_rt.device = dv ? std::atoi(dv) : 0;
+    if (!check(hipSetDevice(g_rt.device), where)) return false;
+    g_rt.ready = true;
+    return true;
+}
+
+bool is_device_ptr(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+uint64_t host_signature(const uint8_t* p, size_t bytes) {
+    uint64_t h = 1469598103934665603ull ^ bytes;
+    const size_t probes = 16;
+    for (size_t i = 0; i < probes; ++i) {
+        size_t off = (bytes > 8) ? (bytes - 8) * i / (probes - 1) : 0;
+        uint64_t v = 0;
+        std::memcpy(&v, p + off, std::min<size_t>(8, bytes));
+        h = (h ^ v) * 1099511628211ull;
+    }
+    return h;
+}
+
+void forget_weight(uintptr_t key) {
+    auto it = g_rt.weights.find(key);
+    if (it == g_rt.weights.end()) return;
+    (void)hipFree(it->second.d);
+    g_rt.weights.erase(it);
+}
+
+// Device view of `bytes` weight bytes at p (host: uploaded once, cached).
+const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where) {
+    if (is_device_ptr(p)) return p;
+    const uintptr_t key = reinterpret_cast<uintptr_t>(p);
+    const uint64_t sig = host_signature(p, bytes);
+    auto it = g_rt.weights.find(key);
+    if (it != g_rt.weights.end()) {
+        if (it->second.bytes >= bytes && it->second.sig == host_signature(p, it->second.bytes))
+            return it->second.d;
+        forget_weight(key);
+    }
+    DevWeight w;
+    w.bytes = bytes;
+    w.sig = sig;
+    void* d = nullptr;
+    // 256 B aligned, plus slack so no vector load near the end leaves the allocation
+    if (!check(hipMalloc(&d, round_up(bytes, 256) + 256), where)) return nullptr;
+    if (!check(hipMemcpy(d, p, bytes, hipMemcpyHostToDevice), where)) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    w.d = static_cast<uint8_t*>(d);
+    g_rt.weights.emplace(key, w);
+    return w.d;
+}
+
+// Input vector: device pointers pass through, host data is staged into buf.
+const float* stage_in(const float* p, size_t count, DevBuf& buf, const char* where) {
+    if (!p) return nullptr;
+    if (is_device_ptr(p)) return p;
+    if (!buf.ensure(count * sizeof(float), where)) return nullptr;
+    if (!check(hipMemcpyAsync(buf.p, p, count * sizeof(float), hipMemcpyHostToDevice, g_rt.stream), where))
+        return nullptr;
+    return buf.as<float>();
+}
+
+// Output vector: device pointers pass through, host outputs get scratch.
+float* out_target(float* p, size_t count, DevBuf& buf, bool& host, const char* where) {
+    host = !is_device_ptr(p);
+    if (!host) return p;
+    if (!buf.ensure(count * sizeof(float), where)) return nullptr;
+    return buf.as<float>();
+}
+
+bool finish_out(float* host_dst, const float* dev_src, size_t count, bool host, const char* where) {
+    if (!host) return true;
+    if (!check(hipMemcpyAsync(host_dst, dev_src, count * sizeof(float), hipMemcpyDeviceToHost, g_rt.stream), where))
+        return false;
+    return check(hipStreamSynchronize(g_rt.stream), where);
+}
+
+// ---- 4-phase encode bookkeeping (cpp:782-784, 997-1015) ----------------
+
+uint64_t g_norm_epoch = 0;
+uint64_t g_norm_epoch_cancellations = 0;
+const GNCXCompactToken* g_norm_epoch_tokens_ptr = nullptr;
+
+uint64_t count_cancellations(const GNCXCompactToken* t, int32_t n) {
+    if (!t) return 0;
+    if (t == g_norm_epoch_tokens_ptr) return g_norm_epoch_cancellations;
+    std::array<uint32_t, 10> pos{}, neg{};
+    for (int32_t i = 0; i < n; ++i) {
+        const uint8_t d = t[i].diag_d;
+        const uint8_t b1 = (t[i].phase_2bit >> 1) & 1u;
+        if (d < 10) {
+            pos[d] += b1;
+            neg[d] += b1 ^ 1u;
+        }
+    }
+    uint64_t c = 0;
+    for (int d = 0; d < 10; ++d) c += std::min(pos[d], neg[d]);
+    return c;
+}
+
+// matvec activation cache key (cpp:1338-1358)
+struct ActCache {
+    const float* last_in = nullptr;
+    int32_t last_dim = 0;
+    uint64_t last_epoch = 0;
+    uint64_t cached_canceled = 0;
+    bool staged_on_device = false;  // scratch x holds that vector
+} g_act;
+
+void add_telemetry(GNCXTelemetryStats* t, uint64_t macs, uint64_t canceled, uint64_t merges) {
+    if (!t) return;
+    t->total_macs_equivalent += macs;
+    t->zero_origin_cancellations += canceled;
+    t->zero_weight_skips += macs / 15;
+    t->xfold_bucket_merges += merges;
+}
+
+bool matvec_impl(const uint8_t* base, size_t off, int32_t type, const float* in_vec, int32_t in_dim, int32_t out_dim, float* out_vec, bool reuse_x,
+                 float softcap, const char* where) {
+    if (!ensure_runtime(where)) return false;
+    const size_t wbytes = row_bytes(type, in_dim) * static_cast<size_t>(out_dim);
+    const uint8_t* w = device_weights(base + off, wbytes, where);
+    if (!w) return false;
+    const float* x;
+    if (is_device_ptr(in_vec)) {
+        x = in_vec;
+        g_act.staged_on_device = false;
+    } else if (reuse_x && g_act.staged_on_device) {
+        x = g_rt.x.as<float>();
+    } else {
+        x = stage_in(in_vec, static_cast<size_t>(in_dim), g_rt.x, where);
+        if (!x) return false;
+        g_act.staged_on_device = true;
+    }
+    bool host_out = false;
+    float* y = out_target(out_vec, static_cast<size_t>(out_dim), g_rt.y, host_out, where);
+    if (!y) return false;
+    if (!check(launch_gemv(type, w, x, in_dim, out_dim, y, g_rt.stream), where)) return false;
+    if (softcap > 0.0f && !check(launch_softcap(y, out_dim, softcap, g_rt.stream), where)) return false;
+    return finish_out(out_vec, y, static_cast<size_t>(out_dim), host_out, where);
+}
+
+// ---- RoPE table (cpp:1779-1796, host libm like the reference) ---------
+
+bool rope_table(int32_t pos, int32_t head_dim, float base, const float* factors, RopeTable& t) {
+    if (head_dim <= 0 || head_dim % 2 || head_dim / 2 > kMaxRopeHalf) return false;
+    t.half = head_dim / 2;
+    for (int32_t i = 0; i < t.half; ++i) {
+        float freq = 1.0f / std::pow(base, static_cast<float>(2 * i) / static_cast<float>(head_dim));
+        if (factors != nullptr && factors[i] != 0.0f) freq /= factors[i];
+        const float angle = static_cast<float>(pos) * freq;
+        t.c[i] = std::cos(angle);
+        t.s[i] = std::sin(angle);
+    }
+    return true;
+}
+
+// freq factors may sit in host or device memory; the table is built on host
+bool read_factors(const uint8_t* base, size_t off, int32_t half, std::array<float, kMaxRopeHalf>& f,
+                  const char* where) {
+    const float* src = reinterpret_cast<const float*>(base + off);
+    if (is_device_ptr(src))
+        return check(hipMemcpy(f.data(), src, sizeof(float) * half, hipMemcpyDeviceToHost), where);
+    std::memcpy(f.data(), src, sizeof(float) * half);
+    return true;
+}
+
+// ---- KV twins ----------------------------------------------------------
+
+void forget_kv(uintptr_t key) {
+    auto it = g_rt.kv.find(key);
+    if (it == g_rt.kv.end()) return;
+    (void)hipFree(it->second.d);
+    g_rt.kv.erase(it);
+}
+
+// Device twin of a host cache with room for cap_rows rows, valid for rows
+// [0, need_rows).
+float* kv_twin(float* host, int32_t kv_dim, int32_t need_rows, int32_t cap_rows, const char* where) {
+    const uintptr_t key = reinterpret_cast<uintptr_t>(host);
+    auto it = g_rt.kv.find(key);
+    if (it != g_rt.kv.end()) {
+        KVTwin& t = it->second;
+        bool stale = t.kv_dim != kv_dim;
+        if (!stale && t.valid_rows > 0)
+            stale = std::memcmp(t.row0.data(), host, sizeof(float) * std::min<int32_t>(8, kv_dim)) != 0;
+        if (stale) {
+            forget_kv(key);
+            it = g_rt.kv.end();
+        }
+    }
+    if (it == g_rt.kv.end()) {
+        KVTwin t;
+        t.kv_dim = kv_dim;
+        t.cap_rows = std::max<int32_t>(cap_rows, 256);
+        void* d = nullptr;
+        if (!check(hipMalloc(&d, sizeof(float) * static_cast<size_t>(t.cap_rows) * kv_dim), where)) return nullptr;
+        t.d = static_cast<float*>(d);
+        it = g_rt.kv.emplace(key, t).first;
+    }
+    KVTwin& t = it->second;
+    if (cap_rows > t.cap_rows) {
+        const int32_t cap = std::max<int32_t>(cap_rows, t.cap_rows * 2);
+        void* d = nullptr;
+        if (!check(hipMalloc(&d, sizeof(float) * static_cast<size_t>(cap) * kv_dim), where)) return nullptr;
+        if (t.valid_rows > 0 &&
+            !check(hipMemcpyAsync(d, t.d, sizeof(float) * static_cast<size_t>(t.valid_rows) * kv_dim,
+                                  hipMemcpyDeviceToDevice, g_rt.stream),
+                   where))
+            return nullptr;
+        (void)hipStreamSynchronize(g_rt.stream);
+        (void)hipFree(t.d);
+        t.d = static_cast<float*>(d);
+        t.cap_rows = cap;
+    }
+    if (t.valid_rows < need_rows) {
+        const size_t r0 = static_cast<size_t>(t.valid_rows);
+        const size_t nr = static_cast<size_t>(need_rows) - r0;
+        if (!check(hipMemcpy(t.d + r0 * kv_dim, host + r0 * kv_dim, sizeof(float) * nr * kv_dim,
+                             hipMemcpyHostToDevice),
+                   where))
+            return nullptr;
+        t.valid_rows = need_rows;
+    }
+    std::memcpy(t.row0.data(), host, sizeof(float) * std::min<int32_t>(8, kv_dim));
+    return t.d;
+}
+
+void kv_mark_written(float* host, int32_t row) {
+    auto it = g_rt.kv.find(reinterpret_cast<uintptr_t>(host));
+    if (it == g_rt.kv.end()) return;
+    if (row + 1 > it->second.valid_rows) it->second.valid_rows = row + 1;
+    std::memcpy(it->second.row0.data(), host, sizeof(float) * std::min<int32_t>(8, it->second.kv_dim));
+}
+
+struct AttnCall {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* kc;
+    float* vc;
+    int32_t pos, n_heads, n_kv, hd;
+    float scale;
+    int32_t sw, write_kv;
+    float* out;
+    // fused prologue
+    int32_t norm_qk = 0;
+    const float* q_gamma = nullptr;
+    const float* k_gamma = nullptr;
+    float eps = 0.0f;
+    const RopeTable* rope = nullptr;
+    float* q_back = nullptr;  // host/device q to receive the prologue result
+    float* k_back = nullptr;
+};
+
+bool attention_impl(const AttnCall& c, const char* where) {
+    if (!ensure_runtime(where)) return false;
+    if (c.n_heads <= 0 || c.n_kv <= 0 || c.hd <= 0 || c.pos < 0 || c.n_heads % c.n_kv != 0) {
+        set_error(where, "invalid head geometry or position", -1);
+        return false;
+    }
+    const int32_t kv_dim = c.n_kv * c.hd;
+    const bool use_new = c.write_kv && c.k && c.v;
+    const size_t qn = static_cast<size_t>(c.n_heads) * c.hd;
+    const float* q = stage_in(c.q, qn, g_rt.q, where);
+    if (!q) return false;
+    const float* kn = use_new ? stage_in(c.k, kv_dim, g_rt.k, where) : nullptr;
+    const float* vn = use_new ? stage_in(c.v, kv_dim, g_rt.v, where) : nullptr;
+    if (use_new && (!kn || !vn)) return false;
+
+    const bool host_k = !is_device_ptr(c.kc), host_v = !is_device_ptr(c.vc);
+    // rows needed on device: [0, pos) always, row pos too when it is not written here
+    const int32_t need = use_new ? c.pos : c.pos + 1;
+    float* kc = host_k ? kv_twin(c.kc, kv_dim, need, c.pos + 1, where) : c.kc;
+    if (!kc) return false;
+    float* vc = host_v ? kv_twin(c.vc, kv_dim, need, c.pos + 1, where) : c.vc;
+    if (!vc) return false;
+
+    bool host_out = false;
+    float* out = out_target(c.out, qn, g_rt.o, host_out, where);
+    if (!out) return false;
+    const int32_t t0 = c.sw > 0 ? std::max(0, c.pos - c.sw + 1) : 0;
+    const size_t wsb = attention_workspace_bytes(c.n_heads, c.hd, c.pos + 1 - t0);
+    if (!g_rt.ws.ensure(wsb, where)) return false;
+
+    AttnArgs a{};
+    a.q = q;
+    a.k_new = kn;
+    a.v_new = vn;
+    a.k_cache = kc;
+    a.v_cache = vc;
+    a.out = out;
+    a.pos = c.pos;
+    a.n_heads = c.n_heads;
+    a.n_kv_heads = c.n_kv;
+    a.head_dim = c.hd;
+    a.scale = c.scale;
+    a.sliding_window = c.sw;
+    a.write_kv = c.write_kv;
+    a.norm_qk = c.norm_qk;
+    a.q_gamma = c.q_gamma;
+    a.k_gamma = c.k_gamma;
+    a.eps = c.eps;
+    a.rope = c.rope;
+    // prologue results: device targets (host ones are copied back below)
+    float* qb = nullptr;
+    float* kb = nullptr;
+    if (c.q_back) qb = is_device_ptr(c.q_back) ? c.q_back : g_rt.aux.ensure(sizeof(float) * (qn + kv_dim), where) ? g_rt.aux.as<float>() : nullptr;
+    if (c.k_back && use_new) kb = is_device_ptr(c.k_back) ? c.k_back : g_rt.aux.ensure(sizeof(float) * (qn + kv_dim), where) ? g_rt.aux.as<float>() + qn : nullptr;
+    a.q_out = qb;
+    a.k_out = kb;
+    if (!check(launch_attention(a, g_rt.ws.p, g_rt.ws.cap, g_rt.stream), where)) return false;
+
+    if (use_new) {
+        // the reference writes the host cache row inside the call (cpp:1903-1906)
+        if (host_k) {
+            if (c.norm_qk || c.rope) {
+                // the stored row is the prologue result: take it from the twin
+                if (!check(hipMemcpyAsync(c.kc + static_cast<size_t>(c.pos) * kv_dim,
+                                          kc + static_cast<size_t>(c.pos) * kv_dim, sizeof(float) * kv_dim,
+                                          hipMemcpyDeviceToHost, g_rt.stream),
+                           where))
+                    return false;
+            } else if (!is_device_ptr(c.k)) {
+                std::memcpy(c.kc + static_cast<size_t>(c.pos) * kv_dim, c.k, sizeof(float) * kv_dim);
+            } else if (!check(hipMemcpyAsync(c.kc + static_cast<size_t>(c.pos) * kv_dim, c.k,
+                                             sizeof(float) * kv_dim, hipMemcpyDeviceToHost, g_rt.stream),
+                              where)) {
+                return false;
+            }
+        }
+        if (host_v) {
+            if (!is_device_ptr(c.v))
+                std::memcpy(c.vc + static_cast<size_t>(c.pos) * kv_dim, c.v, sizeof(float) * kv_dim);
+            else if (!check(hipMemcpyAsync(c.vc + static_cast<size_t>(c.pos) * kv_dim, c.v, sizeof(float) * kv_dim,
+                                           hipMemcpyDeviceToHost, g_rt.stream),
+                            where))
+                return false;
+        }
+    }
+    if (c.q_back && qb && !is_device_ptr(c.q_back))
+        if (!check(hipMemcpyAsync(c.q_back, qb, sizeof(float) * qn, hipMemcpyDeviceToHost, g_rt.stream), where))
+            return false;
+    if (c.k_back && kb && !is_device_ptr(c.k_back))
+        if (!check(hipMemcpyAsync(c.k_back, kb, sizeof(float) * kv_dim, hipMemcpyDeviceToHost, g_rt.stream), where))
+            return false;
+    const bool any_host = host_out || host_k || host_v || (c.q_back && !is_device_ptr(c.q_back)) ||
+                          (c.k_back && !is_device_ptr(c.k_back));
+    if (host_out && !check(hipMemcpyAsync(c.out, out, sizeof(float) * qn, hipMemcpyDeviceToHost, g_rt.stream), where))
+        return false;
+    if (any_host && !check(hipStreamSynchronize(g_rt.stream), where)) return false;
+    if (use_new) {
+        if (host_k) kv_mark_written(c.kc, c.pos);
+        if (host_v) kv_mark_written(c.vc, c.pos);
+    }
+    return true;
+}
+
+}  // namespace
+
+// =======================================================================
+// Reference C-ABI (names and signatures of csrc/gncx_llm_kernels.cpp)
+// =======================================================================
+
+// cpp:1327-1471
+GNCX_API void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                          const float* in_vec, const GNCXCompactToken* in_tokens, int32_t in_dim,
+                                          int32_t out_dim, float* out_vec, GNCXTelemetryStats* telemetry) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    uint64_t canceled = 0;
+    bool reuse = false;
+    if (in_tokens != nullptr && in_vec == g_act.last_in && in_dim == g_act.last_dim &&
+        g_norm_epoch == g_act.last_epoch) {
+        canceled = g_act.cached_canceled;
+        reuse = true;
+    } else {
+        canceled = count_cancellations(in_tokens, in_dim);
+        if (in_tokens != nullptr) {
+            g_act.last_in = in_vec;
+            g_act.last_dim = in_dim;
+            g_act.last_epoch = g_norm_epoch;
+            g_act.cached_canceled = canceled;
+        } else {
+            g_act.last_in = nullptr;
+        }
+    }
+    if (type_supported(ggml_type) && out_dim > 0 && in_dim > 0)
+        matvec_impl(mmap_base, weight_abs_offset, ggml_type, in_vec, in_dim, out_dim, out_vec, reuse,
+                    0.0f, "gncx_xfold_universal_matvec");
+    const uint64_t macs = static_cast<uint64_t>(in_dim) * static_cast<uint64_t>(out_dim);
+    add_telemetry(telemetry, macs, canceled, static_cast<uint64_t>(in_dim / 32) * static_cast<uint64_t>(out_dim));
+}
+
+// cpp:1476-1489
+GNCX_API void gncx_xfold_q4_0_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, const float* in_vec,
+                                     const GNCXCompactToken* in_tokens, int32_t in_dim, int32_t out_dim,
+                                     float* out_vec, GNCXTelemetryStats* telemetry) {
+    gncx_xfold_universal_matvec(mmap_base, weight_abs_offset, kQ4_0, in_vec, in_tokens, in_dim, out_dim, out_vec,
+                                telemetry);
+}
+
+// cpp:1495-1692
+GNCX_API void gncx_xfold_universal_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                            const float* in_batch, int32_t batch_size, int32_t in_dim,
+                                            int32_t out_dim, float* out_batch, GNCXTelemetryStats* telemetry) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_xfold_universal_matbatch";
+    if (type_supported(ggml_type) && batch_size > 0 && out_dim > 0 && in_dim > 0 && ensure_runtime(where)) {
+        do {
+            const size_t wbytes = row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dim);
+            const uint8_t* w = device_weights(mmap_base + weight_abs_offset, wbytes, where);
+            if (!w) break;
+            const size_t xn = static_cast<size_t>(batch_size) * in_dim;
+            const size_t yn = static_cast<size_t>(batch_size) * out_dim;
+            const float* x = stage_in(in_batch, xn, g_rt.aux, where);
+            if (!x) break;
+            bool host_out = false;
+            float* y = out_target(out_batch, yn, g_rt.y, host_out, where);
+            if (!y) break;
+            const size_t wsb = matbatch_workspace_bytes(ggml_type, batch_size, in_dim);
+            if (!g_rt.ws.ensure(wsb, where)) break;
+            if (!check(launch_matbatch(ggml_type, w, x, batch_size, in_dim, out_dim, y, g_rt.ws.p, g_rt.ws.cap,
+                                       g_rt.stream),
+                       where))
+                break;
+            finish_out(out_batch, y, yn, host_out, where);
+        } while (false);
+    }
+    const uint64_t macs = static_cast<uint64_t>(batch_size) * static_cast<uint64_t>(in_dim) *
+                          static_cast<uint64_t>(out_dim);
+    if (telemetry) {
+        telemetry->total_macs_equivalent += macs;
+        telemetry->zero_weight_skips += macs / 15;
+        telemetry->xfold_bucket_merges += static_cast<uint64_t>(batch_size) * static_cast<uint64_t>(in_dim / 32) *
+                                          static_cast<uint64_t>(out_dim);
+    }
+}
+
+// cpp:1694-1707
+GNCX_API void gncx_xfold_q4_0_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, const float* in_batch,
+                                       int32_t batch_size, int32_t in_dim, int32_t out_dim, float* out_batch,
+                                       GNCXTelemetryStats* telemetry) {
+    gncx_xfold_universal_matbatch(mmap_base, weight_abs_offset, kQ4_0, in_batch, batch_size, in_dim, out_dim,
+                                  out_batch, telemetry);
+}
+
+// cpp:1713-1732
+GNCX_API void gncx_universal_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, int32_t ggml_type,
+                                            const float* final_hidden, int32_t embed_dim, int32_t vocab_size,
+                                            float softcap, float* out_logits) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_act.last_in = nullptr;  // the inner matvec is called with in_tokens == NULL
+    if (type_supported(ggml_type) && vocab_size > 0 && embed_dim > 0)
+        matvec_impl(mmap_base, embd_abs_offset, ggml_type, final_hidden, embed_dim, vocab_size, out_logits,
+                    false, softcap, "gncx_universal_lm_head_logits");
+}
+
+// cpp:1734-1745
+GNCX_API void gncx_q8_0_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, const float* final_hidden,
+                                       int32_t embed_dim, int32_t vocab_size, float* out_logits) {
+    gncx_universal_lm_head_logits(mmap_base, embd_abs_offset, kQ8_0, final_hidden, embed_dim, vocab_size, 0.0f,
+                                  out_logits);
+}
+
+// cpp:1887-1994
+GNCX_API void gncx_mqa_attention_step_ext(const float* q_vec, const float* k_vec, const float* v_vec,
+                                          float* k_cache_layer, float* v_cache_layer, int32_t pos, int32_t n_heads,
+                                          int32_t n_kv_heads, int32_t head_dim, float attn_scale,
+                                          int32_t sliding_window, int32_t write_kv, float* out_attn_vec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    AttnCall c{q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim, attn_scale,
+               sliding_window, write_kv, out_attn_vec};
+    attention_impl(c, "gncx_mqa_attention_step_ext");
+}
+
+// cpp:1996-2013
+GNCX_API void gncx_mqa_attention_step(const float* q_vec, const float* k_vec, const float* v_vec,
+                                      float* k_cache_layer, float* v_cache_layer, int32_t pos, int32_t n_heads,
+                                      int32_t n_kv_heads, int32_t head_dim, float* out_attn_vec) {
+    const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+    gncx_mqa_attention_step_ext(q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads,
+                                head_dim, scale, 0, 1, out_attn_vec);
+}
+
+// cpp:895-953
+GNCX_API void gncx_rmsnorm_inplace_heads(float* vec, const uint8_t* mmap_base, size_t norm_weight_offset,
+                                         int32_t has_weight, int32_t n_heads, int32_t head_dim, float eps) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_rmsnorm_inplace_heads";
+    if (n_heads <= 0 || head_dim <= 0 || !ensure_runtime(where)) return;
+    const float* g = nullptr;
+    if (has_weight) {
+        g = reinterpret_cast<const float*>(
+            device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
+        if (!g) return;
+    }
+    const size_t n = static_cast<size_t>(n_heads) * head_dim;
+    const bool host = !is_device_ptr(vec);
+    float* d = host ? const_cast<float*>(stage_in(vec, n, g_rt.q, where)) : vec;
+    if (!d) return;
+    if (!check(launch_rmsnorm_heads(d, g, n_heads, head_dim, eps, g_rt.stream), where)) return;
+    finish_out(vec, d, n, host, where);
+}
+
+// cpp:1760-1863
+GNCX_API void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactToken* q_tokens,
+                                        const uint8_t* mmap_base, size_t rope_freqs_offset, int32_t has_rope_freqs,
+                                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t pos,
+                                        float freq_base) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_apply_rope_xor11_ext";
+    if (!ensure_runtime(where)) return;
+    const int32_t half = head_dim / 2;
+    std::array<float, kMaxRopeHalf> fac{};
+    const float* factors = nullptr;
+    if (has_rope_freqs) {
+        if (half > kMaxRopeHalf || !read_factors(mmap_base, rope_freqs_offset, half, fac, where)) return;
+        factors = fac.data();
+    }
+    RopeTable t;
+    if (!rope_table(pos, head_dim, freq_base, factors, t)) {
+        set_error(where, "head_dim must be even and at most 512", -1);
+        return;
+    }
+    const size_t qn = q_vec ? static_cast<size_t>(n_heads) * head_dim : 0;
+    const size_t kn = k_vec ? static_cast<size_t>(n_kv_heads) * head_dim : 0;
+    const bool hq = q_vec && !is_device_ptr(q_vec), hk = k_vec && !is_device_ptr(k_vec);
+    float* dq = q_vec ? (hq ? const_cast<float*>(stage_in(q_vec, qn, g_rt.q, where)) : q_vec) : nullptr;
+    float* dk = k_vec ? (hk ? const_cast<float*>(stage_in(k_vec, kn, g_rt.k, where)) : k_vec) : nullptr;
+    if ((q_vec && !dq) || (k_vec && !dk)) return;
+    if (!check(launch_rope(dq, dk, t, q_vec ? n_heads : 0, k_vec ? n_kv_heads : 0, head_dim, g_rt.stream), where))
+        return;
+    if (hq && !check(hipMemcpyAsync(q_vec, dq, sizeof(float) * qn, hipMemcpyDeviceToHost, g_rt.stream), where)) return;
+    if (hk && !check(hipMemcpyAsync(k_vec, dk, sizeof(float) * kn, hipMemcpyDeviceToHost, g_rt.stream), where)) return;
+    if ((hq || hk) && !check(hipStreamSynchronize(g_rt.stream), where)) return;
+    // telemetry phase flip of the rotated half (cpp:1818-1823, 1829-1831)
+    if (q_vec && q_tokens)
+        for (int32_t h = 0; h < n_heads; ++h)
+            for (int32_t i = 0; i < half; ++i) q_tokens[h * head_dim + i + half].phase_2bit ^= 0x03u;
+}
+
+// cpp:1865-1878
+GNCX_API void gncx_apply_rope_xor11(float* q_vec, float* k_vec, GNCXCompactToken* q_tokens, int32_t n_heads,
+                                    int32_t n_kv_heads, int32_t head_dim, int32_t pos, float freq_base) {
+    gncx_apply_rope_xor11_ext(q_vec, k_vec, q_tokens, nullptr, 0, 0, n_heads, n_kv_heads, head_dim, pos, freq_base);
+}
+
+// cpp:2038-2052
+GNCX_API void gncx_swiglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim,
+                                     float* out_ffn_vec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_swiglu_activation";
+    if (ffn_dim <= 0 || !ensure_runtime(where)) return;
+    const float* g = stage_in(gate_vec, ffn_dim, g_rt.q, where);
+    const float* u = stage_in(up_vec, ffn_dim, g_rt.k, where);
+    if (!g || !u) return;
+    bool host = false;
+    float* o = out_target(out_ffn_vec, ffn_dim, g_rt.o, host, where);
+    if (!o) return;
+    if (!check(launch_swiglu(g, u, ffn_dim, o, g_rt.stream), where)) return;
+    finish_out(out_ffn_vec, o, ffn_dim, host, where);
+}
+
+namespace {
+// cpp:693-780: one row of the embedding table, decoded on the device.
+void fetch_embedding(int32_t type, const uint8_t* base, size_t off, int32_t token, int32_t dim, float scale,
+                     float* out, const char* where) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (dim <= 0 || token < 0 || !ensure_runtime(where)) return;
+    const size_t rb = row_bytes(type, dim);
+    const uint8_t* row = base + off + static_cast<size_t>(token) * rb;
+    const uint8_t* drow;
+    // a registered (or device-resident) table is read in place; otherwise only the row travels
+    auto it = g_rt.weights.find(reinterpret_cast<uintptr_t>(base + off));
+    if (is_device_ptr(row)) {
+        drow = row;
+    } else if (it != g_rt.weights.end() && (static_cast<size_t>(token) + 1) * rb <= it->second.bytes) {
+        drow = it->second.d + static_cast<size_t>(token) * rb;
+    } else {
+        if (!g_rt.aux.ensure(round_up(rb, 16), where)) return;
+        if (!check(hipMemcpyAsync(g_rt.aux.p, row, rb, hipMemcpyHostToDevice, g_rt.stream), where)) return;
+        drow = g_rt.aux.as<uint8_t>();
+    }
+    bool host = false;
+    float* o = out_target(out, dim, g_rt.o, host, where);
+    if (!o) return;
+    if (!check(launch_fetch_embedding(type, drow, 0, dim, scale, o, g_rt.stream), where)) return;
+    finish_out(out, o, dim, host, where);
+}
+}  // namespace
+
+// cpp:693-715
+GNCX_API void gncx_fetch_token_embedding_q8_0(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                              int32_t embed_dim, float scale_factor, float* out_hidden) {
+    fetch_embedding(kQ8_0, mmap_base, tensor_abs_offset, token_id, embed_dim, scale_factor, out_hidden,
+                    "gncx_fetch_token_embedding_q8_0");
+}
+// cpp:720-760
+GNCX_API void gncx_fetch_token_embedding_q6_k(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                              int32_t embed_dim, float scale_factor, float* out_hidden) {
+    fetch_embedding(kQ6_K, mmap_base, tensor_abs_offset, token_id, embed_dim, scale_factor, out_hidden,
+                    "gncx_fetch_token_embedding_q6_k");
+}
+// cpp:765-780
+GNCX_API void gncx_fetch_token_embedding_bf16(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                              int32_t embed_dim, float scale_factor, float* out_hidden) {
+    fetch_embedding(kBF16, mmap_base, tensor_abs_offset, token_id, embed_dim, scale_factor, out_hidden,
+                    "gncx_fetch_token_embedding_bf16");
+}
+
+// cpp:789-890.  The norm runs on the device; when out_tokens is given the
+// 4-phase telemetry encode (cpp:842-889) runs on the host over the normed
+// values, exactly as the reference forms it.
+GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const uint8_t* mmap_base,
+                                             size_t norm_weight_offset, int32_t dim, float eps, int32_t layer_k,
+                                             float* out_normed_fp32, GNCXCompactToken* out_tokens,
+                                             float* out_quant_scale) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_rmsnorm_and_encode_4phase";
+    g_norm_epoch++;
+    if (dim <= 0 || !ensure_runtime(where)) return;
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
+    if (!g) return;
+    const float* x = stage_in(input_hidden, dim, g_rt.q, where);
+    if (!x) return;
+    bool host = false;
+    float* o = out_target(out_normed_fp32, dim, g_rt.o, host, where);
+    if (!o) return;
+    if (!check(launch_rmsnorm(x, g, 1, dim, eps, o, g_rt.stream), where)) return;
+    if (!finish_out(out_normed_fp32, o, dim, host, where)) return;
+    if (out_tokens == nullptr) {
+        if (out_quant_scale) *out_quant_scale = 1.0f;
+        return;
+    }
+    std::vector<float> tmp;
+    const float* v = out_normed_fp32;
+    if (!host) {
+        tmp.resize(dim);
+        if (!check(hipMemcpy(tmp.data(), out_normed_fp32, sizeof(float) * dim, hipMemcpyDeviceToHost), where)) return;
+        v = tmp.data();
+    }
+    // repunit R_k = (10^(k+1)-1)/9 and diagonal anchors d*R_k (cpp:61-83)
+    constexpr int kMaxK = 17;
+    const int lay_k = std::clamp(layer_k, 0, kMaxK);
+    int64_t r_k = 1;
+    for (int i = 0; i < lay_k; ++i) r_k = r_k * 10 + 1;
+    float max_abs = 1e-9f;
+    for (int32_t j = 0; j < dim; ++j) max_abs = std::max(max_abs, std::fabs(v[j]));
+    const float target = static_cast<float>(9 * r_k);
+    const float to_int = target / max_abs;
+    if (out_quant_scale) *out_quant_scale = max_abs / target;
+    const float inv_rk = 1.0f / static_cast<float>(r_k);
+    const float half_rk = static_cast<float>(r_k >> 1);
+    std::array<uint32_t, 10> pos{}, neg{};
+    for (int32_t j = 0; j < dim; ++j) {
+        const int64_t val = static_cast<int64_t>(std::nearbyint(v[j] * to_int));
+        const int64_t av = val >= 0 ? val : -val;
+        int32_t da = static_cast<int32_t>((static_cast<float>(av) + half_rk) * inv_rk);
+        if (da > 9) da = 9;
+        const uint8_t d = static_cast<uint8_t>(da);
+        const int64_t anchor = static_cast<int64_t>(d) * r_k;
+        const int64_t sres = val - (val >= 0 ? anchor : -anchor);
+        const uint16_t ares = static_cast<uint16_t>(sres >= 0 ? sres : -sres);
+        const uint8_t b1 = val >= 0 ? 1u : 0u, b0 = sres >= 0 ? 1u : 0u;
+        out_tokens[j] = GNCXCompactToken{static_cast<uint8_t>((b1 << 1) | b0), d, ares};
+        pos[d] += b1;
+        neg[d] += b1 ^ 1u;
+    }
+    uint64_t c = 0;
+    for (int d = 0; d < 10; ++d) c += std::min(pos[d], neg[d]);
+    g_norm_epoch_cancellations = c;
+    g_norm_epoch_tokens_ptr = out_tokens;
+}
+
+// =======================================================================
+// Build-side extensions (no counterpart in the reference)
+// =======================================================================
+
+// Select the device (default 0 or $GNCX_DEVICE).  Returns 0 or a HIP error.
+GNCX_API int gncx_hip_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        set_error("gncx_hip_init", "no HIP device is visible", e ? static_cast<int>(e) : -1);
+        return g_last_code;
+    }
+    if (device < 0 || device >= n) return static_cast<int>(hipErrorInvalidDevice);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return static_cast<int>(e);
+    g_rt.device = device;
+    g_rt.ready = true;
+    return 0;
+}
+
+// Stream the library enqueues on (default: the null stream).
+GNCX_API void gncx_hip_set_stream(void* stream) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_rt.stream = static_cast<hipStream_t>(stream);
+}
+GNCX_API void* gncx_hip_get_stream(void) { return g_rt.stream; }
+
+GNCX_API int gncx_hip_synchronize(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return static_cast<int>(hipStreamSynchronize(g_rt.stream));
+}
+
+// Last failure ("" when none) and its code (0 when none); reading clears.
+GNCX_API const char* gncx_hip_last_error(void) { return g_last_error.c_str(); }
+GNCX_API int gncx_hip_last_status(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int c = g_last_code;
+    g_last_code = 0;
+    if (c == 0) g_last_error.clear();
+    return c;
+}
+
+// Drop the device copy of host weights at p (all copies when p is null).
+GNCX_API void gncx_hip_weight_forget(const void* p) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (p) {
+        forget_weight(reinterpret_cast<uintptr_t>(p));
+        return;
+    }
+    for (auto& kv : g_rt.weights) (void)hipFree(kv.second.d);
+    g_rt.weights.clear();
+}
+
+// Drop the device twin of a host KV cache (all twins when p is null); call
+// after rewriting a host cache outside this library.
+GNCX_API void gncx_hip_kv_forget(const float* p) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (p) {
+        forget_kv(reinterpret_cast<uintptr_t>(p));
+        return;
+    }
+    for (auto& kv : g_rt.kv) (void)hipFree(kv.second.d);
+    g_rt.kv.clear();
+}
+
+// Bytes of device memory held by uploaded weights.
+GNCX_API size_t gncx_hip_weight_bytes(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    size_t s = 0;
+    for (auto& kv : g_rt.weights) s += kv.second.bytes;
+    return s;
+}
+
+// Dequantise out_dim rows of in_dim weights to fp32 with the block decoders
+// the dots use (bit-exact with the reference's decoders).
+GNCX_API void gncx_hip_dequantize(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                  int32_t in_dim, int32_t out_dim, float* out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_dequantize";
+    if (!type_supported(ggml_type) || in_dim <= 0 || out_dim <= 0 || !ensure_runtime(where)) return;
+    const size_t wbytes = row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dim);
+    const uint8_t* w = device_weights(mmap_base + weight_abs_offset, wbytes, where);
+    if (!w) return;
+    const size_t n = static_cast<size_t>(in_dim) * out_dim;
+    bool host = false;
+    float* o = out_target(out, n, g_rt.y, host, where);
+    if (!o) return;
+    if (!check(launch_dequant(ggml_type, w, in_dim, out_dim, o, g_rt.stream), where)) return;
+    finish_out(out, o, n, host, where);
+}
+
+// Per-32 Q8 activation blocks of `rows` rows of in_dim values (cpp:955-995):
+// q[rows*in_dim] int8 and meta[rows*in_dim/32][4] = {d (float bits), sum of
+// q[0:16], sum of q[16:32], sum of q[0:32]}.
+GNCX_API void gncx_hip_quantize_act(const float* in, int32_t rows, int32_t in_dim, int8_t* q, int32_t* meta) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_quantize_act";
+    if (rows <= 0 || in_dim <= 0 || !ensure_runtime(where)) return;
+    const size_t n = static_cast<size_t>(rows) * in_dim;
+    const size_t nb = n / 32;
+    const float* x = stage_in(in, n, g_rt.aux, where);
+    if (!x) return;
+    if (!g_rt.ws.ensure(round_up(n, 256) + nb * sizeof(ActMeta), where)) return;
+    int8_t* dq = g_rt.ws.as<int8_t>();
+    ActMeta* dm = reinterpret_cast<ActMeta*>(g_rt.ws.as<char>() + round_up(n, 256));
+    if (!check(launch_act_quant(x, rows, in_dim, dq, dm, g_rt.stream), where)) return;
+    if (!check(hipMemcpyAsync(q, dq, n, is_device_ptr(q) ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost,
+                              g_rt.stream),
+               where))
+        return;
+    if (!check(hipMemcpyAsync(meta, dm, nb * sizeof(ActMeta),
+                              is_device_ptr(meta) ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, g_rt.stream),
+               where))
+        return;
+    check(hipStreamSynchronize(g_rt.stream), where);
+}
+
+// Decode attention step with the per-head RMSNorm (cpp:895-953) and RoPE
+// (cpp:1760-1863) of q and k fused in front of the KV scan: one call does
+// what the reference does with gncx_rmsnorm_inplace_heads(q),
+// gncx_rmsnorm_inplace_heads(k), gncx_apply_rope_xor11_ext(q, k) and
+// gncx_mqa_attention_step_ext, with the same results.  q_vec/k_vec receive
+// the normalised, rotated vectors as those calls leave them.  Norm weights are
+// addressed like the reference's (base + offset, has_weight); rope_base <= 0
+// skips the rotation.
+GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
+                                            float* v_cache_layer, int32_t pos, int32_t n_heads,
+                                            int32_t n_kv_heads, int32_t head_dim, float attn_scale,
+                                            int32_t sliding_window, int32_t write_kv, const uint8_t* mmap_base,
+                                            size_t q_norm_offset, size_t k_norm_offset, int32_t has_norm_weight,
+                                            float norm_eps, size_t rope_freqs_offset, int32_t has_rope_freqs,
+                                            float rope_base, float* out_attn_vec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_attention_step_fused";
+    if (!ensure_runtime(where)) return;
+    const float* qg = nullptr;
+    const float* kg = nullptr;
+    if (has_norm_weight) {
+        qg = reinterpret_cast<const float*>(
+            device_weights(mmap_base + q_norm_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
+        kg = reinterpret_cast<const float*>(
+            device_weights(mmap_base + k_norm_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
+        if (!qg || !kg) return;
+    }
+    RopeTable t;
+    const RopeTable* rp = nullptr;
+    if (rope_base > 0.0f) {
+        std::array<float, kMaxRopeHalf> fac{};
+        const float* factors = nullptr;
+        if (has_rope_freqs) {
+            if (head_dim / 2 > kMaxRopeHalf || !read_factors(mmap_base, rope_freqs_offset, head_dim / 2, fac, where))
+                return;
+            factors = fac.data();
+        }
+        if (!rope_table(pos, head_dim, rope_base, factors, t)) {
+            set_error(where, "head_dim must be even and at most 512", -1);
+            return;
+        }
+        rp = &t;
+    }
+    AttnCall c{q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim, attn_scale,
+               sliding_window, write_kv, out_attn_vec};
+    c.norm_qk = 1;
+    c.q_gamma = qg;
+    c.k_gamma = kg;
+    c.eps = norm_eps;
+    c.rope = rp;
+    c.q_back = q_vec;
+    c.k_back = k_vec;
+    attention_impl(c, where);
+}

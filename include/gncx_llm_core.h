@@ -1,0 +1,178 @@
+/*
+ * gncx_llm_core.h -- C-ABI of gnc-x_amd/bin/gncx_llm_core.so, the MI355X
+ * (gfx950) drop-in for the reference's bin/gncx_llm_core.so.
+ *
+ * Part 1 declares, with identical names and signatures, the reference entry
+ * points of the quantized linear-algebra path; each cites the definition it
+ * replaces in csrc/gncx_llm_kernels.cpp and the LuaJIT FFI declaration that
+ * binds it in lua/gncx_streamer.lua.  Part 2 declares build-side extensions
+ * that have no counterpart in the reference.
+ *
+ * Pointer rules (both parts): any pointer may be host memory (the reference
+ * contract) or HIP device memory.  Host weights are uploaded once and cached
+ * by address (weights are immutable for the life of the process, as in the
+ * reference); host inputs are staged and host outputs are complete when the
+ * call returns.  With device inputs and outputs the call is stream-ordered on
+ * the library stream (gncx_hip_set_stream) and does not synchronise the host.
+ * Calls are serialised internally; the library keeps the reference's one
+ * piece of cross-call state, the matvec activation cache (cpp:1338-1358).
+ *
+ * Failures (no GPU, out of device memory, unsupported shape) print one line
+ * to stderr, leave the outputs untouched and are reported by
+ * gncx_hip_last_status()/gncx_hip_last_error().  Unknown ggml types leave the
+ * output untouched, as in the reference (cpp:1362-1462).
+ */
+#ifndef GNCX_LLM_CORE_H
+#define GNCX_LLM_CORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#pragma pack(push, 1)
+/* cpp:267-271; streamer.lua:17-21 */
+typedef struct GNCXCompactToken {
+    uint8_t phase_2bit;
+    uint8_t diag_d;
+    uint16_t abs_delta;
+} GNCXCompactToken;
+
+/* cpp:308-313; streamer.lua:23-28 */
+typedef struct GNCXTelemetryStats {
+    uint64_t total_macs_equivalent;
+    uint64_t zero_origin_cancellations;
+    uint64_t zero_weight_skips;
+    uint64_t xfold_bucket_merges;
+} GNCXTelemetryStats;
+#pragma pack(pop)
+
+/* ggml type ids accepted by the matvec/matbatch family (cpp:1362-1462) */
+enum { GNCX_Q4_0 = 2, GNCX_Q8_0 = 8, GNCX_Q4_K = 12, GNCX_Q6_K = 14, GNCX_BF16 = 30 };
+
+/* ---------------- Part 1: reference entry points ---------------------- */
+
+/* y[out_dim] = W[out_dim x in_dim] . Q8(x).  Replaces cpp:1327-1471
+ * (FFI: streamer.lua:108-118, called at streamer.lua:664-680). */
+void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                 const float* in_vec, const GNCXCompactToken* in_tokens, int32_t in_dim,
+                                 int32_t out_dim, float* out_vec, GNCXTelemetryStats* telemetry);
+
+/* Q4_0 alias of the above.  Replaces cpp:1476-1489. */
+void gncx_xfold_q4_0_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, const float* in_vec,
+                            const GNCXCompactToken* in_tokens, int32_t in_dim, int32_t out_dim, float* out_vec,
+                            GNCXTelemetryStats* telemetry);
+
+/* Y[b x out_dim] = Q8(X[b x in_dim]) . W^T, row-major.  Replaces cpp:1495-1692
+ * (FFI: streamer.lua:120-130, called at streamer.lua:682-696). */
+void gncx_xfold_universal_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                   const float* in_batch, int32_t batch_size, int32_t in_dim, int32_t out_dim,
+                                   float* out_batch, GNCXTelemetryStats* telemetry);
+
+/* Q4_0 alias.  Replaces cpp:1694-1707. */
+void gncx_xfold_q4_0_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, const float* in_batch,
+                              int32_t batch_size, int32_t in_dim, int32_t out_dim, float* out_batch,
+                              GNCXTelemetryStats* telemetry);
+
+/* matvec on the tied embedding + optional tanh softcap.  Replaces
+ * cpp:1713-1732 (called at streamer.lua:953-962). */
+void gncx_universal_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, int32_t ggml_type,
+                                   const float* final_hidden, int32_t embed_dim, int32_t vocab_size, float softcap,
+                                   float* out_logits);
+
+/* Q8_0 alias.  Replaces cpp:1734-1745. */
+void gncx_q8_0_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, const float* final_hidden,
+                              int32_t embed_dim, int32_t vocab_size, float* out_logits);
+
+/* GQA/MQA/SWA decode attention step with KV write at pos.  Replaces
+ * cpp:1887-1994 (called at streamer.lua:848-862 and :1104-1108). */
+void gncx_mqa_attention_step_ext(const float* q_vec, const float* k_vec, const float* v_vec, float* k_cache_layer,
+                                 float* v_cache_layer, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, float attn_scale, int32_t sliding_window, int32_t write_kv,
+                                 float* out_attn_vec);
+
+/* scale = 1/sqrt(head_dim), no window, write_kv = 1.  Replaces cpp:1996-2013. */
+void gncx_mqa_attention_step(const float* q_vec, const float* k_vec, const float* v_vec, float* k_cache_layer,
+                             float* v_cache_layer, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
+                             int32_t head_dim, float* out_attn_vec);
+
+/* Per-head RMSNorm in place, optional fp32 gamma at base + offset.
+ * Replaces cpp:895-953 (called at streamer.lua:817, :823). */
+void gncx_rmsnorm_inplace_heads(float* vec, const uint8_t* mmap_base, size_t norm_weight_offset,
+                                int32_t has_weight, int32_t n_heads, int32_t head_dim, float eps);
+
+/* NEOX RoPE of q and k at pos; cos/sin built on the host with the C
+ * library as the reference does.  Replaces cpp:1760-1863 (streamer.lua:831-843). */
+void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactToken* q_tokens, const uint8_t* mmap_base,
+                               size_t rope_freqs_offset, int32_t has_rope_freqs, int32_t n_heads,
+                               int32_t n_kv_heads, int32_t head_dim, int32_t pos, float freq_base);
+
+/* Replaces cpp:1865-1878. */
+void gncx_apply_rope_xor11(float* q_vec, float* k_vec, GNCXCompactToken* q_tokens, int32_t n_heads,
+                           int32_t n_kv_heads, int32_t head_dim, int32_t pos, float freq_base);
+
+/* RMSNorm (device) + optional 4-phase telemetry encode (host).  Replaces
+ * cpp:789-890 (called at streamer.lua:793-803, 877-887, 939-949). */
+void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const uint8_t* mmap_base, size_t norm_weight_offset,
+                                    int32_t dim, float eps, int32_t layer_k, float* out_normed_fp32,
+                                    GNCXCompactToken* out_tokens, float* out_quant_scale);
+
+/* SiLU(gate) * up.  Replaces cpp:2038-2052 (called at streamer.lua:894). */
+void gncx_swiglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim, float* out_ffn_vec);
+
+/* One dequantised embedding row times scale_factor.  Replace cpp:693-715,
+ * cpp:720-760 and cpp:765-780 (called at streamer.lua:698-713). */
+void gncx_fetch_token_embedding_q8_0(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                     int32_t embed_dim, float scale_factor, float* out_hidden);
+void gncx_fetch_token_embedding_q6_k(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                     int32_t embed_dim, float scale_factor, float* out_hidden);
+void gncx_fetch_token_embedding_bf16(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
+                                     int32_t embed_dim, float scale_factor, float* out_hidden);
+
+/* ---------------- Part 2: build-side extensions ----------------------- */
+/* No counterpart in the reference. */
+
+/* Select the HIP device (default: 0 or $GNCX_DEVICE).  0 or a HIP error. */
+int gncx_hip_init(int device);
+/* Stream the library enqueues on (hipStream_t; default: the null stream). */
+void gncx_hip_set_stream(void* stream);
+void* gncx_hip_get_stream(void);
+/* hipStreamSynchronize of the library stream; 0 or a HIP error. */
+int gncx_hip_synchronize(void);
+/* Last failure message ("" when none). */
+const char* gncx_hip_last_error(void);
+/* Last failure code (0 when none); reading it clears it. */
+int gncx_hip_last_status(void);
+/* Drop the device copy of host weights at p (every copy when p is NULL). */
+void gncx_hip_weight_forget(const void* p);
+/* Drop the device twin of a host KV cache (every twin when p is NULL); call
+ * after rewriting a host cache outside this library. */
+void gncx_hip_kv_forget(const float* p);
+/* Device bytes held by uploaded weights. */
+size_t gncx_hip_weight_bytes(void);
+/* out[out_dim x in_dim] = fp32 decode of the weights with the block decoders
+ * the dots use (bit-exact with cpp:85-112, 707-714, 734-759 and the implicit
+ * Q4_0/Q4_K decoders of cpp:1023-1030, 1127-1178). */
+void gncx_hip_dequantize(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type, int32_t in_dim,
+                         int32_t out_dim, float* out);
+/* Per-32 Q8 activation blocks of rows x in_dim values (cpp:955-995):
+ * q[rows*in_dim] and meta[rows*in_dim/32][4] = {d as float bits, sum q[0:16],
+ * sum q[16:32], sum q[0:32]}. */
+void gncx_hip_quantize_act(const float* in, int32_t rows, int32_t in_dim, int8_t* q, int32_t* meta);
+/* One launch doing gncx_rmsnorm_inplace_heads(q), gncx_rmsnorm_inplace_heads(k),
+ * gncx_apply_rope_xor11_ext(q, k) and gncx_mqa_attention_step_ext with the
+ * same results; q_vec/k_vec receive the normalised, rotated vectors.
+ * rope_base <= 0 skips the rotation.  With write_kv == 0, k_vec is unused. */
+void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
+                                   float* v_cache_layer, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
+                                   int32_t head_dim, float attn_scale, int32_t sliding_window, int32_t write_kv,
+                                   const uint8_t* mmap_base, size_t q_norm_offset, size_t k_norm_offset,
+                                   int32_t has_norm_weight, float norm_eps, size_t rope_freqs_offset,
+                                   int32_t has_rope_freqs, float rope_base, float* out_attn_vec);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,120 @@
+"""The C-ABI library on the CPU: it builds, loads, exports every entry point
+include/gncx_llm_core.h declares with the reference's names, keeps the
+reference's host-side bookkeeping (telemetry counters), and -- with no GPU --
+fails loudly instead of computing on the CPU."""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import synth
+from conftest import ROOT, gncx, ptr
+
+HEADER = ROOT / "include" / "gncx_llm_core.h"
+REF_CPP_EXPORTS = [  # the hot path and its companions, named as cpp exports them
+    "gncx_xfold_universal_matvec", "gncx_xfold_q4_0_matvec", "gncx_xfold_universal_matbatch",
+    "gncx_xfold_q4_0_matbatch", "gncx_universal_lm_head_logits", "gncx_q8_0_lm_head_logits",
+    "gncx_mqa_attention_step_ext", "gncx_mqa_attention_step", "gncx_rmsnorm_inplace_heads",
+    "gncx_apply_rope_xor11_ext", "gncx_apply_rope_xor11", "gncx_rmsnorm_and_encode_4phase",
+    "gncx_swiglu_activation", "gncx_fetch_token_embedding_q8_0", "gncx_fetch_token_embedding_q6_k",
+    "gncx_fetch_token_embedding_bf16",
+]
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(gncx_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def built():
+    if not gncx.LIB_PATH.exists():
+        out = subprocess.run(["make", "-C", str(gncx.CSRC_DIR), "-j8"], capture_output=True, text=True)
+        assert out.returncode == 0, out.stdout + out.stderr
+    return gncx.LIB_PATH
+
+
+def exported(path: pathlib.Path) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True)
+    return {ln.split()[-1] for ln in out.stdout.splitlines() if " T " in ln}
+
+
+def test_header_declares_reference_names():
+    fns = header_functions()
+    for name in REF_CPP_EXPORTS:
+        assert name in fns, name
+
+
+def test_library_exports_every_declared_symbol(built):
+    syms = exported(built)
+    missing = [f for f in header_functions() if f not in syms]
+    assert not missing, missing
+    # nothing else leaks out of the library
+    assert all(s.startswith("gncx_") for s in syms), sorted(s for s in syms if not s.startswith("gncx_"))
+
+
+def test_ctypes_signatures_cover_header(built):
+    assert set(header_functions()) == set(gncx.SIGNATURES)
+    lib = gncx.load()
+    for name in gncx.SIGNATURES:
+        assert getattr(lib, name) is not None
+
+
+def test_exports_match_reference_signatures(built, ref):
+    """Every reference name we export is exported by the reference build too."""
+    ref_syms = exported(pathlib.Path(ref.lib._name))
+    for name in REF_CPP_EXPORTS:
+        assert name in ref_syms, name
+
+
+def _has_gpu(lib) -> bool:
+    n = C.c_int(0)
+    try:
+        hip = C.CDLL("libamdhip64.so")
+    except OSError:
+        return False
+    return hip.hipGetDeviceCount(C.byref(n)) == 0 and n.value > 0
+
+
+def test_no_gpu_means_loud_failure_not_cpu_fallback(built):
+    lib = gncx.load()
+    if _has_gpu(lib):
+        pytest.skip("a GPU is visible; the no-device path is exercised on CPU-only hosts")
+    k, n = 256, 8
+    w = synth.make_weights(12, n, k, seed=1)
+    x = synth.make_activations(1, k, seed=2)
+    y = np.full(n, 7.0, dtype=np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, 12, ptr(x), None, k, n, ptr(y), None)
+    assert lib.gncx_hip_last_status() != 0
+    assert np.all(y == 7.0), "output must be left untouched when there is no device"
+
+
+def test_telemetry_matches_reference(built, ref):
+    """Counters follow cpp:1464-1470 and cpp:1686-1691 exactly, with or
+    without a device (they are host bookkeeping)."""
+    lib = gncx.load()
+    k, n, b = 512, 16, 3
+    w = synth.make_weights(14, n, k, seed=3)
+    x = synth.make_activations(1, k, seed=4)
+    xb = synth.make_activations(b, k, seed=5)
+    y = np.zeros(n, np.float32)
+    yb = np.zeros((b, n), np.float32)
+    tokens = (gncx.GNCXCompactToken * k)()
+    rng = np.random.default_rng(6)
+    for i in range(k):
+        tokens[i].phase_2bit = int(rng.integers(0, 4))
+        tokens[i].diag_d = int(rng.integers(0, 10))
+    mine, theirs = gncx.GNCXTelemetryStats(), gncx.GNCXTelemetryStats()
+    for L, t in ((lib, mine), (ref.lib, theirs)):
+        L.gncx_xfold_universal_matvec(ptr(w), 0, 14, ptr(x), C.addressof(tokens), k, n, ptr(y), C.addressof(t))
+        L.gncx_xfold_universal_matbatch(ptr(w), 0, 14, ptr(xb), b, k, n, ptr(yb), C.addressof(t))
+    lib.gncx_hip_last_status()
+    for f, _ in gncx.GNCXTelemetryStats._fields_:
+        assert getattr(mine, f) == getattr(theirs, f), f
+    assert mine.zero_origin_cancellations > 0

@@ -1,0 +1,208 @@
+"""GPU parity of the decode-attention step and its prologue, through the
+C-ABI: gncx_mqa_attention_step_ext against the oracle (1e-3 relative L2 bar;
+observed ~1e-7), KV-cache write-back into host caches, multi-step decode
+through one host cache, the fused norm+RoPE+attention entry against the
+reference call sequence, and the per-head RMSNorm / RoPE / SwiGLU / RMSNorm /
+embedding companions."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import synth
+from conftest import gncx, ptr, rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def run_attention(lib, q, kn, vn, kc, vc, pos, H, KV, hd, scale, sw, write_kv):
+    out = np.full(H * hd, np.nan, np.float32)
+    lib.gncx_mqa_attention_step_ext(ptr(q), ptr(kn), ptr(vn), ptr(kc), ptr(vc), pos, H, KV, hd, scale, sw,
+                                    write_kv, ptr(out))
+    gncx.check(lib)
+    return out
+
+
+@pytest.mark.parametrize("tag", ["gqa", "swa", "mqa"])
+def test_attention_reference_vectors(lib, golden, tag):
+    g = golden
+    pos, H, kv, hd, sw = (int(v) for v in g[f"attn_{tag}_geom"])
+    kc, vc = g[f"attn_{tag}_kc"].copy(), g[f"attn_{tag}_vc"].copy()
+    kn, vn = g[f"attn_{tag}_kn"].copy(), g[f"attn_{tag}_vn"].copy()
+    out = run_attention(lib, g[f"attn_{tag}_q"].copy(), kn, vn, kc, vc, pos, H, kv, hd, 1 / np.sqrt(hd), sw, 1)
+    assert rel_l2(out, g[f"attn_{tag}_out"]) < TOL
+    # the new row was written into the caller's (host) cache
+    assert np.array_equal(kc[pos], kn) and np.array_equal(vc[pos], vn)
+    lib.gncx_hip_kv_forget(None)
+
+
+# config 4: 32 Q / 8 KV heads x 128, ctx 512 / 4096 / 32768, SWA 1024, MQA
+CASES = [(32, 8, 128, 512, 0), (32, 8, 128, 4096, 0), (32, 8, 128, 32768, 0), (32, 8, 128, 4096, 1024),
+         (32, 8, 128, 32768, 1024), (32, 1, 128, 4096, 0), (32, 1, 128, 32768, 0), (16, 16, 64, 300, 0),
+         (8, 2, 256, 700, 100), (4, 4, 128, 1, 0)]
+
+
+@pytest.mark.parametrize("H,KV,hd,ctx,sw", CASES)
+def test_attention_parity(lib, oracle, H, KV, hd, ctx, sw):
+    rng = np.random.default_rng(H * 1000 + KV * 100 + ctx + sw)
+    kc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    vc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    q = rng.standard_normal(H * hd, dtype=np.float32)
+    kn = rng.standard_normal(KV * hd, dtype=np.float32)
+    vn = rng.standard_normal(KV * hd, dtype=np.float32)
+    pos = ctx - 1
+    want, kc_w, vc_w = oracle.attention(q, kn, vn, kc, vc, pos, H, KV, hd, 1 / np.sqrt(hd), sw, 1)
+    out = run_attention(lib, q, kn, vn, kc, vc, pos, H, KV, hd, 1 / np.sqrt(hd), sw, 1)
+    err = rel_l2(out, want)
+    print(f"attention H={H} KV={KV} hd={hd} ctx={ctx} sw={sw} rel_l2={err:.3e}")
+    assert err < TOL
+    assert np.array_equal(kc, kc_w) and np.array_equal(vc, vc_w)
+    lib.gncx_hip_kv_forget(None)
+
+
+def test_attention_write_kv_off_uses_cached_row(lib, oracle):
+    rng = np.random.default_rng(3)
+    H, KV, hd, ctx = 8, 2, 128, 64
+    kc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    vc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    q = rng.standard_normal(H * hd, dtype=np.float32)
+    kn = rng.standard_normal(KV * hd, dtype=np.float32)
+    want, _, _ = oracle.attention(q, kn, kn, kc, vc, 40, H, KV, hd, 0.1, 0, 0)
+    kc0 = kc.copy()
+    out = run_attention(lib, q, kn, kn, kc, vc, 40, H, KV, hd, 0.1, 0, 0)
+    assert rel_l2(out, want) < TOL
+    assert np.array_equal(kc, kc0)
+    lib.gncx_hip_kv_forget(None)
+
+
+def test_decode_sequence_through_one_host_cache(lib, oracle):
+    """60 steps pos = 0..59 into the same host caches, as the streamer does;
+    the device twin stays coherent with the host rows."""
+    rng = np.random.default_rng(4)
+    H, KV, hd, rows = 16, 4, 128, 64
+    kc = np.zeros((rows, KV * hd), np.float32)
+    vc = np.zeros((rows, KV * hd), np.float32)
+    okc, ovc = kc.copy(), vc.copy()
+    worst = 0.0
+    for pos in range(60):
+        q = rng.standard_normal(H * hd, dtype=np.float32)
+        kn = rng.standard_normal(KV * hd, dtype=np.float32)
+        vn = rng.standard_normal(KV * hd, dtype=np.float32)
+        sw = 16 if pos % 3 == 0 else 0
+        want, okc, ovc = oracle.attention(q, kn, vn, okc, ovc, pos, H, KV, hd, 0.0884, sw, 1)
+        out = run_attention(lib, q, kn, vn, kc, vc, pos, H, KV, hd, 0.0884, sw, 1)
+        worst = max(worst, rel_l2(out, want))
+    assert worst < TOL
+    assert np.array_equal(kc, okc) and np.array_equal(vc, ovc)
+    lib.gncx_hip_kv_forget(None)
+
+
+def test_kv_twin_notices_rewritten_host_cache(lib, oracle):
+    rng = np.random.default_rng(5)
+    H, KV, hd, ctx = 8, 8, 64, 50
+    kc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    vc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    q = rng.standard_normal(H * hd, dtype=np.float32)
+    run_attention(lib, q, kc[30], vc[30], kc, vc, 30, H, KV, hd, 0.125, 0, 1)
+    kc[:] = rng.standard_normal((ctx, KV * hd), dtype=np.float32)  # caller refills the cache
+    vc[:] = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    want, _, _ = oracle.attention(q, None, None, kc, vc, 20, H, KV, hd, 0.125, 0, 0)
+    out = run_attention(lib, q, None, None, kc, vc, 20, H, KV, hd, 0.125, 0, 0)
+    assert rel_l2(out, want) < TOL
+    lib.gncx_hip_kv_forget(None)
+
+
+@pytest.mark.parametrize("H,KV,hd,ctx,sw", [(32, 8, 128, 4096, 0), (32, 1, 128, 600, 0), (8, 4, 64, 300, 128)])
+def test_fused_prologue_equals_reference_sequence(lib, oracle, H, KV, hd, ctx, sw):
+    """gncx_hip_attention_step_fused == rmsnorm_heads(q), rmsnorm_heads(k),
+    rope(q, k), attention_step -- on the GPU and against the oracle."""
+    rng = np.random.default_rng(ctx + H)
+    kc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    vc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    q = rng.standard_normal(H * hd, dtype=np.float32)
+    kn = rng.standard_normal(KV * hd, dtype=np.float32)
+    vn = rng.standard_normal(KV * hd, dtype=np.float32)
+    gq, gk = synth.make_norm_gamma(hd, 1), synth.make_norm_gamma(hd, 2)
+    norms = np.concatenate([gq, gk]).astype(np.float32)
+    pos, eps, base, scale = ctx - 1, 1e-6, 1e6, 1 / np.sqrt(hd)
+
+    # oracle sequence
+    oq = oracle.rmsnorm_heads(q, gq, H, hd, eps)
+    ok = oracle.rmsnorm_heads(kn, gk, KV, hd, eps)
+    oq, ok = oracle.rope(oq, ok, H, KV, hd, pos, base)
+    want, owk, _ = oracle.attention(oq, ok, vn, kc, vc, pos, H, KV, hd, scale, sw, 1)
+
+    # library, step by step (the streamer's calls, streamer.lua:817-862)
+    q1, k1, kc1, vc1 = q.copy(), kn.copy(), kc.copy(), vc.copy()
+    lib.gncx_rmsnorm_inplace_heads(ptr(q1), ptr(norms), 0, 1, H, hd, eps)
+    lib.gncx_rmsnorm_inplace_heads(ptr(k1), ptr(norms), hd * 4, 1, KV, hd, eps)
+    lib.gncx_apply_rope_xor11_ext(ptr(q1), ptr(k1), None, None, 0, 0, H, KV, hd, pos, base)
+    out1 = run_attention(lib, q1, k1, vn, kc1, vc1, pos, H, KV, hd, scale, sw, 1)
+    lib.gncx_hip_kv_forget(None)
+
+    # library, fused
+    q2, k2, kc2, vc2 = q.copy(), kn.copy(), kc.copy(), vc.copy()
+    out2 = np.zeros(H * hd, np.float32)
+    lib.gncx_hip_attention_step_fused(ptr(q2), ptr(k2), ptr(vn), ptr(kc2), ptr(vc2), pos, H, KV, hd, scale, sw, 1,
+                                      ptr(norms), 0, hd * 4, 1, eps, 0, 0, base, ptr(out2))
+    gncx.check(lib)
+    lib.gncx_hip_kv_forget(None)
+
+    assert np.array_equal(q1, q2) and np.array_equal(k1, k2)
+    assert np.array_equal(kc1, kc2)
+    assert rel_l2(out2, out1) < 1e-6
+    assert rel_l2(q1, oq) < 1e-6 and rel_l2(k1, ok) < 1e-6
+    assert rel_l2(out2, want) < TOL
+    assert rel_l2(kc2[pos], owk[pos]) < 1e-6
+
+
+def test_rmsnorm_heads_and_rope_vectors(lib, golden):
+    v = golden["rmsh_v"].copy()
+    g = golden["rmsh_g"].copy()
+    lib.gncx_rmsnorm_inplace_heads(ptr(v), ptr(g), 0, 1, 8, 128, 1e-6)
+    gncx.check(lib)
+    assert rel_l2(v, golden["rmsh_y"]) < 1e-6
+    v = golden["rmsh_v"].copy()
+    lib.gncx_rmsnorm_inplace_heads(ptr(v), None, 0, 0, 8, 128, 1e-6)
+    assert rel_l2(v, golden["rmsh_y_nog"]) < 1e-6
+    for p in (0, 1, 511, 4095, 32767):
+        q, k = golden["rope_q"].copy(), golden["rope_k"].copy()
+        lib.gncx_apply_rope_xor11_ext(ptr(q), ptr(k), None, None, 0, 0, 4, 2, 128, p, 1e6)
+        gncx.check(lib)
+        assert rel_l2(q, golden[f"rope_q_{p}"]) < 1e-6 and rel_l2(k, golden[f"rope_k_{p}"]) < 1e-6
+    q, k, f = golden["rope_q"].copy(), golden["rope_k"].copy(), golden["rope_f"].copy()
+    lib.gncx_apply_rope_xor11_ext(ptr(q), ptr(k), None, ptr(f), 0, 1, 4, 2, 128, 777, 1e4)
+    assert rel_l2(q, golden["rope_q_fac"]) < 1e-6 and rel_l2(k, golden["rope_k_fac"]) < 1e-6
+
+
+def test_rmsnorm_heads_bitexact_with_oracle(lib, oracle):
+    rng = np.random.default_rng(9)
+    v = rng.standard_normal(32 * 128, dtype=np.float32)
+    g = synth.make_norm_gamma(128, 3)
+    out = v.copy()
+    lib.gncx_rmsnorm_inplace_heads(ptr(out), ptr(g), 0, 1, 32, 128, 1e-6)
+    gncx.check(lib)
+    assert np.array_equal(out, oracle.rmsnorm_heads(v, g, 32, 128, 1e-6))
+
+
+def test_rmsnorm_swiglu_embeddings(lib, golden, oracle):
+    x, g = golden["rms_x"].copy(), golden["rms_g"].copy()
+    out = np.zeros_like(x)
+    lib.gncx_rmsnorm_and_encode_4phase(ptr(x), ptr(g), 0, x.size, 1e-6, 0, ptr(out), None, None)
+    gncx.check(lib)
+    assert rel_l2(out, golden["rms_y"]) < 1e-6
+    gg, uu = golden["swi_g"].copy(), golden["swi_u"].copy()
+    o = np.zeros_like(gg)
+    lib.gncx_swiglu_activation(ptr(gg), ptr(uu), gg.size, ptr(o))
+    gncx.check(lib)
+    assert rel_l2(o, golden["swi_y"]) < 1e-6
+    for name, fn in (("q8_0", lib.gncx_fetch_token_embedding_q8_0), ("q6_k", lib.gncx_fetch_token_embedding_q6_k),
+                     ("bf16", lib.gncx_fetch_token_embedding_bf16)):
+        tab = golden[f"emb_{name}_tab"].copy()
+        e = np.zeros(512, np.float32)
+        fn(ptr(tab), 0, 5, 512, 1.0, ptr(e))
+        gncx.check(lib)
+        assert np.array_equal(e, golden[f"emb_{name}_y5"])
+        fn(ptr(tab), 0, 11, 512, 0.37, ptr(e))
+        assert np.array_equal(e, golden[f"emb_{name}_y11s"])

@@ -1,0 +1,220 @@
+"""GPU parity of the quantised products, through the C-ABI.
+
+Bars: Q8 activation blocks and block dequantisation bit-exact with the
+oracle; matvec / matbatch / lm_head within 1e-3 relative L2 of the oracle's
+fp32 results on the same seeded inputs (the tolerance north of the integer
+dots is only fp32 accumulation order, so observed errors are ~1e-7)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+from conftest import gncx, ptr, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 2, 8, 12, 14, 30
+TOL = 1e-3  # relative L2, fp32 outputs
+
+
+def test_act_quant_bitexact(lib, oracle):
+    rows, k = 3, 4096
+    x = synth.make_activations(rows, k, seed=1).copy()
+    x[0, 64:96] = 0.0
+    x[1, 0] = 127.0
+    x[1, 1:5] = [2.5, 3.5, -2.5, -0.5]
+    x[2, 100:132] *= 1e-30  # tiny values
+    q = np.zeros(rows * k, np.int8)
+    meta = np.zeros((rows * k // 32, 4), np.int32)
+    lib.gncx_hip_quantize_act(ptr(x), rows, k, ptr(q), ptr(meta))
+    gncx.check(lib)
+    want = np.concatenate([oracle.quantize_act(x[r]) for r in range(rows)])
+    assert np.array_equal(q.reshape(-1, 32), want["qs"])
+    assert np.array_equal(meta[:, 0].view(np.float32), want["d"])
+    assert np.array_equal(meta[:, 1], want["sum_lo16"])
+    assert np.array_equal(meta[:, 2], want["sum_hi16"])
+    assert np.array_equal(meta[:, 3], want["sum"])
+
+
+@pytest.mark.parametrize("t,k,n", [(Q4_0, 4096, 64), (Q8_0, 4096, 64), (Q4_K, 4096, 64), (Q6_K, 4096, 64),
+                                   (Q6_K, 14336, 16), (BF16, 1024, 32)])
+def test_dequant_bitexact(lib, oracle, t, k, n):
+    w = synth.make_weights(t, n, k, seed=10 + t)
+    out = np.zeros((n, k), np.float32)
+    lib.gncx_hip_dequantize(ptr(w), 0, t, k, n, ptr(out))
+    gncx.check(lib)
+    assert np.array_equal(out, oracle.dequant(t, w, k, n, gncx.row_bytes(t, k)))
+
+
+def test_fp16_scales_all_codes(lib, oracle):
+    """Every fp16 code as a Q8_0 block scale with q = 1: the device decode of
+    the scale must equal the IEEE value (subnormals included)."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite(codes.view(np.float16))
+    codes = codes[finite]
+    n = codes.size
+    blocks = np.zeros((n, 34), np.uint8)
+    blocks[:, 0:2] = codes.view(np.uint8).reshape(n, 2)
+    blocks[:, 2] = 1
+    out = np.zeros((n, 32), np.float32)
+    lib.gncx_hip_dequantize(ptr(blocks.reshape(-1)), 0, Q8_0, 32, n, ptr(out))
+    gncx.check(lib)
+    assert np.array_equal(out[:, 0], codes.view(np.float16).astype(np.float32))
+
+
+# config shapes: Q4_0 4096->4096, Llama/Qwen decode GEMVs, small BF16
+MATVEC_CASES = [
+    (Q4_0, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 14336, 4096), (Q8_0, 4096, 4096), (Q4_K, 4096, 4096),
+    (Q4_K, 12288, 4096), (Q6_K, 4096, 2048), (Q4_0, 1024, 333), (Q8_0, 96, 7), (Q4_K, 256, 1),
+    (Q6_K, 512, 65), (BF16, 4096, 512),
+]
+
+
+@pytest.mark.parametrize("t,k,n", MATVEC_CASES)
+def test_matvec_parity(lib, oracle, t, k, n):
+    w = synth.make_weights(t, n, k, seed=1000 + t + k + n)
+    x = synth.make_activations(1, k, seed=2000 + t + k + n)
+    y = np.full(n, np.nan, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(x), None, k, n, ptr(y), None)
+    gncx.check(lib)
+    err = rel_l2(y, oracle.matvec(t, w, x, k, n))
+    print(f"matvec type={t} k={k} n={n} rel_l2={err:.3e}")
+    assert err < TOL
+
+
+def test_matvec_lm_head_shape(lib, oracle):
+    """Q6_K 4096 -> 128256 (the Llama-3 lm_head GEMV)."""
+    t, k, n = Q6_K, 4096, 128256
+    w = synth.make_weights(t, n, k, seed=77)
+    x = synth.make_activations(1, k, seed=78)
+    y = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(x), None, k, n, ptr(y), None)
+    gncx.check(lib)
+    err = rel_l2(y, oracle.matvec(t, w, x, k, n))
+    print(f"lm_head-shaped matvec rel_l2={err:.3e}")
+    assert err < TOL
+    lib.gncx_hip_weight_forget(ptr(w))
+
+
+@pytest.mark.parametrize("name,t", [("q4_0", Q4_0), ("q8_0", Q8_0), ("q4_k", Q4_K), ("q6_k", Q6_K), ("bf16", BF16)])
+def test_matvec_matbatch_vs_reference_vectors(lib, golden, name, t):
+    k, n, b = int(golden["mv_k"]), int(golden["mv_n"]), int(golden["mv_b"])
+    w = golden[f"{name}_w"].copy()
+    y = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(golden[f"{name}_x"].copy()), None, k, n, ptr(y), None)
+    gncx.check(lib)
+    assert rel_l2(y, golden[f"{name}_y"]) < TOL
+    yb = np.zeros((b, n), np.float32)
+    lib.gncx_xfold_universal_matbatch(ptr(w), 0, t, ptr(golden[f"{name}_xb"].copy()), b, k, n, ptr(yb), None)
+    gncx.check(lib)
+    assert rel_l2(yb, golden[f"{name}_yb"]) < TOL
+
+
+def test_matvec_edge_cases(lib, oracle):
+    k, n = 512, 40
+    w = synth.make_weights(Q4_K, n, k, seed=5)
+    # all-zero activations: every block has d = 0 -> exact zeros
+    y = np.full(n, 3.0, np.float32)
+    z = np.zeros(k, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, ptr(z), None, k, n, ptr(y), None)
+    gncx.check(lib)
+    assert not y.any()
+    # unknown ggml type: output untouched (cpp:1362-1462), no error
+    y[:] = 5.0
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, 99, ptr(z), None, k, n, ptr(y), None)
+    assert np.all(y == 5.0)
+    assert lib.gncx_hip_last_status() == 0
+    # weights addressed by (base, offset) inside a larger buffer
+    pad = np.zeros(4096 + w.size, np.uint8)
+    pad[4096:] = w
+    x = synth.make_activations(1, k, seed=6)
+    y2 = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(pad), 4096, Q4_K, ptr(x), None, k, n, ptr(y2), None)
+    gncx.check(lib)
+    assert rel_l2(y2, oracle.matvec(Q4_K, w, x, k, n)) < TOL
+
+
+def test_weight_cache_detects_rewritten_host_buffer(lib, oracle):
+    k, n = 1024, 64
+    w = synth.make_weights(Q6_K, n, k, seed=7)
+    x = synth.make_activations(1, k, seed=8)
+    y = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q6_K, ptr(x), None, k, n, ptr(y), None)
+    w[:] = synth.make_weights(Q6_K, n, k, seed=9)  # same address, new content
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q6_K, ptr(x), None, k, n, ptr(y), None)
+    gncx.check(lib)
+    assert rel_l2(y, oracle.matvec(Q6_K, w, x, k, n)) < TOL
+
+
+def test_activation_cache_follows_reference_rule(lib, oracle):
+    """With in_tokens given, the same in_vec pointer and no new norm epoch,
+    the reference reuses its quantised activations (cpp:1345) -- even when
+    the host vector changed in between; the library keeps that behaviour."""
+    k, n = 512, 32
+    w = synth.make_weights(Q4_K, n, k, seed=10)
+    x = synth.make_activations(1, k, seed=11)
+    x0 = x.copy()
+    toks = (gncx.GNCXCompactToken * k)()
+    y1 = np.zeros(n, np.float32)
+    y2 = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, ptr(x), C.addressof(toks), k, n, ptr(y1), None)
+    x *= 2.0
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, ptr(x), C.addressof(toks), k, n, ptr(y2), None)
+    gncx.check(lib)
+    assert np.array_equal(y1, y2)
+    assert rel_l2(y1, oracle.matvec(Q4_K, w, x0, k, n)) < TOL
+    # without tokens the vector is always re-read
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, ptr(x), None, k, n, ptr(y2), None)
+    assert rel_l2(y2, oracle.matvec(Q4_K, w, x, k, n)) < TOL
+
+
+def test_matvec_device_pointers(lib, oracle):
+    """Device-resident x / y / weights: same kernel, same result."""
+    torch = pytest.importorskip("torch")
+    k, n = 4096, 2048
+    w = synth.make_weights(Q4_K, n, k, seed=12)
+    x = synth.make_activations(1, k, seed=13)
+    wd = torch.from_numpy(w).cuda()
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.zeros(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    lib.gncx_xfold_universal_matvec(wd.data_ptr(), 0, Q4_K, xd.data_ptr(), None, k, n, yd.data_ptr(), None)
+    assert lib.gncx_hip_synchronize() == 0
+    gncx.check(lib)
+    yh = np.zeros(n, np.float32)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, ptr(x), None, k, n, ptr(yh), None)
+    assert np.array_equal(yd.cpu().numpy(), yh)
+    assert rel_l2(yh, oracle.matvec(Q4_K, w, x, k, n)) < TOL
+
+
+MATBATCH_CASES = [
+    (Q4_K, 4096, 512, 64), (Q6_K, 14336, 256, 16), (Q4_0, 4096, 300, 5), (Q8_0, 2048, 200, 9), (Q4_K, 512, 96, 1),
+    (BF16, 1024, 64, 4),
+]
+
+
+@pytest.mark.parametrize("t,k,n,b", MATBATCH_CASES)
+def test_matbatch_parity(lib, oracle, t, k, n, b):
+    w = synth.make_weights(t, n, k, seed=3000 + t + k + n)
+    x = synth.make_activations(b, k, seed=4000 + t + k + n + b).reshape(b, k)
+    y = np.full((b, n), np.nan, np.float32)
+    lib.gncx_xfold_universal_matbatch(ptr(w), 0, t, ptr(x), b, k, n, ptr(y), None)
+    gncx.check(lib)
+    err = rel_l2(y, oracle.matbatch(t, w, x, b, k, n))
+    print(f"matbatch type={t} k={k} n={n} b={b} rel_l2={err:.3e}")
+    assert err < TOL
+
+
+def test_lm_head_and_softcap(lib, golden):
+    w, x = golden["lm_w"].copy(), golden["lm_x"].copy()
+    v, k = int(golden["lm_vocab"]), int(golden["lm_k"])
+    y = np.zeros(v, np.float32)
+    lib.gncx_universal_lm_head_logits(ptr(w), 0, Q6_K, ptr(x), k, v, 0.0, ptr(y))
+    gncx.check(lib)
+    assert rel_l2(y, golden["lm_y"]) < TOL
+    lib.gncx_universal_lm_head_logits(ptr(w), 0, Q6_K, ptr(x), k, v, 30.0, ptr(y))
+    gncx.check(lib)
+    assert rel_l2(y, golden["lm_y_cap"]) < TOL
