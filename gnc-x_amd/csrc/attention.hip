@@ -55,19 +55,20 @@ struct AttnParams {
 template <int HD>
 __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope, float eps,
                               const RopeTable& t, int lane) {
+#pragma clang fp contract(off)
     if (norm) {
         const float inv = head_inv_rms(v, HD, eps, lane);
         for (int i = lane; i < HD; i += 64) {
-            const float x = __fmul_rn(v[i], inv);
-            v[i] = gamma ? __fmul_rn(x, gamma[i]) : x;
+            const float x = v[i] * inv;
+            v[i] = gamma ? x * gamma[i] : x;
         }
     }
     if (rope) {
         constexpr int H = HD / 2;
         for (int i = lane; i < H; i += 64) {
             const float x1 = v[i], x2 = v[i + H];
-            v[i] = __fsub_rn(__fmul_rn(x1, t.c[i]), __fmul_rn(x2, t.s[i]));
-            v[i + H] = __fadd_rn(__fmul_rn(x2, t.c[i]), __fmul_rn(x1, t.s[i]));
+            v[i] = x1 * t.c[i] - x2 * t.s[i];
+            v[i + H] = x2 * t.c[i] + x1 * t.s[i];
         }
     }
 }
@@ -244,25 +245,60 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     }
 }
 
-// out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12)
-__global__ void attn_merge_kernel(const float* __restrict part_o, const float* __restrict part_ml,
-                                  int32_t n_split, int32_t n_heads, int32_t hd, float* __restrict out) {
-    const int h = blockIdx.x;
-    float M = -1e30f;
-    for (int s = 0; s < n_split; ++s) M = fmaxf(M, part_ml[(static_cast<size_t>(s) * n_heads + h) * 2]);
-    float L = 0.0f;
-    for (int s = 0; s < n_split; ++s) {
-        const float* ml = part_ml + (static_cast<size_t>(s) * n_heads + h) * 2;
-        L += ml[1] * expf(ml[0] - M);
+// out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12), one
+// work-group per query head: the split weights e^(m_j - M) are formed once in
+// LDS, then each thread sums a strided subset of splits for one dimension.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxSplit = 4096;
+
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict part_o,
+                                                                   const float* __restrict part_ml, int32_t n_split,
+                                                                   int32_t n_heads, int32_t hd,
+                                                                   float* __restrict out) {
+    __shared__ float wgt[kMergeMaxSplit];
+    __shared__ float red[kMergeThreads];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    float m = -1e30f;
+    for (int s = tid; s < n_split; s += kMergeThreads)
+        m = fmaxf(m, part_ml[(static_cast<size_t>(s) * n_heads + h) * 2]);
+    red[tid] = m;
+    __syncthreads();
+    for (int o = kMergeThreads / 2; o > 0; o >>= 1) {
+        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+        __syncthreads();
     }
-    const float inv = __fdiv_rn(1.0f, L + 1e-12f);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float acc = 0.0f;
-        for (int s = 0; s < n_split; ++s) {
-            const float m = part_ml[(static_cast<size_t>(s) * n_heads + h) * 2];
-            acc += part_o[(static_cast<size_t>(s) * n_heads + h) * hd + d] * expf(m - M);
-        }
-        out[static_cast<size_t>(h) * hd + d] = acc * inv;
+    const float M = red[0];
+    __syncthreads();
+    float l = 0.0f;
+    for (int s = tid; s < n_split; s += kMergeThreads) {
+        const float* ml = part_ml + (static_cast<size_t>(s) * n_heads + h) * 2;
+        const float e = expf(ml[0] - M);
+        wgt[s] = e;
+        l += ml[1] * e;
+    }
+    red[tid] = l;
+    __syncthreads();
+    for (int o = kMergeThreads / 2; o > 0; o >>= 1) {
+        if (tid < o) red[tid] += red[tid + o];
+        __syncthreads();
+    }
+    const float inv = 1.0f / (red[0] + 1e-12f);
+    __syncthreads();
+    // thread (d, lane group) sums splits lg, lg + groups, ...
+    const int groups = kMergeThreads / hd;  // hd <= 256
+    const int d = tid % hd, lg = tid / hd;
+    float acc = 0.0f;
+    if (lg < groups) {
+#pragma unroll 8
+        for (int s = lg; s < n_split; s += groups)
+            acc += part_o[(static_cast<size_t>(s) * n_heads + h) * hd + d] * wgt[s];
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float t = 0.0f;
+        for (int g = 0; g < groups; ++g) t += red[g * hd + tid];
+        out[static_cast<size_t>(h) * hd + tid] = t * inv;
     }
 }
 
@@ -270,7 +306,18 @@ struct Plan {
     int32_t t0, t1, chunk, n_split;
 };
 
-Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv) {
+size_t lds_bytes(int32_t chunk, int32_t G, int32_t hd);
+
+// LDS per work-group: scores [kHeadBlock][chunk] + wave partials + q + k_new,
+// kept within 64 KB by capping the chunk.
+constexpr size_t kLdsBudget = 64 * 1024;
+
+size_t lds_bytes(int32_t chunk, int32_t G, int32_t hd) {
+    return sizeof(float) * (static_cast<size_t>(kHeadBlock) * chunk + static_cast<size_t>(kWaves) * kHeadBlock * hd +
+                            static_cast<size_t>(G) * hd + hd);
+}
+
+Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv, int32_t G, int32_t hd) {
     Plan pl;
     pl.t0 = sw > 0 ? (pos - sw + 1 > 0 ? pos - sw + 1 : 0) : 0;
     pl.t1 = pos + 1;
@@ -281,6 +328,9 @@ Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv) {
     chunk = ((chunk + 31) / 32) * 32;
     if (chunk < 32) chunk = 32;
     if (chunk > kMaxChunk) chunk = kMaxChunk;
+    while (chunk > 32 && lds_bytes(chunk, G, hd) > kLdsBudget) chunk -= 32;
+    // the merge weighs at most kMergeMaxSplit chunks
+    while ((win + chunk - 1) / chunk > kMergeMaxSplit) chunk += 32;
     pl.chunk = chunk;
     pl.n_split = (win + chunk - 1) / chunk;
     return pl;
@@ -314,13 +364,12 @@ hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* pa
     if (a.rope) p.rope = *a.rope;
     else p.rope.half = 0;
     const int G = a.n_heads / a.n_kv_heads;
-    const size_t lds = sizeof(float) * (static_cast<size_t>(kHeadBlock) * pl.chunk + kWaves * kHeadBlock * HD +
-                                        static_cast<size_t>(G) * HD + HD);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    const size_t lds = lds_bytes(pl.chunk, G, HD);
+    if (lds > kLdsBudget || pl.chunk > kMaxChunk) return hipErrorInvalidValue;  // window too long for one step
     hipLaunchKernelGGL(attn_chunk_kernel<HD>, dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), lds, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(HD < 256 ? HD : 256), 0, stream, part_o, part_ml,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml,
                        pl.n_split, a.n_heads, HD, a.out);
     return hipGetLastError();
 }
@@ -328,8 +377,9 @@ hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* pa
 }  // namespace
 
 size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window) {
-    // upper bound over n_kv: the smallest chunk is 32 tokens
-    const int32_t n_split = (window + 31) / 32;
+    // upper bound over n_kv: chunks of at least 32 tokens, at most kMergeMaxSplit of them
+    int32_t n_split = (window + 31) / 32;
+    if (n_split > kMergeMaxSplit) n_split = kMergeMaxSplit;
     return sizeof(float) * static_cast<size_t>(n_split) * n_heads * (head_dim + 2) + 256;
 }
 
@@ -340,7 +390,7 @@ hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace
     const uintptr_t al = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k_cache) |
                          reinterpret_cast<uintptr_t>(a.v_cache) | reinterpret_cast<uintptr_t>(a.out);
     if (al & 15u) return hipErrorInvalidValue;
-    const Plan pl = make_plan(a.pos, a.sliding_window, a.n_kv_heads);
+    const Plan pl = make_plan(a.pos, a.sliding_window, a.n_kv_heads, a.n_heads / a.n_kv_heads, a.head_dim);
     const size_t need_o = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * a.head_dim;
     const size_t need_ml = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * 2;
     if (need_o + need_ml > workspace_bytes) return hipErrorInvalidValue;

@@ -18,37 +18,40 @@ using namespace dev;
 // one wave per head; values stay in global memory (hd <= a few hundred)
 __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict v, const float* __restrict g,
                                                             int32_t n_heads, int32_t hd, float eps) {
+#pragma clang fp contract(off)
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (h >= n_heads) return;
     float* x = v + static_cast<size_t>(h) * hd;
     const float inv = head_inv_rms(x, hd, eps, lane);
     for (int i = lane; i < hd; i += 64) {
-        const float y = __fmul_rn(x[i], inv);
-        x[i] = g ? __fmul_rn(y, g[i]) : y;
+        const float y = x[i] * inv;
+        x[i] = g ? y * g[i] : y;
     }
 }
 
 // one work-group per row; fp32 per-thread partials, combined in double
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict x, const float* __restrict g,
                                                       int32_t dim, float eps, float* __restrict out) {
+#pragma clang fp contract(off)
     __shared__ double part[4];
     const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
     float* yr = out + static_cast<size_t>(blockIdx.x) * dim;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 256) s = __fadd_rn(s, __fmul_rn(xr[i], xr[i]));
+    for (int i = threadIdx.x; i < dim; i += 256) s += xr[i] * xr[i];
     double d = static_cast<double>(s);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = d;
     __syncthreads();
     const double tot = part[0] + part[1] + part[2] + part[3];
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(static_cast<float>(tot / dim), eps)));
-    for (int i = threadIdx.x; i < dim; i += 256) yr[i] = __fmul_rn(__fmul_rn(xr[i], inv), g[i]);
+    const float inv = 1.0f / sqrtf(static_cast<float>(tot / dim) + eps);
+    for (int i = threadIdx.x; i < dim; i += 256) yr[i] = xr[i] * inv * g[i];
 }
 
 __global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable t, int32_t n_heads,
                             int32_t n_kv, int32_t hd) {
+#pragma clang fp contract(off)
     const int half = hd / 2;
     const int total = (n_heads + n_kv) * half;
     for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
@@ -57,8 +60,8 @@ __global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable 
                                : (k ? k + static_cast<size_t>(h - n_heads) * hd : nullptr);
         if (!v) continue;
         const float x1 = v[i], x2 = v[i + half];
-        v[i] = __fsub_rn(__fmul_rn(x1, t.c[i]), __fmul_rn(x2, t.s[i]));
-        v[i + half] = __fadd_rn(__fmul_rn(x2, t.c[i]), __fmul_rn(x1, t.s[i]));
+        v[i] = x1 * t.c[i] - x2 * t.s[i];
+        v[i + half] = x2 * t.c[i] + x1 * t.s[i];
     }
 }
 

@@ -29,36 +29,197 @@ using namespace dev;
 
 constexpr int kThreads = 256;  // 4 waves per work-group
 
-template <int TYPE>
+// Resident waves the grid is sized for (256 CUs x this many).
+#ifndef GNCX_GEMV_WAVES_PER_CU
+#define GNCX_GEMV_WAVES_PER_CU 16
+#endif
+
+// One wave owns groups of R consecutive rows.  A row's slots are consumed in
+// batches of P passes (64 slots per pass).  The loads of one batch are always
+// in flight while the previous batch is being reduced (double buffering in
+// registers, across batches of a row and across groups), and the first batch
+// is issued before the work-group quantises x into LDS, so the activation
+// pass hides under the first HBM round trip.  With AREG (a row fits in one
+// batch) each lane's activation slice is the same for every row, so it is
+// read from LDS once into registers.
+template <int TYPE, int P, int R, bool AREG>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict w, size_t rbytes,
                                                         const float* __restrict x, int32_t k, int32_t n,
                                                         float* __restrict y) {
+    using S = Slot<TYPE>;
+    using Frag = typename S::Frag;
+    using Act = typename S::Act;
     extern __shared__ __align__(16) uint8_t lds[];
     int8_t* q = reinterpret_cast<int8_t*>(lds);
     ActMeta* meta = reinterpret_cast<ActMeta*>(lds + k);
-    if (TYPE != kBF16) {
-        dev::quantize_block8(x, k / 32, threadIdx.x, kThreads, q, meta);
-        __syncthreads();
-    }
     const int lane = threadIdx.x & 63;
     const int32_t wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int32_t nwaves = gridDim.x * (kThreads / 64);
-    int32_t slots;
-    if (TYPE == kQ4_K || TYPE == kQ6_K) slots = (k / 256) * 4;
-    else if (TYPE == kBF16) slots = (k + 7) / 8;
-    else slots = k / 32;
-    for (int32_t r = wave; r < n; r += nwaves) {
-        const uint8_t* row = w + static_cast<size_t>(r) * rbytes;
-        float acc = 0.0f;
-        for (int32_t s = lane; s < slots; s += 64) {
-            if (TYPE == kQ4_K) acc += slot_q4_k(row, s, q, meta);
-            else if (TYPE == kQ6_K) acc += slot_q6_k(row, s, q, meta);
-            else if (TYPE == kQ4_0) acc += slot_q4_0(row, s, q, meta);
-            else if (TYPE == kQ8_0) acc += slot_q8_0(row, s, q, meta);
-            else acc += slot_bf16(row, s, k, x);
+    const int32_t slots = S::slots(k);
+    const int32_t ngroups = (n + R - 1) / R;
+    const int32_t nbatch = (slots + 64 * P - 1) / (64 * P);
+
+    Frag cur[R][P];
+    Frag nxt[R][P];
+    auto issue = [&](Frag (&f)[R][P], int32_t grp, int32_t b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int32_t row = grp * R + r;
+            if (row < n) {
+                const uint8_t* rp = w + static_cast<size_t>(row) * rbytes;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const int s = lane + 64 * (b * P + p);
+                    if (s < slots) S::load(f[r][p], rp, s);
+                }
+            }
         }
-        acc = wave_sum(acc);
-        if (lane == 0) y[r] = acc;
+    };
+
+    int32_t g = wave;
+    if (g < ngroups) issue(cur, g, 0);
+    if (TYPE != kBF16) {
+        quantize_block8(x, k / 32, threadIdx.x, kThreads, q, meta);
+        __syncthreads();
+    }
+    Act areg[AREG ? P : 1];
+    if constexpr (AREG) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int s = lane + 64 * p;
+            if (s < slots) slot_act<TYPE>(areg[p], s, q, meta, x);
+        }
+    }
+    for (; g < ngroups; g += nwaves) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        for (int32_t b = 0; b < nbatch; ++b) {
+            if (b + 1 < nbatch) issue(nxt, g, b + 1);
+            else if (g + nwaves < ngroups) issue(nxt, g + nwaves, 0);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int32_t row = g * R + r;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const int s = lane + 64 * (b * P + p);
+                    if (s < slots && row < n) {
+                        if constexpr (AREG) {
+                            acc[r] += S::dot(cur[r][p], areg[p], s);
+                        } else {
+                            Act a;
+                            slot_act<TYPE>(a, s, q, meta, x);
+                            acc[r] += S::dot(cur[r][p], a, s);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int p = 0; p < P; ++p) cur[r][p] = nxt[r][p];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = wave_sum(acc[r]);
+            const int32_t row = g * R + r;
+            if (lane == 0 && row < n) y[row] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Band kernel (the main path): one 1024-thread work-group per CU, so x is
+// quantised into LDS only 256 times per call.  Work-group g owns rows
+// g, g + G, g + 2G, ... (G = number of work-groups): at any moment the whole
+// GPU is sweeping one contiguous stretch of the matrix, which keeps HBM pages
+// and channels busy the way a plain streaming read does (a contiguous band
+// per work-group measured 2x slower).  Waves are arranged nwk x nwr: wave
+// (kw, rw) handles slots [64 kw, 64 kw + 64) (one K-slice, its activations
+// kept in registers) of the work-group's local rows rw, rw + nwr, ...  Rows go
+// R at a time in two register buffers used in turn; the first batches' loads
+// are issued before the quantisation.  Each wave's per-row partial goes to LDS
+// and the K-slices are added in a fixed order at the end (deterministic).
+constexpr int kBandThreads = 1024;
+constexpr int kBandWaves = kBandThreads / 64;
+constexpr int32_t kBandGroups = 256;          // one work-group per CU of an MI355X
+constexpr size_t kBandLds = 64 * 1024;
+
+template <int TYPE, int R>
+__global__ __launch_bounds__(kBandThreads) void gemv_band_kernel(const uint8_t* __restrict w, size_t rbytes,
+                                                                 const float* __restrict x, int32_t k,
+                                                                 int32_t n, float* __restrict y,
+                                                                 int32_t rows_per_wg, int32_t nwk, int32_t nwr) {
+    using S = Slot<TYPE>;
+    using Frag = typename S::Frag;
+    using Act = typename S::Act;
+    constexpr int QU = 4;  // x tasks per thread loaded ahead (covers k <= 16384)
+    extern __shared__ __align__(16) uint8_t lds[];
+    const size_t qbytes = TYPE == kBF16 ? 0 : static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta);
+    int8_t* q = reinterpret_cast<int8_t*>(lds);
+    ActMeta* meta = reinterpret_cast<ActMeta*>(lds + k);
+    float* part = reinterpret_cast<float*>(lds + qbytes);  // [rows_per_wg][nwk]
+
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int kw = wv % nwk, rw = wv / nwk;
+    const bool active = rw < nwr;
+    const int32_t slots = S::slots(k);
+    const int s = kw * 64 + lane;
+    const bool has_slot = active && s < slots;
+    const int32_t groups = gridDim.x;
+    // local row li of this work-group is global row li * groups + blockIdx.x
+    const int32_t rows_here = (n - static_cast<int32_t>(blockIdx.x) + groups - 1) / groups;
+    const int32_t per_wave = (rows_per_wg + nwr - 1) / nwr;
+    const int32_t nb = (per_wave + R - 1) / R;
+    auto grow = [&](int32_t li) { return static_cast<size_t>(li) * groups + blockIdx.x; };
+
+    // two weight buffers used in turn (no register copies: a copy would wait
+    // for the loads in flight).  Loads are unconditional -- lanes without a
+    // slot or row read slot 0 of row 0 and their result is masked -- so the
+    // waitcnts before each use only wait for that use's loads.
+    Frag fa[R], fb[R];
+    auto issue = [&](Frag (&f)[R], int32_t b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int32_t li = rw + nwr * (b * R + r);
+            const bool ok = has_slot && li < rows_here;
+            S::load(f[r], ok ? w + grow(li) * rbytes : w, ok ? s : 0);
+        }
+    };
+    auto reduce = [&](const Frag (&f)[R], const Act& a, int32_t b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int32_t li = rw + nwr * (b * R + r);
+            if (active && li < rows_here) {  // wave-uniform
+                float v = has_slot ? S::dot(f[r], a, s) : 0.0f;
+                v = wave_sum(v);
+                if (lane == 0) part[li * nwk + kw] = v;
+            }
+        }
+    };
+
+    // x first (it is waited for first), then every weight batch this wave can hold
+    float4 xv[QU];
+    if (TYPE != kBF16) quant_load<QU>(xv, x, k / 32, threadIdx.x, kBandThreads);
+    issue(fa, 0);
+    if (nb > 1) issue(fb, 1);
+    if (TYPE != kBF16) quant_finish<QU>(xv, x, k / 32, threadIdx.x, kBandThreads, q, meta);
+    __syncthreads();
+    Act a;
+    if (has_slot) slot_act<TYPE>(a, s, q, meta, x);
+    for (int32_t b = 0; b < nb; b += 2) {
+        reduce(fa, a, b);
+        if (b + 2 < nb) issue(fa, b + 2);
+        if (b + 1 < nb) {
+            reduce(fb, a, b + 1);
+            if (b + 3 < nb) issue(fb, b + 3);
+        }
+    }
+    __syncthreads();
+    for (int32_t li = threadIdx.x; li < rows_here; li += kBandThreads) {
+        float acc = 0.0f;
+        for (int j = 0; j < nwk; ++j) acc += part[li * nwk + j];
+        y[grow(li)] = acc;
     }
 }
 
@@ -75,15 +236,54 @@ __global__ __launch_bounds__(kThreads) void act_quant_kernel(const float* __rest
                          meta + static_cast<size_t>(row) * nb + b0);
 }
 
-template <int TYPE>
-hipError_t launch_gemv_t(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y,
-                         hipStream_t stream) {
+template <int TYPE, int P, int R, bool AREG>
+hipError_t launch_shape(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
     const size_t rb = row_bytes(TYPE, k);
     const size_t lds = TYPE == kBF16 ? 0 : static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta);
-    const int32_t rows_per_group = kThreads / 64;
-    int32_t groups = (n + rows_per_group - 1) / rows_per_group;
-    if (groups > 2048) groups = 2048;
-    hipLaunchKernelGGL(gemv_kernel<TYPE>, dim3(groups), dim3(kThreads), lds, stream, w, rb, x, k, n, y);
+    const int32_t ngroups = (n + R - 1) / R;
+    int32_t waves = 256 * GNCX_GEMV_WAVES_PER_CU;
+    if (waves > ngroups) waves = ngroups;
+    const int32_t groups = (waves + kThreads / 64 - 1) / (kThreads / 64);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, P, R, AREG>), dim3(groups), dim3(kThreads), lds, stream, w, rb, x, k, n, y);
+    return hipGetLastError();
+}
+
+// Rows of one pass (<= 64 slots) go two to a wave; longer rows one to a wave,
+// in batches of up to PMAX passes (register budget of the format's slot).
+template <int TYPE, int PMAX>
+hipError_t launch_gemv_t(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+    const int32_t passes = (Slot<TYPE>::slots(k) + 63) / 64;
+    if (passes <= 1) return launch_shape<TYPE, 1, 2, true>(w, x, k, n, y, stream);
+    if (passes == 2) return launch_shape<TYPE, 2, 1, true>(w, x, k, n, y, stream);
+    if (PMAX == 2) return launch_shape<TYPE, 2, 1, false>(w, x, k, n, y, stream);
+    if (passes <= PMAX) return launch_shape<TYPE, (PMAX > 2 ? PMAX : 2), 1, true>(w, x, k, n, y, stream);
+    return launch_shape<TYPE, (PMAX > 2 ? PMAX : 2), 1, false>(w, x, k, n, y, stream);
+}
+
+
+// Band kernel geometry for (type, k, n); false when the shape does not fit it.
+bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t& rows_per_wg, int32_t& groups,
+               int32_t& nwk, int32_t& nwr, size_t& lds) {
+    nwk = (slots + 63) / 64;
+    if (nwk < 1 || nwk > kBandWaves) return false;
+    nwr = kBandWaves / nwk;
+    groups = n < kBandGroups ? n : kBandGroups;
+    rows_per_wg = (n + groups - 1) / groups;
+    groups = (n + rows_per_wg - 1) / rows_per_wg;
+    const size_t qbytes = quantised ? static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta) : 0;
+    lds = qbytes + sizeof(float) * static_cast<size_t>(rows_per_wg) * nwk;
+    return lds <= kBandLds;
+}
+
+template <int TYPE, int R>
+hipError_t launch_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream,
+                       bool& used) {
+    int32_t rpw, groups, nwk, nwr;
+    size_t lds;
+    used = band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, rpw, groups, nwk, nwr, lds);
+    if (!used) return hipSuccess;
+    hipLaunchKernelGGL((gemv_band_kernel<TYPE, R>), dim3(groups), dim3(kBandThreads), lds, stream, w,
+                       row_bytes(TYPE, k), x, k, n, y, rpw, nwk, nwr);
     return hipGetLastError();
 }
 
@@ -95,6 +295,7 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     if (k <= 0 || k > kMaxGemvK) return hipErrorInvalidValue;
     if (type != kBF16 && (k % 32) != 0) return hipErrorInvalidValue;
     if ((type == kQ4_K || type == kQ6_K) && (k % 256) != 0) return hipErrorInvalidValue;
+    if (type == kBF16 && (k % 8) != 0) return hipErrorInvalidValue;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
     if ((xa & 15u) != 0) return hipErrorInvalidValue;
@@ -103,12 +304,23 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     } else if ((wa & 3u) != 0) {
         return hipErrorInvalidValue;
     }
+    bool used = false;
+    hipError_t e = hipSuccess;
     switch (type) {
-    case kQ4_0: return launch_gemv_t<kQ4_0>(w, x, k, n, y, stream);
-    case kQ8_0: return launch_gemv_t<kQ8_0>(w, x, k, n, y, stream);
-    case kQ4_K: return launch_gemv_t<kQ4_K>(w, x, k, n, y, stream);
-    case kQ6_K: return launch_gemv_t<kQ6_K>(w, x, k, n, y, stream);
-    case kBF16: return launch_gemv_t<kBF16>(w, x, k, n, y, stream);
+    case kQ4_0: e = launch_band<kQ4_0, 4>(w, x, k, n, y, stream, used); break;
+    case kQ8_0: e = launch_band<kQ8_0, 2>(w, x, k, n, y, stream, used); break;
+    case kQ4_K: e = launch_band<kQ4_K, 2>(w, x, k, n, y, stream, used); break;
+    case kQ6_K: e = launch_band<kQ6_K, 1>(w, x, k, n, y, stream, used); break;
+    case kBF16: e = launch_band<kBF16, 4>(w, x, k, n, y, stream, used); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (used || e != hipSuccess) return e;
+    switch (type) {
+    case kQ4_0: return launch_gemv_t<kQ4_0, 4>(w, x, k, n, y, stream);
+    case kQ8_0: return launch_gemv_t<kQ8_0, 2>(w, x, k, n, y, stream);
+    case kQ4_K: return launch_gemv_t<kQ4_K, 2>(w, x, k, n, y, stream);
+    case kQ6_K: return launch_gemv_t<kQ6_K, 2>(w, x, k, n, y, stream);
+    case kBF16: return launch_gemv_t<kBF16, 4>(w, x, k, n, y, stream);
     default: return hipErrorInvalidValue;
     }
 }

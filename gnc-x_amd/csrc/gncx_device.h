@@ -77,62 +77,122 @@ __device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, ui
 // 1/rms of one head of hd values, formed as the reference does
 // (cpp:905-926): four fp32 lane sums over i mod 4 for the multiple-of-4
 // prefix, the lanes added in double, a double tail, then
-// 1 / sqrtf((float)(sum/hd) + eps).  No contraction, IEEE div/sqrt.
+// 1 / sqrtf((float)(sum/hd) + eps).  No contraction; IEEE division and
+// sqrtf (correctly rounded here, unlike the 1-ulp __fsqrt_rn).
 // Called by a whole wave; every lane returns the same value.
 __device__ __forceinline__ float head_inv_rms(const float* v, int hd, float eps, int lane) {
+#pragma clang fp contract(off)
     const int full = hd & ~3;
     float part = 0.0f;
     if (lane < 4)
-        for (int i = lane; i < full; i += 4) part = __fadd_rn(part, __fmul_rn(v[i], v[i]));
+        for (int i = lane; i < full; i += 4) part += v[i] * v[i];
     const float p0 = __shfl(part, 0, 64), p1 = __shfl(part, 1, 64);
     const float p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
     double s = static_cast<double>(p0) + static_cast<double>(p1) + static_cast<double>(p2) + static_cast<double>(p3);
     for (int i = full; i < hd; ++i) s += static_cast<double>(v[i]) * static_cast<double>(v[i]);
     const float mean = static_cast<float>(s / static_cast<double>(hd));
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    return 1.0f / sqrtf(mean + eps);
+}
+
+// max / sum over aligned groups of 8 lanes with DPP (no LDS traffic):
+// half-mirror (lane i <-> 7-i), then quad xor 2, then quad xor 1; every lane
+// of the group ends with the group's result.
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false)));
+    return v;
+}
+// sum over aligned groups of 4 lanes (quad xor 2, xor 1)
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false);
+    return v;
 }
 
 // Per-32 Q8 quantisation of x[k] (reference cpp:955-995), done by the whole
-// work-group: 8 lanes per 32-block, 4 values per lane.  Writes int8 values
-// to q[k] and one ActMeta per block.  blockDim.x must be a multiple of 64.
-// Bit-exact with the reference: IEEE 127/amax and amax/127, one rounding for
-// x*inv, round-half-even.
-__device__ __forceinline__ void quantize_block8(const float* __restrict x, int32_t nb, int tid,
-                                                int nthr, int8_t* __restrict q,
-                                                ActMeta* __restrict meta) {
+// work-group: 8 lanes per 32-block, 4 values per lane, up to four tasks per
+// thread with their loads issued together.  Writes int8 values to q[k] and
+// one ActMeta per block.  blockDim.x must be a multiple of 64.  Bit-exact with
+// the reference: IEEE 127/amax and amax/127, one rounding for x*inv,
+// round-half-even.
+__device__ __forceinline__ void quantize_task(const float4 v, int32_t b, int j, int8_t* __restrict q,
+                                              ActMeta* __restrict meta) {
+    const float a = group8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    float d = 0.0f;
+    if (a != 0.0f) {
+        const float inv = 127.0f / a;
+        d = a / 127.0f;
+        q0 = static_cast<int>(rintf(v.x * inv));
+        q1 = static_cast<int>(rintf(v.y * inv));
+        q2 = static_cast<int>(rintf(v.z * inv));
+        q3 = static_cast<int>(rintf(v.w * inv));
+    }
+    const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
+                            ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
+    *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * 32 + j * 4) = packed;
+    // lanes 0-3 of the group: sum of q[0:16]; lanes 4-7: q[16:32]
+    const int s = quad_sum(q0 + q1 + q2 + q3);
+    const int other = __builtin_amdgcn_mov_dpp(s, 0x141, 0xf, 0xf, false);  // lane i <- lane 7-i
+    if (j == 0) {
+        ActMeta m;
+        m.d = d;
+        m.sum_lo16 = s;
+        m.sum_hi16 = other;
+        m.sum = s + other;
+        meta[b] = m;
+    }
+}
+
+// Split form for kernels that must order their loads: quant_load issues the
+// first U tasks' x loads (call it before issuing other global loads, since
+// vmcnt retires loads in order), quant_finish quantises them and any tasks
+// beyond U * nthr.
+// Loads are unconditional (tasks past the end re-read the last one), so the
+// number of loads in flight is static and the waitcnt for x does not wait for
+// the weight loads issued after it.
+template <int U>
+__device__ __forceinline__ void quant_load(float4 (&v)[U], const float* __restrict x, int32_t nb, int tid,
+                                           int nthr) {
     const int32_t ntask = nb * 8;
-    for (int32_t task = tid; task < ntask; task += nthr) {
-        const int32_t b = task >> 3;
-        const int j = task & 7;
-        const float4 v = *reinterpret_cast<const float4*>(x + static_cast<size_t>(b) * 32 + j * 4);
-        float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        a = fmaxf(a, __shfl_xor(a, 1, 8));
-        a = fmaxf(a, __shfl_xor(a, 2, 8));
-        a = fmaxf(a, __shfl_xor(a, 4, 8));
-        int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-        float d = 0.0f;
-        if (a != 0.0f) {
-            const float inv = __fdiv_rn(127.0f, a);
-            d = __fdiv_rn(a, 127.0f);
-            q0 = static_cast<int>(rintf(v.x * inv));
-            q1 = static_cast<int>(rintf(v.y * inv));
-            q2 = static_cast<int>(rintf(v.z * inv));
-            q3 = static_cast<int>(rintf(v.w * inv));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int32_t t = min(tid + u * nthr, ntask - 1);
+        v[u] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * 4);
+    }
+}
+
+template <int U>
+__device__ __forceinline__ void quant_finish(const float4 (&v)[U], const float* __restrict x, int32_t nb, int tid,
+                                             int nthr, int8_t* __restrict q, ActMeta* __restrict meta) {
+    const int32_t ntask = nb * 8;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int32_t t = tid + u * nthr;
+        if (t < ntask) quantize_task(v[u], t >> 3, t & 7, q, meta);
+    }
+    for (int32_t t = tid + U * nthr; t < ntask; t += nthr) {
+        const float4 w = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * 4);
+        quantize_task(w, t >> 3, t & 7, q, meta);
+    }
+}
+
+__device__ __forceinline__ void quantize_block8(const float* __restrict x, int32_t nb, int tid, int nthr,
+                                                int8_t* __restrict q, ActMeta* __restrict meta) {
+    constexpr int U = 4;
+    const int32_t ntask = nb * 8;
+    for (int32_t base = tid; base < ntask; base += U * nthr) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int32_t t = base + u * nthr;
+            if (t < ntask) v[u] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * 4);
         }
-        const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
-                                ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
-        *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * 32 + j * 4) = packed;
-        int s = q0 + q1 + q2 + q3;
-        s += __shfl_xor(s, 1, 8);
-        s += __shfl_xor(s, 2, 8);  // lanes 0-3: sum of q[0:16]; lanes 4-7: q[16:32]
-        const int other = __shfl_xor(s, 4, 8);
-        if (j == 0) {
-            ActMeta m;
-            m.d = d;
-            m.sum_lo16 = s;
-            m.sum_hi16 = other;
-            m.sum = s + other;
-            meta[b] = m;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int32_t t = base + u * nthr;
+            if (t < ntask) quantize_task(v[u], t >> 3, t & 7, q, meta);
         }
     }
 }

@@ -1,13 +1,22 @@
 // gncx_slots.h -- per-lane block dots shared by the GEMV and the small-batch
 // matbatch kernels.  A "slot" maps one lane to a fixed byte range of one
-// block of a weight row; each function returns that slot's fp32 share of the
-// row sum, using Q8 activations (int8 values q + ActMeta per 32-block):
-//   Q4_K  4 slots per 144 B super-block (16 B header + 32 B of nibbles each),
-//         reference dot cpp:1127-1205
-//   Q6_K  4 slots per 210 B super-block, (128-half, 16-group) each,
-//         reference dot cpp:1211-1321
-//   Q4_0  1 slot per 18 B block (cpp:1362-1382), Q8_0 1 per 34 B block
-//         (cpp:1413-1431), BF16 16 bytes of weights with fp32 x (cpp:1432-1461)
+// block of a weight row.  Each format has
+//   Frag                 the raw weight registers one slot needs from HBM,
+//   load(f, row, s)      issues those loads (plain loads: non-temporal ones
+//                        measured up to 2.3x slower on these 2-aligned,
+//                        partly overlapping fields and fetched 1.5x the bytes),
+//   Act                  the Q8 activation registers the slot multiplies,
+//   load_act(a, s, ...)  reads them (LDS q + ActMeta, or fp32 x for BF16),
+//   dot(f, a, s)         the slot's fp32 share of the row sum,
+// so kernels can put several slots' weight loads in flight before touching
+// any, and keep a slot's activations in registers across rows.
+//   Q4_K  4 slots per 144 B super-block: 16 B header + 32 B of nibbles each
+//         (reference dot cpp:1127-1205)
+//   Q6_K  4 slots per 210 B super-block, one (128-half, 16-group) each
+//         (reference dot cpp:1211-1321)
+//   Q4_0  1 slot per 18 B block (cpp:1362-1382)
+//   Q8_0  1 slot per 34 B block (cpp:1413-1431)
+//   BF16  8 weights (16 B) per slot, fp32 x (cpp:1432-1461)
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -16,141 +25,294 @@
 namespace gncx {
 namespace dev {
 
-__device__ __forceinline__ float slot_q4_k(const uint8_t* __restrict row, int s,
-                                           const int8_t* __restrict q, const ActMeta* __restrict meta) {
-    const int sb = s >> 2, c = s & 3;
-    const uint8_t* blk = row + static_cast<size_t>(sb) * 144;
-    const uint4 hdr = ld16_aligned(blk);
-    const uint4 w0 = ld16_aligned(blk + 16 + 32 * c);
-    const uint4 w1 = ld16_aligned(blk + 32 + 32 * c);
-    const int ab = sb * 8 + 2 * c;
-    const uint4* xq = reinterpret_cast<const uint4*>(q + static_cast<size_t>(ab) * 32);
-    const uint4 xl0 = xq[0], xl1 = xq[1], xh0 = xq[2], xh1 = xq[3];
-    const ActMeta ml = meta[ab], mh = meta[ab + 1];
-    const uint32_t M = 0x0f0f0f0fu;
-    int dl = 0, dh = 0;
-    dl = sdot4(w0.x & M, xl0.x, dl); dh = sdot4((w0.x >> 4) & M, xh0.x, dh);
-    dl = sdot4(w0.y & M, xl0.y, dl); dh = sdot4((w0.y >> 4) & M, xh0.y, dh);
-    dl = sdot4(w0.z & M, xl0.z, dl); dh = sdot4((w0.z >> 4) & M, xh0.z, dh);
-    dl = sdot4(w0.w & M, xl0.w, dl); dh = sdot4((w0.w >> 4) & M, xh0.w, dh);
-    dl = sdot4(w1.x & M, xl1.x, dl); dh = sdot4((w1.x >> 4) & M, xh1.x, dh);
-    dl = sdot4(w1.y & M, xl1.y, dl); dh = sdot4((w1.y >> 4) & M, xh1.y, dh);
-    dl = sdot4(w1.z & M, xl1.z, dl); dh = sdot4((w1.z >> 4) & M, xh1.z, dh);
-    dl = sdot4(w1.w & M, xl1.w, dl); dh = sdot4((w1.w >> 4) & M, xh1.w, dh);
-    int s1, m1, s2, m2;
-    k4_scale_min(2 * c, hdr.y, hdr.z, hdr.w, s1, m1);
-    k4_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, s2, m2);
-    const float d = half_bits_to_float(hdr.x & 0xffffu);
-    const float dmin = half_bits_to_float(hdr.x >> 16);
-    const float d1 = d * static_cast<float>(s1), dm1 = dmin * static_cast<float>(m1);
-    const float d2 = d * static_cast<float>(s2), dm2 = dmin * static_cast<float>(m2);
-    return ml.d * (d1 * static_cast<float>(dl) - dm1 * static_cast<float>(ml.sum)) +
-           mh.d * (d2 * static_cast<float>(dh) - dm2 * static_cast<float>(mh.sum));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 w_ld16(const uint8_t* p) {  // 16-byte aligned
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4a4 w_ld16_a4(const uint8_t* p) {  // 4-byte aligned
+    return *reinterpret_cast<const u32x4a4*>(p);
+}
+__device__ __forceinline__ u32x2a4 w_ld8_a4(const uint8_t* p) {
+    return *reinterpret_cast<const u32x2a4*>(p);
+}
+__device__ __forceinline__ uint32_t w_ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
 }
 
-__device__ __forceinline__ float slot_q6_k(const uint8_t* __restrict row, int s,
-                                           const int8_t* __restrict q, const ActMeta* __restrict meta) {
-    const int sb = s >> 2, n = (s >> 1) & 1, g = s & 1;
-    const uint8_t* blk = row + static_cast<size_t>(sb) * 210;
-    const uint4 pa = ld16_a2(blk + 64 * n + 16 * g);
-    const uint4 pb = ld16_a2(blk + 64 * n + 32 + 16 * g);
-    const uint4 ph = ld16_a2(blk + 128 + 32 * n + 16 * g);
-    // scales sc[8n .. 8n+7] (2-aligned 8 bytes)
-    const uint8_t* ps = blk + 192 + 8 * n;
-    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ps) & 3u);
-    const u32x2a4 sv = *reinterpret_cast<const u32x2a4*>(ps - sh);
-    const uint32_t st = ld_u16(ps + 6);
-    const uint32_t sc_lo = __builtin_amdgcn_alignbyte(sv.y, sv.x, sh);  // sc[8n+0..3]
-    const uint32_t sc_hi = __builtin_amdgcn_alignbyte(st, sv.y, sh);    // sc[8n+4..7]
-    const float d = half_bits_to_float(ld_u16(blk + 208));
+// raw 16-byte field at a 2-aligned address p: the dword-aligned dwordx4 at
+// p - sh and the 2 bytes at p + 14 (see ld16_a2); sh = p mod 4 is kept by
+// the caller (all fields of one block share it) and the field is realigned
+// only when used
+struct Raw16 {
+    u32x4a4 v;
+    uint32_t tail;
+};
 
-    const int ab = sb * 8 + 4 * n;
-    const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
-    const uint32_t wa[4] = {pa.x, pa.y, pa.z, pa.w};
-    const uint32_t wb[4] = {pb.x, pb.y, pb.z, pb.w};
-    const uint32_t wh[4] = {ph.x, ph.y, ph.z, ph.w};
-    int dot[4] = {0, 0, 0, 0};
+__device__ __forceinline__ uint32_t addr_sh(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+}
+
+__device__ __forceinline__ void raw16_load(Raw16& r, const uint8_t* p, uint32_t sh) {
+    r.v = w_ld16_a4(p - sh);
+    r.tail = w_ld_u16(p + 14);
+}
+
+__device__ __forceinline__ uint4 raw16_get(const Raw16& r, uint32_t sh) {
+    uint4 o;
+    o.x = __builtin_amdgcn_alignbyte(r.v.y, r.v.x, sh);
+    o.y = __builtin_amdgcn_alignbyte(r.v.z, r.v.y, sh);
+    o.z = __builtin_amdgcn_alignbyte(r.v.w, r.v.z, sh);
+    o.w = __builtin_amdgcn_alignbyte(r.tail, r.v.w, sh);
+    return o;
+}
+
+__device__ __forceinline__ uint4 lds16(const int8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <int TYPE>
+struct Slot;
+
+// ---------------------------------------------------------------- Q4_K
+template <>
+struct Slot<kQ4_K> {
+    struct Frag {
+        u32x4 hdr, w0, w1;
+    };
+    struct Act {
+        uint4 xl0, xl1, xh0, xh1;  // q of sub-blocks 2c (low nibbles) and 2c+1 (high)
+        float dl, dh;
+        int sl, sh;
+    };
+    static constexpr int32_t slots(int32_t k) { return (k / 256) * 4; }
+    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
+        const int sb = s >> 2, c = s & 3;
+        const uint8_t* blk = row + static_cast<size_t>(sb) * 144;
+        f.hdr = w_ld16(blk);
+        f.w0 = w_ld16(blk + 16 + 32 * c);
+        f.w1 = w_ld16(blk + 32 + 32 * c);
+    }
+    __device__ static __forceinline__ void load_act(Act& a, int s, const int8_t* __restrict q,
+                                                    const ActMeta* __restrict meta) {
+        const int ab = (s >> 2) * 8 + 2 * (s & 3);
+        const int8_t* xq = q + static_cast<size_t>(ab) * 32;
+        a.xl0 = lds16(xq);
+        a.xl1 = lds16(xq + 16);
+        a.xh0 = lds16(xq + 32);
+        a.xh1 = lds16(xq + 48);
+        const ActMeta ml = meta[ab], mh = meta[ab + 1];
+        a.dl = ml.d;
+        a.dh = mh.d;
+        a.sl = ml.sum;
+        a.sh = mh.sum;
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int s) {
+        const int c = s & 3;
+        const uint32_t M = 0x0f0f0f0fu;
+        int dl = 0, dh = 0;
+        dl = sdot4(f.w0.x & M, a.xl0.x, dl); dh = sdot4((f.w0.x >> 4) & M, a.xh0.x, dh);
+        dl = sdot4(f.w0.y & M, a.xl0.y, dl); dh = sdot4((f.w0.y >> 4) & M, a.xh0.y, dh);
+        dl = sdot4(f.w0.z & M, a.xl0.z, dl); dh = sdot4((f.w0.z >> 4) & M, a.xh0.z, dh);
+        dl = sdot4(f.w0.w & M, a.xl0.w, dl); dh = sdot4((f.w0.w >> 4) & M, a.xh0.w, dh);
+        dl = sdot4(f.w1.x & M, a.xl1.x, dl); dh = sdot4((f.w1.x >> 4) & M, a.xh1.x, dh);
+        dl = sdot4(f.w1.y & M, a.xl1.y, dl); dh = sdot4((f.w1.y >> 4) & M, a.xh1.y, dh);
+        dl = sdot4(f.w1.z & M, a.xl1.z, dl); dh = sdot4((f.w1.z >> 4) & M, a.xh1.z, dh);
+        dl = sdot4(f.w1.w & M, a.xl1.w, dl); dh = sdot4((f.w1.w >> 4) & M, a.xh1.w, dh);
+        int s1, m1, s2, m2;
+        k4_scale_min(2 * c, f.hdr.y, f.hdr.z, f.hdr.w, s1, m1);
+        k4_scale_min(2 * c + 1, f.hdr.y, f.hdr.z, f.hdr.w, s2, m2);
+        const float d = half_bits_to_float(f.hdr.x & 0xffffu);
+        const float dmin = half_bits_to_float(f.hdr.x >> 16);
+        const float d1 = d * static_cast<float>(s1), dm1 = dmin * static_cast<float>(m1);
+        const float d2 = d * static_cast<float>(s2), dm2 = dmin * static_cast<float>(m2);
+        return a.dl * (d1 * static_cast<float>(dl) - dm1 * static_cast<float>(a.sl)) +
+               a.dh * (d2 * static_cast<float>(dh) - dm2 * static_cast<float>(a.sh));
+    }
+};
+
+// ---------------------------------------------------------------- Q6_K
+template <>
+struct Slot<kQ6_K> {
+    struct Frag {
+        Raw16 pa, pb, ph;
+        u32x2a4 sv;      // scales sc[8n..8n+7], dword-aligned below
+        uint32_t st;     // their trailing 2 bytes
+        uint32_t sh;     // block address mod 4 (every field offset is a multiple of 4)
+        uint32_t d;      // fp16 bits
+    };
+    struct Act {
+        uint4 x[4];   // bytes [16g, 16g+16) of the four 32-blocks of this 128-half
+        float d[4];
+        int s[4];     // sum of those 16 q
+    };
+    static constexpr int32_t slots(int32_t k) { return (k / 256) * 4; }
+    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
+        const int sb = s >> 2, n = (s >> 1) & 1, g = s & 1;
+        const uint8_t* blk = row + static_cast<size_t>(sb) * 210;
+        f.sh = addr_sh(blk);
+        raw16_load(f.pa, blk + 64 * n + 16 * g, f.sh);
+        raw16_load(f.pb, blk + 64 * n + 32 + 16 * g, f.sh);
+        raw16_load(f.ph, blk + 128 + 32 * n + 16 * g, f.sh);
+        const uint8_t* ps = blk + 192 + 8 * n;
+        f.sv = w_ld8_a4(ps - f.sh);
+        f.st = w_ld_u16(ps + 6);
+        f.d = w_ld_u16(blk + 208);
+    }
+    __device__ static __forceinline__ void load_act(Act& a, int s, const int8_t* __restrict q,
+                                                    const ActMeta* __restrict meta) {
+        const int sb = s >> 2, n = (s >> 1) & 1, g = s & 1;
+        const int ab = sb * 8 + 4 * n;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(q + static_cast<size_t>(ab + k) * 32 + 16 * g);
-        const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t v;
-            if (k == 0) v = (wa[i] & M4) | ((wh[i] & M2) << 4);
-            else if (k == 1) v = (wb[i] & M4) | (((wh[i] >> 2) & M2) << 4);
-            else if (k == 2) v = ((wa[i] >> 4) & M4) | (((wh[i] >> 4) & M2) << 4);
-            else v = ((wb[i] >> 4) & M4) | (((wh[i] >> 6) & M2) << 4);
-            dot[k] = sdot4(v, xs[i], dot[k]);
+        for (int k = 0; k < 4; ++k) {
+            a.x[k] = lds16(q + static_cast<size_t>(ab + k) * 32 + 16 * g);
+            const ActMeta m = meta[ab + k];
+            a.d[k] = m.d;
+            a.s[k] = g == 0 ? m.sum_lo16 : m.sum_hi16;
         }
     }
-    float p = 0.0f;
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int s) {
+        const int g = s & 1;
+        const uint4 pa = raw16_get(f.pa, f.sh), pb = raw16_get(f.pb, f.sh), ph = raw16_get(f.ph, f.sh);
+        const uint32_t sc_lo = __builtin_amdgcn_alignbyte(f.sv.y, f.sv.x, f.sh);  // sc[8n+0..3]
+        const uint32_t sc_hi = __builtin_amdgcn_alignbyte(f.st, f.sv.y, f.sh);    // sc[8n+4..7]
+        const uint32_t M4 = 0x0f0f0f0fu, M2 = 0x03030303u;
+        const uint32_t wa[4] = {pa.x, pa.y, pa.z, pa.w};
+        const uint32_t wb[4] = {pb.x, pb.y, pb.z, pb.w};
+        const uint32_t wh[4] = {ph.x, ph.y, ph.z, ph.w};
+        float p = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const ActMeta m = meta[ab + k];
-        const int sidx = g + 2 * k;  // 0..7 within sc[8n..8n+7]
-        const uint32_t word = sidx < 4 ? sc_lo : sc_hi;
-        const int scv = static_cast<int>(static_cast<int8_t>(byte_of(word, sidx & 3)));
-        const int ssum = g == 0 ? m.sum_lo16 : m.sum_hi16;
-        p += static_cast<float>(dot[k] - 32 * ssum) * (m.d * static_cast<float>(scv));
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t xs[4] = {a.x[k].x, a.x[k].y, a.x[k].z, a.x[k].w};
+            int dot = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t v;
+                if (k == 0) v = (wa[i] & M4) | ((wh[i] & M2) << 4);
+                else if (k == 1) v = (wb[i] & M4) | (((wh[i] >> 2) & M2) << 4);
+                else if (k == 2) v = ((wa[i] >> 4) & M4) | (((wh[i] >> 4) & M2) << 4);
+                else v = ((wb[i] >> 4) & M4) | (((wh[i] >> 6) & M2) << 4);
+                dot = sdot4(v, xs[i], dot);
+            }
+            const int sidx = g + 2 * k;  // 0..7 within sc[8n..8n+7]
+            const uint32_t word = sidx < 4 ? sc_lo : sc_hi;
+            const int scv = static_cast<int>(static_cast<int8_t>(byte_of(word, sidx & 3)));
+            p += static_cast<float>(dot - 32 * a.s[k]) * (a.d[k] * static_cast<float>(scv));
+        }
+        return half_bits_to_float(f.d) * p;
     }
-    return d * p;
-}
+};
 
-__device__ __forceinline__ float slot_q4_0(const uint8_t* __restrict row, int b,
-                                           const int8_t* __restrict q, const ActMeta* __restrict meta) {
-    const ActMeta m = meta[b];
-    const uint8_t* blk = row + static_cast<size_t>(b) * 18;
-    const float wd = half_bits_to_float(ld_u16(blk));
-    const uint4 qs = ld16_a2(blk + 2);
-    const uint4* xq = reinterpret_cast<const uint4*>(q + static_cast<size_t>(b) * 32);
-    const uint4 xl = xq[0], xh = xq[1];
-    const uint32_t M = 0x0f0f0f0fu;
-    int dot = 0;
-    dot = sdot4(qs.x & M, xl.x, dot); dot = sdot4((qs.x >> 4) & M, xh.x, dot);
-    dot = sdot4(qs.y & M, xl.y, dot); dot = sdot4((qs.y >> 4) & M, xh.y, dot);
-    dot = sdot4(qs.z & M, xl.z, dot); dot = sdot4((qs.z >> 4) & M, xh.z, dot);
-    dot = sdot4(qs.w & M, xl.w, dot); dot = sdot4((qs.w >> 4) & M, xh.w, dot);
-    const int folded = dot - 8 * m.sum;
-    // cpp:1371: blocks with a zero activation scale are skipped
-    return m.d != 0.0f ? static_cast<float>(folded) * (wd * m.d) : 0.0f;
-}
+// ---------------------------------------------------------------- Q4_0
+template <>
+struct Slot<kQ4_0> {
+    struct Frag {
+        uint32_t d, sh;
+        Raw16 qs;
+    };
+    struct Act {
+        uint4 xl, xh;
+        float d;
+        int sum;
+    };
+    static constexpr int32_t slots(int32_t k) { return k / 32; }
+    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int b) {
+        const uint8_t* blk = row + static_cast<size_t>(b) * 18;
+        f.d = w_ld_u16(blk);
+        f.sh = addr_sh(blk + 2);
+        raw16_load(f.qs, blk + 2, f.sh);
+    }
+    __device__ static __forceinline__ void load_act(Act& a, int b, const int8_t* __restrict q,
+                                                    const ActMeta* __restrict meta) {
+        a.xl = lds16(q + static_cast<size_t>(b) * 32);
+        a.xh = lds16(q + static_cast<size_t>(b) * 32 + 16);
+        const ActMeta m = meta[b];
+        a.d = m.d;
+        a.sum = m.sum;
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int) {
+        const uint4 qs = raw16_get(f.qs, f.sh);
+        const uint32_t M = 0x0f0f0f0fu;
+        int dot = 0;
+        dot = sdot4(qs.x & M, a.xl.x, dot); dot = sdot4((qs.x >> 4) & M, a.xh.x, dot);
+        dot = sdot4(qs.y & M, a.xl.y, dot); dot = sdot4((qs.y >> 4) & M, a.xh.y, dot);
+        dot = sdot4(qs.z & M, a.xl.z, dot); dot = sdot4((qs.z >> 4) & M, a.xh.z, dot);
+        dot = sdot4(qs.w & M, a.xl.w, dot); dot = sdot4((qs.w >> 4) & M, a.xh.w, dot);
+        const int folded = dot - 8 * a.sum;
+        // cpp:1371: blocks with a zero activation scale are skipped
+        return a.d != 0.0f ? static_cast<float>(folded) * (half_bits_to_float(f.d) * a.d) : 0.0f;
+    }
+};
 
-__device__ __forceinline__ float slot_q8_0(const uint8_t* __restrict row, int b,
-                                           const int8_t* __restrict q, const ActMeta* __restrict meta) {
-    const ActMeta m = meta[b];
-    const uint8_t* blk = row + static_cast<size_t>(b) * 34;
-    const float wd = half_bits_to_float(ld_u16(blk));
-    const uint4 w0 = ld16_a2(blk + 2);
-    const uint4 w1 = ld16_a2(blk + 18);
-    const uint4* xq = reinterpret_cast<const uint4*>(q + static_cast<size_t>(b) * 32);
-    const uint4 x0 = xq[0], x1 = xq[1];
-    int dot = 0;
-    dot = sdot4(w0.x, x0.x, dot); dot = sdot4(w0.y, x0.y, dot);
-    dot = sdot4(w0.z, x0.z, dot); dot = sdot4(w0.w, x0.w, dot);
-    dot = sdot4(w1.x, x1.x, dot); dot = sdot4(w1.y, x1.y, dot);
-    dot = sdot4(w1.z, x1.z, dot); dot = sdot4(w1.w, x1.w, dot);
-    return static_cast<float>(dot) * (wd * m.d);
-}
+// ---------------------------------------------------------------- Q8_0
+template <>
+struct Slot<kQ8_0> {
+    struct Frag {
+        uint32_t d, sh;
+        Raw16 lo, hi;
+    };
+    struct Act {
+        uint4 x0, x1;
+        float d;
+    };
+    static constexpr int32_t slots(int32_t k) { return k / 32; }
+    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int b) {
+        const uint8_t* blk = row + static_cast<size_t>(b) * 34;
+        f.d = w_ld_u16(blk);
+        f.sh = addr_sh(blk + 2);
+        raw16_load(f.lo, blk + 2, f.sh);
+        raw16_load(f.hi, blk + 18, f.sh);
+    }
+    __device__ static __forceinline__ void load_act(Act& a, int b, const int8_t* __restrict q,
+                                                    const ActMeta* __restrict meta) {
+        a.x0 = lds16(q + static_cast<size_t>(b) * 32);
+        a.x1 = lds16(q + static_cast<size_t>(b) * 32 + 16);
+        a.d = meta[b].d;
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int) {
+        const uint4 w0 = raw16_get(f.lo, f.sh), w1 = raw16_get(f.hi, f.sh);
+        int dot = 0;
+        dot = sdot4(w0.x, a.x0.x, dot); dot = sdot4(w0.y, a.x0.y, dot);
+        dot = sdot4(w0.z, a.x0.z, dot); dot = sdot4(w0.w, a.x0.w, dot);
+        dot = sdot4(w1.x, a.x1.x, dot); dot = sdot4(w1.y, a.x1.y, dot);
+        dot = sdot4(w1.z, a.x1.z, dot); dot = sdot4(w1.w, a.x1.w, dot);
+        return static_cast<float>(dot) * (half_bits_to_float(f.d) * a.d);
+    }
+};
 
+// ---------------------------------------------------------------- BF16
 __device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
 
-__device__ __forceinline__ float slot_bf16(const uint8_t* __restrict row, int s, int32_t k,
-                                           const float* __restrict x) {
-    const int32_t e0 = s * 8;
-    float acc = 0.0f;
-    if (e0 + 8 <= k) {
-        const uint4 w = ld16_aligned(row + static_cast<size_t>(e0) * 2);
-        const float4 xa = *reinterpret_cast<const float4*>(x + e0);
-        const float4 xb = *reinterpret_cast<const float4*>(x + e0 + 4);
-        acc = bf16_bits(w.x & 0xffffu) * xa.x + bf16_bits(w.x >> 16) * xa.y +
-              bf16_bits(w.y & 0xffffu) * xa.z + bf16_bits(w.y >> 16) * xa.w +
-              bf16_bits(w.z & 0xffffu) * xb.x + bf16_bits(w.z >> 16) * xb.y +
-              bf16_bits(w.w & 0xffffu) * xb.z + bf16_bits(w.w >> 16) * xb.w;
-    } else {
-        for (int32_t e = e0; e < k; ++e) acc += bf16_bits(ld_u16(row + static_cast<size_t>(e) * 2)) * x[e];
+template <>
+struct Slot<kBF16> {
+    struct Frag {
+        u32x4 w;
+    };
+    struct Act {
+        float4 a, b;
+    };
+    static constexpr int32_t slots(int32_t k) { return k / 8; }  // launchers require k % 8 == 0
+    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
+        f.w = w_ld16(row + static_cast<size_t>(s) * 16);
     }
-    return acc;
+    // BF16 multiplies the fp32 vector itself (global memory)
+    __device__ static __forceinline__ void load_act_x(Act& a, int s, const float* __restrict x) {
+        a.a = *reinterpret_cast<const float4*>(x + 8 * s);
+        a.b = *reinterpret_cast<const float4*>(x + 8 * s + 4);
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& x, int) {
+        return bf16_bits(f.w.x & 0xffffu) * x.a.x + bf16_bits(f.w.x >> 16) * x.a.y +
+               bf16_bits(f.w.y & 0xffffu) * x.a.z + bf16_bits(f.w.y >> 16) * x.a.w +
+               bf16_bits(f.w.z & 0xffffu) * x.b.x + bf16_bits(f.w.z >> 16) * x.b.y +
+               bf16_bits(f.w.w & 0xffffu) * x.b.z + bf16_bits(f.w.w >> 16) * x.b.w;
+    }
+};
+
+// activations of slot s from the quantised vector (LDS or global) or, for
+// BF16, from the fp32 vector
+template <int TYPE>
+__device__ __forceinline__ void slot_act(typename Slot<TYPE>::Act& a, int s, const int8_t* __restrict q,
+                                         const ActMeta* __restrict meta, const float* __restrict x) {
+    if constexpr (TYPE == kBF16) Slot<TYPE>::load_act_x(a, s, x);
+    else Slot<TYPE>::load_act(a, s, q, meta);
 }
 
 }  // namespace dev

@@ -34,17 +34,15 @@ __global__ __launch_bounds__(kThreads) void matbatch_rowtok_kernel(const uint8_t
     const uint8_t* row = w + static_cast<size_t>(r) * rbytes;
     const int8_t* qt = q + static_cast<size_t>(t) * k;
     const ActMeta* mt = meta + static_cast<size_t>(t) * (k / 32);
-    int32_t slots;
-    if (TYPE == kQ4_K || TYPE == kQ6_K) slots = (k / 256) * 4;
-    else if (TYPE == kBF16) slots = (k + 7) / 8;
-    else slots = k / 32;
+    using S = Slot<TYPE>;
+    const int32_t slots = S::slots(k);
     float acc = 0.0f;
     for (int32_t s = lane; s < slots; s += 64) {
-        if (TYPE == kQ4_K) acc += slot_q4_k(row, s, qt, mt);
-        else if (TYPE == kQ6_K) acc += slot_q6_k(row, s, qt, mt);
-        else if (TYPE == kQ4_0) acc += slot_q4_0(row, s, qt, mt);
-        else if (TYPE == kQ8_0) acc += slot_q8_0(row, s, qt, mt);
-        else acc += slot_bf16(row, s, k, x + static_cast<size_t>(t) * k);
+        typename S::Frag f;
+        typename S::Act a;
+        S::load(f, row, s);
+        slot_act<TYPE>(a, s, qt, mt, x + static_cast<size_t>(t) * k);
+        acc += S::dot(f, a, s);
     }
     acc = wave_sum(acc);
     if (lane == 0) y[static_cast<size_t>(t) * n + r] = acc;

@@ -102,13 +102,16 @@ def test_matvec_lm_head_shape(lib, oracle):
 @pytest.mark.parametrize("name,t", [("q4_0", Q4_0), ("q8_0", Q8_0), ("q4_k", Q4_K), ("q6_k", Q6_K), ("bf16", BF16)])
 def test_matvec_matbatch_vs_reference_vectors(lib, golden, name, t):
     k, n, b = int(golden["mv_k"]), int(golden["mv_n"]), int(golden["mv_b"])
+    # arrays whose address is passed must stay referenced until the call returns
     w = golden[f"{name}_w"].copy()
+    x = golden[f"{name}_x"].copy()
+    xb = golden[f"{name}_xb"].copy()
     y = np.zeros(n, np.float32)
-    lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(golden[f"{name}_x"].copy()), None, k, n, ptr(y), None)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(x), None, k, n, ptr(y), None)
     gncx.check(lib)
     assert rel_l2(y, golden[f"{name}_y"]) < TOL
     yb = np.zeros((b, n), np.float32)
-    lib.gncx_xfold_universal_matbatch(ptr(w), 0, t, ptr(golden[f"{name}_xb"].copy()), b, k, n, ptr(yb), None)
+    lib.gncx_xfold_universal_matbatch(ptr(w), 0, t, ptr(xb), b, k, n, ptr(yb), None)
     gncx.check(lib)
     assert rel_l2(yb, golden[f"{name}_yb"]) < TOL
 
