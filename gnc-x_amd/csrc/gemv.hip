@@ -140,9 +140,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 // R at a time in two register buffers used in turn; the first batches' loads
 // are issued before the quantisation.  Each wave's per-row partial goes to LDS
 // and the K-slices are added in a fixed order at the end (deterministic).
-constexpr int kBandThreads = 1024;
+#ifndef GNCX_BAND_THREADS
+#define GNCX_BAND_THREADS 1024
+#endif
+#ifndef GNCX_BAND_GROUPS
+#define GNCX_BAND_GROUPS 256
+#endif
+#ifndef GNCX_Q4K_ROWS
+#define GNCX_Q4K_ROWS 2
+#endif
+constexpr int kBandThreads = GNCX_BAND_THREADS;
 constexpr int kBandWaves = kBandThreads / 64;
-constexpr int32_t kBandGroups = 256;          // one work-group per CU of an MI355X
+constexpr int32_t kBandGroups = GNCX_BAND_GROUPS;  // one work-group per CU of an MI355X
 constexpr size_t kBandLds = 64 * 1024;
 
 template <int TYPE, int R>
@@ -192,8 +201,8 @@ __global__ __launch_bounds__(kBandThreads) void gemv_band_kernel(const uint8_t* 
             const int32_t li = rw + nwr * (b * R + r);
             if (active && li < rows_here) {  // wave-uniform
                 float v = has_slot ? S::dot(f[r], a, s) : 0.0f;
-                v = wave_sum(v);
-                if (lane == 0) part[li * nwk + kw] = v;
+                v = wave_sum_lane63(v);
+                if (lane == 63) part[li * nwk + kw] = v;
             }
         }
     };
@@ -309,7 +318,7 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     switch (type) {
     case kQ4_0: e = launch_band<kQ4_0, 4>(w, x, k, n, y, stream, used); break;
     case kQ8_0: e = launch_band<kQ8_0, 2>(w, x, k, n, y, stream, used); break;
-    case kQ4_K: e = launch_band<kQ4_K, 2>(w, x, k, n, y, stream, used); break;
+    case kQ4_K: e = launch_band<kQ4_K, GNCX_Q4K_ROWS>(w, x, k, n, y, stream, used); break;
     case kQ6_K: e = launch_band<kQ6_K, 1>(w, x, k, n, y, stream, used); break;
     case kBF16: e = launch_band<kBF16, 4>(w, x, k, n, y, stream, used); break;
     default: return hipErrorInvalidValue;

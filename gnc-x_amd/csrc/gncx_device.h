@@ -53,10 +53,31 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// v + (v of another lane) through DPP; lanes the masks leave out add 0
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, BANK_MASK, BOUND_ZERO);
+    return v + __builtin_bit_cast(float, o);
+}
+
+// Sum over the 64 lanes of a wave, left in lane 63 (and every lane of the
+// last 16-lane row).  Row butterflies (xor 1, xor 2, half-mirror, mirror),
+// then row_bcast:15 / row_bcast:31 carry the row totals up: six DPP adds, no
+// LDS traffic.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v = dpp_add<0xb1>(v);          // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e>(v);          // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);         // row_half_mirror
+    v = dpp_add<0x140>(v);         // row_mirror: every lane holds its row's sum
+    v = dpp_add<0x142, 0xa>(v);    // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);    // row_bcast:31 into rows 2 and 3
     return v;
+}
+
+// Sum over the wave, returned in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = wave_sum_lane63(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Q4_K 6-bit (scale, min) of sub-block j (reference cpp:1112-1120) from the
@@ -65,13 +86,11 @@ __device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, ui
                                              int& sc, int& mn) {
     const int jj = j & 3;
     const uint32_t a = byte_of(s0, jj), b = byte_of(s1, jj), c = byte_of(s2, jj);
-    if (j < 4) {
-        sc = static_cast<int>(a & 63u);
-        mn = static_cast<int>(b & 63u);
-    } else {
-        sc = static_cast<int>((c & 15u) | ((a >> 6) << 4));
-        mn = static_cast<int>((c >> 4) | ((b >> 6) << 4));
-    }
+    // both forms computed and selected: j varies across lanes, a branch would diverge
+    const uint32_t sc_lo = a & 63u, mn_lo = b & 63u;
+    const uint32_t sc_hi = (c & 15u) | ((a >> 6) << 4), mn_hi = (c >> 4) | ((b >> 6) << 4);
+    sc = static_cast<int>(j < 4 ? sc_lo : sc_hi);
+    mn = static_cast<int>(j < 4 ? mn_lo : mn_hi);
 }
 
 // 1/rms of one head of hd values, formed as the reference does
