@@ -101,26 +101,26 @@ def time_gemv(pkg, lib, torch, t, k, n, steps, warmup, copies, seed=1):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     pkg.check(lib)
-    # event pass: one event pair around every launch on the library stream
+    # event pass: one event pair around the whole back-to-back loop on the
+    # library stream; per-launch pairs would add the event overhead (~5 us)
+    # to every launch
     ev = HipEvents(lib.gncx_hip_get_stream() or 0)
-    evs = ev.create(2 * steps)
+    e0, e1 = ev.create(2)
+    ev.record(e0)
     for i in range(steps):
-        ev.record(evs[2 * i])
         fn(wp[i % copies], 0, t, xp, None, k, n, yp, None)
-        ev.record(evs[2 * i + 1])
-    torch.cuda.synchronize()
-    dur = np.array([ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]) * 1e3
-    ev.destroy(evs)
+    ev.record(e1)
+    kernel_us = ev.elapsed_ms(e0, e1) * 1e3 / steps
+    ev.destroy([e0, e1])
     nbytes = gemv_bytes(pkg, t, k, n)
     del ws
     torch.cuda.empty_cache()
     return {
         "bytes": nbytes,
         "wall_ms": wall_ms,
-        "kernel_us_mean": float(dur.mean()),
-        "kernel_us_median": float(np.median(dur)),
+        "kernel_us_mean": kernel_us,
         "gbps_wall": nbytes / (wall_ms * 1e-3) / 1e9,
-        "gbps_kernel": nbytes / (dur.mean() * 1e-6) / 1e9,
+        "gbps_kernel": nbytes / (kernel_us * 1e-6) / 1e9,
         "w_host": w_host,
         "x_host": x_host,
     }
@@ -198,13 +198,27 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
-              file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (GEMV would shard by output rows, "
+              "attention by KV head)", file=sys.stderr)
         return 2
 
     import torch
+    if args.copy_calibration > 0:
+        n = args.copy_calibration << 20
+        src = torch.ones(n // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return 0
+
     pkg = import_pkg()
     lib = pkg.load()
     assert lib.gncx_hip_init(0) == 0, lib.gncx_hip_last_error()
@@ -262,7 +276,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel_us_mean": round(head["kernel_us_mean"], 3),
-                     "kernel_us_median": round(head["kernel_us_median"], 3)},
+                     "timing": "HIP events around the back-to-back timed loop on the library stream"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
                     const int s = lane + 64 * (b * P + p);
-                    if (s < slots) S::load(f[r][p], rp, s);
+                    if (s < slots) S::load(f[r][p], PtrRow{rp}, s);
                 }
             }
         }
@@ -134,40 +134,80 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 // g, g + G, g + 2G, ... (G = number of work-groups): at any moment the whole
 // GPU is sweeping one contiguous stretch of the matrix, which keeps HBM pages
 // and channels busy the way a plain streaming read does (a contiguous band
-// per work-group measured 2x slower).  Waves are arranged nwk x nwr: wave
-// (kw, rw) handles slots [64 kw, 64 kw + 64) (one K-slice, its activations
-// kept in registers) of the work-group's local rows rw, rw + nwr, ...  Rows go
-// R at a time in two register buffers used in turn; the first batches' loads
-// are issued before the quantisation.  Each wave's per-row partial goes to LDS
-// and the K-slices are added in a fixed order at the end (deterministic).
+// per work-group measured 2x slower).
+//
+// Waves are arranged nwk x nwr: wave (kw, rw) covers slots [64 kw, 64 kw + 64)
+// of a row (one K-slice, its activations kept in registers).  Rows are handed
+// out R at a time from an LDS counter per K-slice, so waves the memory system
+// serves first take more rows (with a static split the last of a CU's 16
+// waves finished up to 15% after the first).  Each wave keeps two batches in
+// flight in two register buffers used in turn.
+//
+// The first nqw waves quantise x before they touch weights and publish it
+// with an LDS count; the other waves issue their first two batches at once
+// and wait for that count only when they need x, so the quantisation never
+// waits behind weight loads held up in the memory pipeline.
+//
+// Weight loads go through a per-row buffer resource (base in scalar
+// registers); past-the-end batches use an empty resource, so every wave
+// issues the same loads in the same order and the waitcnt before each use
+// waits only for that use's loads.  With one K-slice per row (nwk == 1) the
+// wave writes y itself; otherwise the slices' partials meet in LDS and are
+// added in a fixed order at the end (results never depend on which wave took
+// which row).
+//
+// Two block sizes: 16 waves per CU for matrices up to kBandStreamBytes per
+// work-group (more loads in flight ramp a short call up faster), 8 waves
+// above that (fewer rows in flight keep the swept window of the matrix small:
+// Q6_K 4096 x 128256 measured 80 us with 8 waves against 98 us with 16).
 #ifndef GNCX_BAND_THREADS
 #define GNCX_BAND_THREADS 1024
+#endif
+#ifndef GNCX_BAND_THREADS_STREAM
+#define GNCX_BAND_THREADS_STREAM 512
+#endif
+#ifndef GNCX_BAND_STREAM_KB
+#define GNCX_BAND_STREAM_KB 256
 #endif
 #ifndef GNCX_BAND_GROUPS
 #define GNCX_BAND_GROUPS 256
 #endif
 #ifndef GNCX_Q4K_ROWS
-#define GNCX_Q4K_ROWS 2
+#define GNCX_Q4K_ROWS 1
+#endif
+#ifndef GNCX_Q40_ROWS
+#define GNCX_Q40_ROWS 1
+#endif
+#ifndef GNCX_Q80_ROWS
+#define GNCX_Q80_ROWS 1
+#endif
+#ifndef GNCX_BF16_ROWS
+#define GNCX_BF16_ROWS 1
 #endif
 constexpr int kBandThreads = GNCX_BAND_THREADS;
-constexpr int kBandWaves = kBandThreads / 64;
+constexpr int kBandThreadsStream = GNCX_BAND_THREADS_STREAM;
+constexpr size_t kBandStreamBytes = static_cast<size_t>(GNCX_BAND_STREAM_KB) * 1024;
 constexpr int32_t kBandGroups = GNCX_BAND_GROUPS;  // one work-group per CU of an MI355X
 constexpr size_t kBandLds = 64 * 1024;
+constexpr int kBandQU = 8;          // x tasks per quantising thread with loads in flight together
+constexpr size_t kBandCtl = 128;    // LDS head: per-K-slice row counters and the quantised count
+constexpr int kCtlQuantised = 31;   // index of the count of waves done quantising
 
-template <int TYPE, int R>
-__global__ __launch_bounds__(kBandThreads) void gemv_band_kernel(const uint8_t* __restrict w, size_t rbytes,
+template <int TYPE, int R, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __restrict w, uint32_t rbytes,
                                                                  const float* __restrict x, int32_t k,
-                                                                 int32_t n, float* __restrict y,
-                                                                 int32_t rows_per_wg, int32_t nwk, int32_t nwr) {
+                                                                 int32_t n, float* __restrict y, int32_t nwk,
+                                                                 int32_t nwr, int32_t nqw) {
     using S = Slot<TYPE>;
     using Frag = typename S::Frag;
     using Act = typename S::Act;
-    constexpr int QU = 4;  // x tasks per thread loaded ahead (covers k <= 16384)
+    constexpr bool kQuant = TYPE != kBF16;
     extern __shared__ __align__(16) uint8_t lds[];
-    const size_t qbytes = TYPE == kBF16 ? 0 : static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta);
-    int8_t* q = reinterpret_cast<int8_t*>(lds);
-    ActMeta* meta = reinterpret_cast<ActMeta*>(lds + k);
-    float* part = reinterpret_cast<float*>(lds + qbytes);  // [rows_per_wg][nwk]
+    int32_t* ctl = reinterpret_cast<int32_t*>(lds);
+    int8_t* q = reinterpret_cast<int8_t*>(lds + kBandCtl);
+    ActMeta* meta = reinterpret_cast<ActMeta*>(lds + kBandCtl + k);
+    const size_t qbytes = kQuant ? static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta) : 0;
+    float* part = reinterpret_cast<float*>(lds + kBandCtl + qbytes);  // [local row][nwk], nwk > 1 only
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int kw = wv % nwk, rw = wv / nwk;
@@ -178,54 +218,72 @@ __global__ __launch_bounds__(kBandThreads) void gemv_band_kernel(const uint8_t* 
     const int32_t groups = gridDim.x;
     // local row li of this work-group is global row li * groups + blockIdx.x
     const int32_t rows_here = (n - static_cast<int32_t>(blockIdx.x) + groups - 1) / groups;
-    const int32_t per_wave = (rows_per_wg + nwr - 1) / nwr;
-    const int32_t nb = (per_wave + R - 1) / R;
+    const int32_t nbt = (rows_here + R - 1) / R;  // batches of R local rows
     auto grow = [&](int32_t li) { return static_cast<size_t>(li) * groups + blockIdx.x; };
 
-    // two weight buffers used in turn (no register copies: a copy would wait
-    // for the loads in flight).  Loads are unconditional -- lanes without a
-    // slot or row read slot 0 of row 0 and their result is masked -- so the
-    // waitcnts before each use only wait for that use's loads.
-    Frag fa[R], fb[R];
-    auto issue = [&](Frag (&f)[R], int32_t b) {
+    if (threadIdx.x < kBandCtl / sizeof(int32_t)) ctl[threadIdx.x] = 0;
+    __syncthreads();
+
+    auto grab = [&]() -> int32_t {
+        int32_t g = 0;
+        if (lane == 0) g = __hip_atomic_fetch_add(&ctl[kw], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return __builtin_amdgcn_readfirstlane(g);
+    };
+    auto issue = [&](Frag (&f)[R], int32_t j) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int32_t li = rw + nwr * (b * R + r);
-            const bool ok = has_slot && li < rows_here;
-            S::load(f[r], ok ? w + grow(li) * rbytes : w, ok ? s : 0);
+            const int32_t li = j * R + r;
+            const bool ok = j < nbt && li < rows_here;
+            S::load(f[r], BufRow(w + (ok ? grow(li) : 0) * rbytes, rbytes, ok), s);
         }
     };
-    auto reduce = [&](const Frag (&f)[R], const Act& a, int32_t b) {
+    auto reduce = [&](const Frag (&f)[R], const Act& a, int32_t j) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int32_t li = rw + nwr * (b * R + r);
-            if (active && li < rows_here) {  // wave-uniform
+            const int32_t li = j * R + r;
+            if (j < nbt && li < rows_here) {  // wave-uniform
                 float v = has_slot ? S::dot(f[r], a, s) : 0.0f;
                 v = wave_sum_lane63(v);
-                if (lane == 63) part[li * nwk + kw] = v;
+                if (lane == 63) {
+                    if (nwk == 1) y[grow(li)] = v;
+                    else part[li * nwk + kw] = v;
+                }
             }
         }
     };
 
-    // x first (it is waited for first), then every weight batch this wave can hold
-    float4 xv[QU];
-    if (TYPE != kBF16) quant_load<QU>(xv, x, k / 32, threadIdx.x, kBandThreads);
-    issue(fa, 0);
-    if (nb > 1) issue(fb, 1);
-    if (TYPE != kBF16) quant_finish<QU>(xv, x, k / 32, threadIdx.x, kBandThreads, q, meta);
-    __syncthreads();
-    Act a;
-    if (has_slot) slot_act<TYPE>(a, s, q, meta, x);
-    for (int32_t b = 0; b < nb; b += 2) {
-        reduce(fa, a, b);
-        if (b + 2 < nb) issue(fa, b + 2);
-        if (b + 1 < nb) {
-            reduce(fb, a, b + 1);
-            if (b + 3 < nb) issue(fb, b + 3);
+    if (kQuant && wv < nqw) {
+        float4 xv[kBandQU];
+        quant_load<kBandQU>(xv, x, k / 32, threadIdx.x, nqw * 64);
+        quant_finish<kBandQU>(xv, x, k / 32, threadIdx.x, nqw * 64, q, meta);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's q / meta writes are done
+        if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (active) {
+        Frag fa[R], fb[R];
+        int32_t ja = grab();
+        issue(fa, ja);
+        int32_t jb = grab();
+        issue(fb, jb);
+        if (kQuant) {
+            // the quantising waves depend on nothing but their own x loads
+            while (__hip_atomic_load(&ctl[kCtlQuantised], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nqw)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        Act a;
+        if (has_slot) slot_act<TYPE>(a, s, q, meta, x);
+        while (ja < nbt || jb < nbt) {  // wave-uniform
+            reduce(fa, a, ja);
+            if (ja < nbt) ja = grab();
+            issue(fa, ja);
+            reduce(fb, a, jb);
+            if (jb < nbt) jb = grab();
+            issue(fb, jb);
         }
     }
+    if (nwk == 1) return;
     __syncthreads();
-    for (int32_t li = threadIdx.x; li < rows_here; li += kBandThreads) {
+    for (int32_t li = threadIdx.x; li < rows_here; li += THREADS) {
         float acc = 0.0f;
         for (int j = 0; j < nwk; ++j) acc += part[li * nwk + j];
         y[grow(li)] = acc;
@@ -270,30 +328,43 @@ hipError_t launch_gemv_t(const uint8_t* w, const float* x, int32_t k, int32_t n,
 }
 
 
-// Band kernel geometry for (type, k, n); false when the shape does not fit it.
-bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t& rows_per_wg, int32_t& groups,
-               int32_t& nwk, int32_t& nwr, size_t& lds) {
+// Band kernel geometry for (type, k, n) with `waves` waves per work-group;
+// false when the shape does not fit it.
+bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t waves, int32_t& groups,
+               int32_t& nwk, int32_t& nwr, int32_t& nqw, size_t& lds) {
     nwk = (slots + 63) / 64;
-    if (nwk < 1 || nwk > kBandWaves) return false;
-    nwr = kBandWaves / nwk;
+    if (nwk < 1 || nwk > waves) return false;
+    nwr = waves / nwk;
     groups = n < kBandGroups ? n : kBandGroups;
-    rows_per_wg = (n + groups - 1) / groups;
+    const int32_t rows_per_wg = (n + groups - 1) / groups;
     groups = (n + rows_per_wg - 1) / rows_per_wg;
+    const int32_t tasks = k / 4;  // 4 values of x per quantisation task
+    nqw = quantised ? (tasks + 64 * kBandQU - 1) / (64 * kBandQU) : 0;
+    if (nqw > waves) nqw = waves;
     const size_t qbytes = quantised ? static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta) : 0;
-    lds = qbytes + sizeof(float) * static_cast<size_t>(rows_per_wg) * nwk;
-    return lds <= kBandLds;
+    lds = kBandCtl + qbytes + (nwk > 1 ? sizeof(float) * static_cast<size_t>(rows_per_wg) * nwk : 0);
+    return lds <= kBandLds && nwk <= static_cast<int32_t>(kCtlQuantised);
+}
+
+template <int TYPE, int R, int THREADS>
+bool try_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+    int32_t groups, nwk, nwr, nqw;
+    size_t lds;
+    if (!band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, THREADS / 64, groups, nwk, nwr, nqw, lds))
+        return false;
+    hipLaunchKernelGGL((gemv_band_kernel<TYPE, R, THREADS>), dim3(groups), dim3(THREADS), lds, stream, w,
+                       static_cast<uint32_t>(row_bytes(TYPE, k)), x, k, n, y, nwk, nwr, nqw);
+    return true;
 }
 
 template <int TYPE, int R>
 hipError_t launch_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream,
                        bool& used) {
-    int32_t rpw, groups, nwk, nwr;
-    size_t lds;
-    used = band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, rpw, groups, nwk, nwr, lds);
-    if (!used) return hipSuccess;
-    hipLaunchKernelGGL((gemv_band_kernel<TYPE, R>), dim3(groups), dim3(kBandThreads), lds, stream, w,
-                       row_bytes(TYPE, k), x, k, n, y, rpw, nwk, nwr);
-    return hipGetLastError();
+    const int32_t groups = n < kBandGroups ? n : kBandGroups;
+    const size_t per_group = row_bytes(TYPE, k) * static_cast<size_t>(n) / static_cast<size_t>(groups);
+    used = (per_group > kBandStreamBytes && try_band<TYPE, R, kBandThreadsStream>(w, x, k, n, y, stream)) ||
+           try_band<TYPE, R, kBandThreads>(w, x, k, n, y, stream);
+    return used ? hipGetLastError() : hipSuccess;
 }
 
 }  // namespace
@@ -316,11 +387,11 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     bool used = false;
     hipError_t e = hipSuccess;
     switch (type) {
-    case kQ4_0: e = launch_band<kQ4_0, 4>(w, x, k, n, y, stream, used); break;
-    case kQ8_0: e = launch_band<kQ8_0, 2>(w, x, k, n, y, stream, used); break;
+    case kQ4_0: e = launch_band<kQ4_0, GNCX_Q40_ROWS>(w, x, k, n, y, stream, used); break;
+    case kQ8_0: e = launch_band<kQ8_0, GNCX_Q80_ROWS>(w, x, k, n, y, stream, used); break;
     case kQ4_K: e = launch_band<kQ4_K, GNCX_Q4K_ROWS>(w, x, k, n, y, stream, used); break;
     case kQ6_K: e = launch_band<kQ6_K, 1>(w, x, k, n, y, stream, used); break;
-    case kBF16: e = launch_band<kBF16, 4>(w, x, k, n, y, stream, used); break;
+    case kBF16: e = launch_band<kBF16, GNCX_BF16_ROWS>(w, x, k, n, y, stream, used); break;
     default: return hipErrorInvalidValue;
     }
     if (used || e != hipSuccess) return e;

@@ -2,9 +2,8 @@
 // matbatch kernels.  A "slot" maps one lane to a fixed byte range of one
 // block of a weight row.  Each format has
 //   Frag                 the raw weight registers one slot needs from HBM,
-//   load(f, row, s)      issues those loads (plain loads: non-temporal ones
-//                        measured up to 2.3x slower on these 2-aligned,
-//                        partly overlapping fields and fetched 1.5x the bytes),
+//   load(f, row, s)      issues those loads from a row source (PtrRow or
+//                        BufRow below),
 //   Act                  the Q8 activation registers the slot multiplies,
 //   load_act(a, s, ...)  reads them (LDS q + ActMeta, or fp32 x for BF16),
 //   dot(f, a, s)         the slot's fp32 share of the row sum,
@@ -27,35 +26,72 @@ namespace dev {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x4 w_ld16(const uint8_t* p) {  // 16-byte aligned
-    return *reinterpret_cast<const u32x4*>(p);
-}
-__device__ __forceinline__ u32x4a4 w_ld16_a4(const uint8_t* p) {  // 4-byte aligned
-    return *reinterpret_cast<const u32x4a4*>(p);
-}
-__device__ __forceinline__ u32x2a4 w_ld8_a4(const uint8_t* p) {
-    return *reinterpret_cast<const u32x2a4*>(p);
-}
-__device__ __forceinline__ uint32_t w_ld_u16(const uint8_t* p) {
-    return *reinterpret_cast<const uint16_t*>(p);
-}
+// Row sources: a slot reads its fields by byte offset within one weight row.
+//   PtrRow  global loads from a row pointer (plain loads: non-temporal ones
+//           measured up to 2.3x slower on these 2-aligned, partly overlapping
+//           fields and fetched 1.5x the bytes),
+//   BufRow  buffer loads through a resource whose base (4-aligned, delta
+//           bytes before the row) sits in scalar registers; an offset at or
+//           past num_records reads 0 and makes no memory request, so a
+//           resource with num_records 0 is a free dummy row.
+// Offsets passed to ld16 are 16-aligned from a 16-aligned row; ld16a4 and
+// ld8a4 take 4-aligned row addresses (sh() gives a field's address mod 4).
+struct PtrRow {
+    const uint8_t* p;
+    __device__ __forceinline__ u32x4 ld16(uint32_t o) const { return *reinterpret_cast<const u32x4*>(p + o); }
+    __device__ __forceinline__ u32x4a4 ld16a4(uint32_t o) const {
+        return *reinterpret_cast<const u32x4a4*>(p + o);
+    }
+    __device__ __forceinline__ u32x2a4 ld8a4(uint32_t o) const {
+        return *reinterpret_cast<const u32x2a4*>(p + o);
+    }
+    __device__ __forceinline__ uint32_t ldu16(uint32_t o) const {
+        return *reinterpret_cast<const uint16_t*>(p + o);
+    }
+    __device__ __forceinline__ uint32_t sh(uint32_t o) const {
+        return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(p) + o) & 3u);
+    }
+};
 
-// raw 16-byte field at a 2-aligned address p: the dword-aligned dwordx4 at
-// p - sh and the 2 bytes at p + 14 (see ld16_a2); sh = p mod 4 is kept by
-// the caller (all fields of one block share it) and the field is realigned
-// only when used
+struct BufRow {
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t delta;
+    // rows start 2-aligned; the resource starts at the 4-aligned address at
+    // or before the row and covers exactly the row (0 bytes when !valid)
+    __device__ __forceinline__ BufRow(const uint8_t* row, uint32_t bytes, bool valid) {
+        const uint32_t dl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(row) & 3u);
+        r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(row - dl), static_cast<short>(0),
+                                              valid ? static_cast<int>(bytes + dl) : 0, 0x00020000);
+        delta = dl;
+    }
+    __device__ __forceinline__ u32x4 ld16(uint32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(delta + o), 0, 0);
+    }
+    __device__ __forceinline__ u32x4a4 ld16a4(uint32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(delta + o), 0, 0);
+    }
+    __device__ __forceinline__ u32x2a4 ld8a4(uint32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(delta + o), 0, 0);
+    }
+    __device__ __forceinline__ uint32_t ldu16(uint32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(delta + o), 0, 0);
+    }
+    __device__ __forceinline__ uint32_t sh(uint32_t o) const { return (delta + o) & 3u; }
+};
+
+// raw 16-byte field at a 2-aligned row offset o: the dword-aligned dwordx4 at
+// o - sh and the 2 bytes at o + 14 (see ld16_a2); sh = field address mod 4 is
+// kept by the caller (all fields of one block share it) and the field is
+// realigned only when used
 struct Raw16 {
     u32x4a4 v;
     uint32_t tail;
 };
 
-__device__ __forceinline__ uint32_t addr_sh(const uint8_t* p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
-}
-
-__device__ __forceinline__ void raw16_load(Raw16& r, const uint8_t* p, uint32_t sh) {
-    r.v = w_ld16_a4(p - sh);
-    r.tail = w_ld_u16(p + 14);
+template <class Row>
+__device__ __forceinline__ void raw16_load(Raw16& r, const Row& row, uint32_t o, uint32_t sh) {
+    r.v = row.ld16a4(o - sh);
+    r.tail = row.ldu16(o + 14);
 }
 
 __device__ __forceinline__ uint4 raw16_get(const Raw16& r, uint32_t sh) {
@@ -84,12 +120,13 @@ struct Slot<kQ4_K> {
         int sl, sh;
     };
     static constexpr int32_t slots(int32_t k) { return (k / 256) * 4; }
-    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
-        const int sb = s >> 2, c = s & 3;
-        const uint8_t* blk = row + static_cast<size_t>(sb) * 144;
-        f.hdr = w_ld16(blk);
-        f.w0 = w_ld16(blk + 16 + 32 * c);
-        f.w1 = w_ld16(blk + 32 + 32 * c);
+    template <class Row>
+    __device__ static __forceinline__ void load(Frag& f, const Row& row, int s) {
+        const uint32_t sb = static_cast<uint32_t>(s) >> 2, c = static_cast<uint32_t>(s) & 3u;
+        const uint32_t blk = sb * 144u;
+        f.hdr = row.ld16(blk);
+        f.w0 = row.ld16(blk + 16u + 32u * c);
+        f.w1 = row.ld16(blk + 32u + 32u * c);
     }
     __device__ static __forceinline__ void load_act(Act& a, int s, const int8_t* __restrict q,
                                                     const ActMeta* __restrict meta) {
@@ -145,17 +182,19 @@ struct Slot<kQ6_K> {
         int s[4];     // sum of those 16 q
     };
     static constexpr int32_t slots(int32_t k) { return (k / 256) * 4; }
-    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
-        const int sb = s >> 2, n = (s >> 1) & 1, g = s & 1;
-        const uint8_t* blk = row + static_cast<size_t>(sb) * 210;
-        f.sh = addr_sh(blk);
-        raw16_load(f.pa, blk + 64 * n + 16 * g, f.sh);
-        raw16_load(f.pb, blk + 64 * n + 32 + 16 * g, f.sh);
-        raw16_load(f.ph, blk + 128 + 32 * n + 16 * g, f.sh);
-        const uint8_t* ps = blk + 192 + 8 * n;
-        f.sv = w_ld8_a4(ps - f.sh);
-        f.st = w_ld_u16(ps + 6);
-        f.d = w_ld_u16(blk + 208);
+    template <class Row>
+    __device__ static __forceinline__ void load(Frag& f, const Row& row, int s) {
+        const uint32_t sb = static_cast<uint32_t>(s) >> 2, n = (static_cast<uint32_t>(s) >> 1) & 1u,
+                       g = static_cast<uint32_t>(s) & 1u;
+        const uint32_t blk = sb * 210u;
+        f.sh = row.sh(blk);
+        raw16_load(f.pa, row, blk + 64u * n + 16u * g, f.sh);
+        raw16_load(f.pb, row, blk + 64u * n + 32u + 16u * g, f.sh);
+        raw16_load(f.ph, row, blk + 128u + 32u * n + 16u * g, f.sh);
+        const uint32_t ps = blk + 192u + 8u * n;
+        f.sv = row.ld8a4(ps - f.sh);
+        f.st = row.ldu16(ps + 6u);
+        f.d = row.ldu16(blk + 208u);
     }
     __device__ static __forceinline__ void load_act(Act& a, int s, const int8_t* __restrict q,
                                                     const ActMeta* __restrict meta) {
@@ -214,11 +253,12 @@ struct Slot<kQ4_0> {
         int sum;
     };
     static constexpr int32_t slots(int32_t k) { return k / 32; }
-    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int b) {
-        const uint8_t* blk = row + static_cast<size_t>(b) * 18;
-        f.d = w_ld_u16(blk);
-        f.sh = addr_sh(blk + 2);
-        raw16_load(f.qs, blk + 2, f.sh);
+    template <class Row>
+    __device__ static __forceinline__ void load(Frag& f, const Row& row, int b) {
+        const uint32_t blk = static_cast<uint32_t>(b) * 18u;
+        f.d = row.ldu16(blk);
+        f.sh = row.sh(blk + 2u);
+        raw16_load(f.qs, row, blk + 2u, f.sh);
     }
     __device__ static __forceinline__ void load_act(Act& a, int b, const int8_t* __restrict q,
                                                     const ActMeta* __restrict meta) {
@@ -254,12 +294,13 @@ struct Slot<kQ8_0> {
         float d;
     };
     static constexpr int32_t slots(int32_t k) { return k / 32; }
-    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int b) {
-        const uint8_t* blk = row + static_cast<size_t>(b) * 34;
-        f.d = w_ld_u16(blk);
-        f.sh = addr_sh(blk + 2);
-        raw16_load(f.lo, blk + 2, f.sh);
-        raw16_load(f.hi, blk + 18, f.sh);
+    template <class Row>
+    __device__ static __forceinline__ void load(Frag& f, const Row& row, int b) {
+        const uint32_t blk = static_cast<uint32_t>(b) * 34u;
+        f.d = row.ldu16(blk);
+        f.sh = row.sh(blk + 2u);
+        raw16_load(f.lo, row, blk + 2u, f.sh);
+        raw16_load(f.hi, row, blk + 18u, f.sh);
     }
     __device__ static __forceinline__ void load_act(Act& a, int b, const int8_t* __restrict q,
                                                     const ActMeta* __restrict meta) {
@@ -290,8 +331,9 @@ struct Slot<kBF16> {
         float4 a, b;
     };
     static constexpr int32_t slots(int32_t k) { return k / 8; }  // launchers require k % 8 == 0
-    __device__ static __forceinline__ void load(Frag& f, const uint8_t* __restrict row, int s) {
-        f.w = w_ld16(row + static_cast<size_t>(s) * 16);
+    template <class Row>
+    __device__ static __forceinline__ void load(Frag& f, const Row& row, int s) {
+        f.w = row.ld16(static_cast<uint32_t>(s) * 16u);
     }
     // BF16 multiplies the fp32 vector itself (global memory)
     __device__ static __forceinline__ void load_act_x(Act& a, int s, const float* __restrict x) {

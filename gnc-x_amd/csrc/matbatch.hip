@@ -40,7 +40,7 @@ __global__ __launch_bounds__(kThreads) void matbatch_rowtok_kernel(const uint8_t
     for (int32_t s = lane; s < slots; s += 64) {
         typename S::Frag f;
         typename S::Act a;
-        S::load(f, row, s);
+        S::load(f, PtrRow{row}, s);
         slot_act<TYPE>(a, s, qt, mt, x + static_cast<size_t>(t) * k);
         acc += S::dot(f, a, s);
     }
