@@ -30,6 +30,7 @@ import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK = 2.5e15  # dense fp16 matrix-core FLOP/s of one MI355X
 METRIC = "Q4_K GEMV HBM GB/s (% of peak); decode tok/s, Qwen3-8B-shaped, 1 GPU"
 
 
@@ -124,6 +125,37 @@ def time_gemv(pkg, lib, torch, t, k, n, steps, warmup, copies, seed=1):
         "w_host": w_host,
         "x_host": x_host,
     }
+
+
+def time_matbatch(pkg, lib, torch, t, k, n, b, steps, copies):
+    """gncx_xfold_universal_matbatch with device pointers; one HIP-event pair
+    around `steps` back-to-back calls (act quantisation + the MFMA product)."""
+    w_host = pkg.synth.make_weights(t, n, k, seed=11)
+    ws = [torch.from_numpy(w_host).cuda() for _ in range(copies)]
+    x = torch.from_numpy(pkg.synth.make_activations(b, k, seed=12).reshape(b, k)).cuda()
+    y = torch.zeros(b, n, dtype=torch.float32, device="cuda")
+    fn = lib.gncx_xfold_universal_matbatch
+    args = lambda i: (ws[i % copies].data_ptr(), 0, t, x.data_ptr(), b, k, n, y.data_ptr(), None)  # noqa: E731
+    for i in range(3):
+        fn(*args(i))
+    torch.cuda.synchronize()
+    pkg.check(lib)
+    ev = HipEvents(lib.gncx_hip_get_stream() or 0)
+    e0, e1 = ev.create(2)
+    ev.record(e0)
+    for i in range(steps):
+        fn(*args(i))
+    ev.record(e1)
+    us = ev.elapsed_ms(e0, e1) * 1e3 / steps
+    ev.destroy([e0, e1])
+    pkg.check(lib)
+    flops = 2.0 * b * k * n
+    nbytes = pkg.row_bytes(t, k) * n + 4 * b * k + 4 * b * n
+    del ws
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+            "frac_fp16_mfma_peak": round(flops / (us * 1e-6) / MFMA_FP16_PEAK, 4),
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
 def time_attention(lib, torch, H, KV, hd, ctx, sw, steps, copies):
@@ -255,6 +287,12 @@ def main() -> int:
             r = time_attention(lib, torch, H, KV, hd, ctx, sw, 50, cp)
             att[name] = {"us_per_step": round(r["us_per_step"], 2), "gbps": round(r["gbps"], 1)}
         extra["attention"] = att
+        mb = {}
+        for name, (tt, kk, nn) in {"q4k_4096x4096": (pkg.Q4_K, 4096, 4096), "q4k_4096x14336": (pkg.Q4_K, 4096, 14336),
+                                   "q6k_14336x4096": (pkg.Q6_K, 14336, 4096)}.items():
+            for bb in (64, 256, 512):
+                mb[f"{name}_b{bb}"] = time_matbatch(pkg, lib, torch, tt, kk, nn, bb, 20, 4)
+        extra["matbatch"] = mb
 
     cpu = None if args.no_cpu else cpu_baseline(pkg, t, k, n, head["w_host"], head["x_host"], args.cpu_seconds)
     line = {

@@ -135,11 +135,11 @@ __device__ __forceinline__ int quad_sum(int v) {
 // one ActMeta per block.  blockDim.x must be a multiple of 64.  Bit-exact with
 // the reference: IEEE 127/amax and amax/127, one rounding for x*inv,
 // round-half-even.
-__device__ __forceinline__ void quantize_task(const float4 v, int32_t b, int j, int8_t* __restrict q,
-                                              ActMeta* __restrict meta) {
+// The four int8 values and the block scale of one task (8 lanes per block).
+__device__ __forceinline__ void quantize_values(const float4 v, int& q0, int& q1, int& q2, int& q3, float& d) {
     const float a = group8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
-    float d = 0.0f;
+    q0 = q1 = q2 = q3 = 0;
+    d = 0.0f;
     if (a != 0.0f) {
         const float inv = 127.0f / a;
         d = a / 127.0f;
@@ -148,6 +148,13 @@ __device__ __forceinline__ void quantize_task(const float4 v, int32_t b, int j, 
         q2 = static_cast<int>(rintf(v.z * inv));
         q3 = static_cast<int>(rintf(v.w * inv));
     }
+}
+
+__device__ __forceinline__ void quantize_task(const float4 v, int32_t b, int j, int8_t* __restrict q,
+                                              ActMeta* __restrict meta) {
+    int q0, q1, q2, q3;
+    float d;
+    quantize_values(v, q0, q1, q2, q3, d);
     const uint32_t packed = (static_cast<uint32_t>(q0) & 0xffu) | ((static_cast<uint32_t>(q1) & 0xffu) << 8) |
                             ((static_cast<uint32_t>(q2) & 0xffu) << 16) | (static_cast<uint32_t>(q3) << 24);
     *reinterpret_cast<uint32_t*>(q + static_cast<size_t>(b) * 32 + j * 4) = packed;

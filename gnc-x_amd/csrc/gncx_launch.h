@@ -31,7 +31,7 @@ hipError_t launch_dequant(int32_t type, const uint8_t* w, int32_t k, int32_t n, 
                           hipStream_t stream);
 
 // Y[b x n] = Q8(X[b x k]) . W^T  (per-row activation quantisation).
-size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k);
+size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n);
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k,
                            int32_t n, float* y, void* workspace, size_t workspace_bytes,
                            hipStream_t stream);

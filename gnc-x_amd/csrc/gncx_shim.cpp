@@ -566,7 +566,7 @@ GNCX_API void gncx_xfold_universal_matbatch(const uint8_t* mmap_base, size_t wei
             bool host_out = false;
             float* y = out_target(out_batch, yn, g_rt.y, host_out, where);
             if (!y) break;
-            const size_t wsb = matbatch_workspace_bytes(ggml_type, batch_size, in_dim);
+            const size_t wsb = matbatch_workspace_bytes(ggml_type, batch_size, in_dim, out_dim);
             if (!g_rt.ws.ensure(wsb, where)) break;
             if (!check(launch_matbatch(ggml_type, w, x, batch_size, in_dim, out_dim, y, g_rt.ws.p, g_rt.ws.cap,
                                        g_rt.stream),

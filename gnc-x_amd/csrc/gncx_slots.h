@@ -34,22 +34,25 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 //           bytes before the row) sits in scalar registers; an offset at or
 //           past num_records reads 0 and makes no memory request, so a
 //           resource with num_records 0 is a free dummy row.
+// Offsets are signed: a realigned field read starts up to 2 bytes before the
+// field (o - sh), which is before the row itself for a row that starts 2 bytes
+// past a 4-byte boundary (still inside the tensor, whose base is 4-aligned).
 // Offsets passed to ld16 are 16-aligned from a 16-aligned row; ld16a4 and
-// ld8a4 take 4-aligned row addresses (sh() gives a field's address mod 4).
+// ld8a4 take 4-aligned addresses (sh() gives a field's address mod 4).
 struct PtrRow {
     const uint8_t* p;
-    __device__ __forceinline__ u32x4 ld16(uint32_t o) const { return *reinterpret_cast<const u32x4*>(p + o); }
-    __device__ __forceinline__ u32x4a4 ld16a4(uint32_t o) const {
+    __device__ __forceinline__ u32x4 ld16(int32_t o) const { return *reinterpret_cast<const u32x4*>(p + o); }
+    __device__ __forceinline__ u32x4a4 ld16a4(int32_t o) const {
         return *reinterpret_cast<const u32x4a4*>(p + o);
     }
-    __device__ __forceinline__ u32x2a4 ld8a4(uint32_t o) const {
+    __device__ __forceinline__ u32x2a4 ld8a4(int32_t o) const {
         return *reinterpret_cast<const u32x2a4*>(p + o);
     }
-    __device__ __forceinline__ uint32_t ldu16(uint32_t o) const {
+    __device__ __forceinline__ uint32_t ldu16(int32_t o) const {
         return *reinterpret_cast<const uint16_t*>(p + o);
     }
-    __device__ __forceinline__ uint32_t sh(uint32_t o) const {
-        return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(p) + o) & 3u);
+    __device__ __forceinline__ uint32_t sh(int32_t o) const {
+        return static_cast<uint32_t>((reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(o)) & 3u);
     }
 };
 
@@ -64,19 +67,40 @@ struct BufRow {
                                               valid ? static_cast<int>(bytes + dl) : 0, 0x00020000);
         delta = dl;
     }
-    __device__ __forceinline__ u32x4 ld16(uint32_t o) const {
-        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(delta + o), 0, 0);
+    __device__ __forceinline__ u32x4 ld16(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int32_t>(delta) + o, 0, 0);
     }
-    __device__ __forceinline__ u32x4a4 ld16a4(uint32_t o) const {
-        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(delta + o), 0, 0);
+    __device__ __forceinline__ u32x4a4 ld16a4(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int32_t>(delta) + o, 0, 0);
     }
-    __device__ __forceinline__ u32x2a4 ld8a4(uint32_t o) const {
-        return __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(delta + o), 0, 0);
+    __device__ __forceinline__ u32x2a4 ld8a4(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int32_t>(delta) + o, 0, 0);
     }
-    __device__ __forceinline__ uint32_t ldu16(uint32_t o) const {
-        return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(delta + o), 0, 0);
+    __device__ __forceinline__ uint32_t ldu16(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int32_t>(delta) + o, 0, 0);
     }
-    __device__ __forceinline__ uint32_t sh(uint32_t o) const { return (delta + o) & 3u; }
+    __device__ __forceinline__ uint32_t sh(int32_t o) const { return (delta + static_cast<uint32_t>(o)) & 3u; }
+};
+
+// Rows of a tile read through one wave-uniform resource over the tile's rows
+// (4-aligned base); each lane adds the byte offset of its own row.  A lane
+// with no row uses an offset past the resource and reads zeros.
+struct TileRow {
+    __amdgpu_buffer_rsrc_t r;
+    int32_t base;
+    __device__ __forceinline__ u32x4 ld16(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, base + o, 0, 0);
+    }
+    __device__ __forceinline__ u32x4a4 ld16a4(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, base + o, 0, 0);
+    }
+    __device__ __forceinline__ u32x2a4 ld8a4(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, base + o, 0, 0);
+    }
+    __device__ __forceinline__ uint32_t ldu16(int32_t o) const {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, base + o, 0, 0);
+    }
+    __device__ __forceinline__ uint32_t sh(int32_t o) const { return static_cast<uint32_t>(base + o) & 3u; }
 };
 
 // raw 16-byte field at a 2-aligned row offset o: the dword-aligned dwordx4 at
@@ -90,8 +114,8 @@ struct Raw16 {
 
 template <class Row>
 __device__ __forceinline__ void raw16_load(Raw16& r, const Row& row, uint32_t o, uint32_t sh) {
-    r.v = row.ld16a4(o - sh);
-    r.tail = row.ldu16(o + 14);
+    r.v = row.ld16a4(static_cast<int32_t>(o) - static_cast<int32_t>(sh));
+    r.tail = row.ldu16(static_cast<int32_t>(o) + 14);
 }
 
 __device__ __forceinline__ uint4 raw16_get(const Raw16& r, uint32_t sh) {
@@ -192,7 +216,7 @@ struct Slot<kQ6_K> {
         raw16_load(f.pb, row, blk + 64u * n + 32u + 16u * g, f.sh);
         raw16_load(f.ph, row, blk + 128u + 32u * n + 16u * g, f.sh);
         const uint32_t ps = blk + 192u + 8u * n;
-        f.sv = row.ld8a4(ps - f.sh);
+        f.sv = row.ld8a4(static_cast<int32_t>(ps) - static_cast<int32_t>(f.sh));
         f.st = row.ldu16(ps + 6u);
         f.d = row.ldu16(blk + 208u);
     }

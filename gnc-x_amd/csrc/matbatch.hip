@@ -5,9 +5,20 @@
 // on its own to per-32 int8 blocks (cpp:1506-1510), then each output is the
 // same integer block dot as the matvec; the output is row-major out[t*N + m].
 //
-// Baseline kernel: the activations are quantised once into the workspace,
-// then a wave computes one (row, token) output with the GEMV slot dots.  The
-// weight row is re-read per token from the caches.
+// Quantised weights (Q4_0, Q8_0, Q4_K, Q6_K) go through the matrix cores:
+//   1. act_f16_kernel quantises each token row exactly as the reference does
+//      and stores the quantised activations q * d as fp16 [B x K] (one
+//      rounding of an exactly quantised value),
+//   2. matbatch_mfma_kernel streams 64-wide K steps: the work-group's weight
+//      rows are dequantised block by block (fp32 arithmetic, one fp16
+//      rounding) into LDS, its token rows are copied into LDS, and each wave
+//      runs v_mfma_f32_32x32x16_f16 tiles with fp32 accumulation.
+// fp16 rounding of both operands keeps Y within about 3e-4 relative L2 of the
+// reference's integer block dots (measured on the CPU for all four formats);
+// the per-32-block scales make an exact int8 MFMA path pay ~3 VALU operations
+// per output and block, several times the matrix-core time.
+// BF16 weights (fp32 activations, cpp:1432-1461) use the slot-dot kernel: a
+// wave per (row, token).
 #include <hip/hip_runtime.h>
 
 #include "gncx_device.h"
@@ -48,6 +59,381 @@ __global__ __launch_bounds__(kThreads) void matbatch_rowtok_kernel(const uint8_t
     if (lane == 0) y[static_cast<size_t>(t) * n + r] = acc;
 }
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+    const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
+    const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
+    return lo | (hi << 16);
+}
+
+// fp16(q * d) of the reference's per-32 quantisation of row blockIdx.y of x
+// (cpp:955-995): 8 lanes per block, 4 values per lane.
+__global__ __launch_bounds__(kThreads) void act_f16_kernel(const float* __restrict x, int32_t k,
+                                                           uint2* __restrict xh) {
+    const int32_t t = blockIdx.x * kThreads + threadIdx.x;  // task: 4 values
+    if (t >= k / 4) return;  // whole 8-lane groups leave together (k % 32 == 0)
+    const size_t at = static_cast<size_t>(blockIdx.y) * (k / 4) + t;
+    const float4 v = reinterpret_cast<const float4*>(x)[at];
+    int q0, q1, q2, q3;
+    float d;
+    quantize_values(v, q0, q1, q2, q3, d);
+    xh[at] = make_uint2(pack_half2(static_cast<float>(q0) * d, static_cast<float>(q1) * d),
+                        pack_half2(static_cast<float>(q2) * d, static_cast<float>(q3) * d));
+}
+
+// Weights e0 .. e0 + 31 (e0 a multiple of 32) of one row: raw block bytes
+// loaded into registers (WRaw::load, issued two K steps ahead of their use),
+// then dequantised in fp32 and rounded once to fp16 pairs (WRaw::get); an
+// all-zero block (what an empty BufRow reads) dequantises to zeros.  Formulas:
+// Q4_0 d (q - 8) (cpp:1023-1030), Q8_0 d q, Q4_K (d sc) q - dmin m
+// (cpp:1135-1178), Q6_K (d sc) q (cpp:742-757).
+template <int TYPE>
+struct WRaw;
+
+template <>
+struct WRaw<kQ4_0> {
+    uint32_t d, sh;
+    Raw16 qs;
+    template <class Row>
+    __device__ __forceinline__ void load(const Row& r, int32_t e0) {
+        const uint32_t blk = static_cast<uint32_t>(e0 / 32) * 18u;
+        d = r.ldu16(blk);
+        sh = r.sh(blk + 2u);
+        raw16_load(qs, r, blk + 2u, sh);
+    }
+    __device__ __forceinline__ void get(int32_t, uint32_t (&o)[16]) const {
+        const float dv = half_bits_to_float(d);
+        const uint4 q = raw16_get(qs, sh);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = w[i] & 0x0f0f0f0fu, hi = (w[i] >> 4) & 0x0f0f0f0fu;
+            o[2 * i] = pack_half2(dv * static_cast<float>(static_cast<int>(lo & 15u) - 8),
+                                  dv * static_cast<float>(static_cast<int>((lo >> 8) & 15u) - 8));
+            o[2 * i + 1] = pack_half2(dv * static_cast<float>(static_cast<int>((lo >> 16) & 15u) - 8),
+                                      dv * static_cast<float>(static_cast<int>(lo >> 24) - 8));
+            o[8 + 2 * i] = pack_half2(dv * static_cast<float>(static_cast<int>(hi & 15u) - 8),
+                                      dv * static_cast<float>(static_cast<int>((hi >> 8) & 15u) - 8));
+            o[8 + 2 * i + 1] = pack_half2(dv * static_cast<float>(static_cast<int>((hi >> 16) & 15u) - 8),
+                                          dv * static_cast<float>(static_cast<int>(hi >> 24) - 8));
+        }
+    }
+};
+
+template <>
+struct WRaw<kQ8_0> {
+    uint32_t d, sh;
+    Raw16 lo, hi;
+    template <class Row>
+    __device__ __forceinline__ void load(const Row& r, int32_t e0) {
+        const uint32_t blk = static_cast<uint32_t>(e0 / 32) * 34u;
+        d = r.ldu16(blk);
+        sh = r.sh(blk + 2u);
+        raw16_load(lo, r, blk + 2u, sh);
+        raw16_load(hi, r, blk + 18u, sh);
+    }
+    __device__ __forceinline__ void get(int32_t, uint32_t (&o)[16]) const {
+        const float dv = half_bits_to_float(d);
+        const uint4 a = raw16_get(lo, sh), b = raw16_get(hi, sh);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int v0 = static_cast<int8_t>(w[i] & 0xffu), v1 = static_cast<int8_t>((w[i] >> 8) & 0xffu);
+            const int v2 = static_cast<int8_t>((w[i] >> 16) & 0xffu), v3 = static_cast<int8_t>(w[i] >> 24);
+            o[2 * i] = pack_half2(dv * static_cast<float>(v0), dv * static_cast<float>(v1));
+            o[2 * i + 1] = pack_half2(dv * static_cast<float>(v2), dv * static_cast<float>(v3));
+        }
+    }
+};
+
+template <>
+struct WRaw<kQ4_K> {
+    u32x4 hdr, a, b;
+    template <class Row>
+    __device__ __forceinline__ void load(const Row& r, int32_t e0) {
+        const uint32_t blk = static_cast<uint32_t>(e0 / 256) * 144u, c = static_cast<uint32_t>(e0 % 256) / 64u;
+        hdr = r.ld16(blk);
+        a = r.ld16(blk + 16u + 32u * c);
+        b = r.ld16(blk + 32u + 32u * c);
+    }
+    __device__ __forceinline__ void get(int32_t e0, uint32_t (&o)[16]) const {
+        const int j = (e0 % 256) / 32, sh = 4 * (j & 1);
+        int sc, mn;
+        k4_scale_min(j, hdr.y, hdr.z, hdr.w, sc, mn);
+        const float s = half_bits_to_float(hdr.x & 0xffffu) * static_cast<float>(sc);
+        const float m = half_bits_to_float(hdr.x >> 16) * static_cast<float>(mn);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t q = (w[i] >> sh) & 0x0f0f0f0fu;
+            o[2 * i] = pack_half2(s * static_cast<float>(q & 15u) - m, s * static_cast<float>((q >> 8) & 15u) - m);
+            o[2 * i + 1] =
+                pack_half2(s * static_cast<float>((q >> 16) & 15u) - m, s * static_cast<float>(q >> 24) - m);
+        }
+    }
+};
+
+template <>
+struct WRaw<kQ6_K> {
+    Raw16 l0, l1, h0, h1;
+    uint32_t scw, d, sh;
+    template <class Row>
+    __device__ __forceinline__ void load(const Row& r, int32_t e0) {
+        const uint32_t blk = static_cast<uint32_t>(e0 / 256) * 210u;
+        const uint32_t rr = static_cast<uint32_t>(e0 % 256), h = rr / 128u, grp = (rr % 128u) / 32u;
+        const uint32_t ql = blk + 64u * h + ((grp & 1u) ? 32u : 0u), qh = blk + 128u + 32u * h;
+        sh = r.sh(blk);  // every field offset used here is even: one shift for all
+        raw16_load(l0, r, ql, sh);
+        raw16_load(l1, r, ql + 16u, sh);
+        raw16_load(h0, r, qh, sh);
+        raw16_load(h1, r, qh + 16u, sh);
+        scw = r.ldu16(blk + 192u + 8u * h + 2u * grp);  // sc of elements 0-15 and 16-31
+        d = r.ldu16(blk + 208u);
+    }
+    __device__ __forceinline__ void get(int32_t e0, uint32_t (&o)[16]) const {
+        const int grp = ((e0 % 256) % 128) / 32;
+        const float dv = half_bits_to_float(d);
+        const float s0 = dv * static_cast<float>(static_cast<int8_t>(scw & 0xffu));
+        const float s1 = dv * static_cast<float>(static_cast<int8_t>(scw >> 8));
+        const uint4 a = raw16_get(l0, sh), b = raw16_get(l1, sh), c = raw16_get(h0, sh), e = raw16_get(h1, sh);
+        const uint32_t L[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t H[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
+        const int lsh = grp >= 2 ? 4 : 0, hsh = 2 * grp;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float s = i < 4 ? s0 : s1;
+            const uint32_t q = ((L[i] >> lsh) & 0x0f0f0f0fu) | (((H[i] >> hsh) & 0x03030303u) << 4);
+            o[2 * i] = pack_half2(s * static_cast<float>(static_cast<int>(q & 63u) - 32),
+                                  s * static_cast<float>(static_cast<int>((q >> 8) & 63u) - 32));
+            o[2 * i + 1] = pack_half2(s * static_cast<float>(static_cast<int>((q >> 16) & 63u) - 32),
+                                      s * static_cast<float>(static_cast<int>(q >> 24) - 32));
+        }
+    }
+};
+
+// Y tile of (64 WM) tokens x (64 WN) rows per work-group of 4 waves (2 x 2);
+// each wave owns WM x WN 32x32 accumulator tiles.  K advances 64 per step
+// through two LDS buffers: token rows [tokens][64 + 8 pad] fp16 and weight
+// rows [rows][64 + 8 pad] fp16.  In step s the MFMAs consume LDS buffer
+// s % 2 while the loads for later steps are in flight, then step s + 1's
+// registers are written to the other buffer; one barrier per step.  All loads
+// are buffer loads whose out-of-range reads return 0 without a memory request
+// (tokens past B, K past the range, rows past N), so each wave issues the same
+// loads every step and each wait covers exactly the loads it needs.
+// MFMA operand layouts (v_mfma_f32_32x32x16_f16): lane l holds
+// A[l % 32][8 (l / 32) .. + 8] and B[8 (l / 32) .. + 8][l % 32]; accumulator
+// register r of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// blockIdx.z selects a K range of kchunk (split K); with gridDim.z > 1 the
+// tile goes to part[z][t][m] and matbatch_reduce_kernel adds the ranges in
+// order.
+constexpr int kMfKs = 64;
+constexpr int kMfLd = kMfKs + 8;  // halves per LDS row (16-byte aligned, staggers banks)
+constexpr int32_t kMfOob = 0x7ffffff0;  // a buffer offset past any resource
+
+template <int TYPE, int WM, int WN>
+__global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __restrict w, size_t rbytes,
+                                                            const _Float16* __restrict xh, int32_t b, int32_t k,
+                                                            int32_t n, float* __restrict y, int32_t kchunk,
+                                                            float* __restrict part) {
+    constexpr int BM = 64 * WM, BN = 64 * WN;
+    constexpr int XCH = BM * 8 / 256;  // 16-byte activation chunks per thread and step
+    __shared__ __align__(16) _Float16 xs[2][BM * kMfLd];
+    __shared__ __align__(16) _Float16 ws[2][BN * kMfLd];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv & 1, wn = wv >> 1;
+    const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int32_t kb = blockIdx.z * kchunk;
+    const int32_t ke = min(k, kb + kchunk);
+    const int32_t nsteps = (ke - kb + kMfKs - 1) / kMfKs;
+
+    floatx16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // activation chunks c = tid + 256 i: token row c / 8 of the tile, halves
+    // 8 (c % 8) .. + 8 of the step; one resource over the tile's token rows
+    const int32_t rows_here = min(BM, b - t0);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(xh + static_cast<size_t>(t0) * k), static_cast<short>(0),
+        rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    // weight segment tid (row tid / 2 of the tile, 32 values at 32 (tid % 2))
+    // for tid < 2 BN, through one resource over the tile's rows
+    const int wrow = tid >> 1, wseg = tid & 1;
+    const int32_t wrows_here = min(BN, n - n0);
+    TileRow wrs;
+    wrs.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes),
+                                              static_cast<short>(0),
+                                              wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
+    wrs.base = tid < 2 * BN && wrow < wrows_here ? wrow * static_cast<int32_t>(rbytes) : kMfOob / 2;
+
+    uint4 xr[XCH];
+    WRaw<TYPE> wr[2];
+    // activation chunks of one step; past the range an offset past the
+    // resource reads zeros
+    auto gload_x = [&](int32_t k0) {
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int c = tid + 256 * i, r = c >> 3, seg = c & 7;
+            const int32_t kx = k0 + 8 * seg;
+            const int32_t off = kx < ke ? (r * k + kx) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+            xr[i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    };
+    // raw weight blocks of one step into register set `set`; past the range
+    // a row offset past the resource reads zeros (k, ke are multiples of 32)
+    auto gload_w = [&](int set, int32_t k0) {
+        const int32_t kw = k0 + 32 * wseg;
+        wr[set].load(wrs, kw < ke ? kw : 1 << 24);
+    };
+    auto lstore = [&](int set, int buf, int32_t k0) {
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int c = tid + 256 * i, r = c >> 3, seg = c & 7;
+            *reinterpret_cast<uint4*>(&xs[buf][r * kMfLd + 8 * seg]) = xr[i];
+        }
+        if (tid < 2 * BN) {
+            uint32_t o[16];
+            const int32_t kw = k0 + 32 * wseg;
+            wr[set].get(kw < ke ? kw : 0, o);
+            uint4* dst = reinterpret_cast<uint4*>(&ws[buf][wrow * kMfLd + 32 * wseg]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        }
+    };
+
+    const int li = lane & 31, lk = 8 * (lane >> 5);
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < kMfKs; kk += 16) {
+            half8 av[WM], bv[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                av[i] = *reinterpret_cast<const half8*>(&xs[buf][(wm * 32 * WM + 32 * i + li) * kMfLd + kk + lk]);
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                bv[j] = *reinterpret_cast<const half8*>(&ws[buf][(wn * 32 * WN + 32 * j + li) * kMfLd + kk + lk]);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Activations are loaded one step ahead, raw weight blocks two steps
+    // ahead in two register sets.  Each step issues the activation loads
+    // before the weight loads: loads retire in order, so the wait before
+    // writing step s + 1 to LDS does not cover step s + 2's weights.  Steps go
+    // in pairs so that register-set and buffer indices are compile-time
+    // constants; loads past the range read nothing.
+    gload_x(kb);
+    gload_w(0, kb);
+    gload_w(1, kb + kMfKs);
+    lstore(0, 0, kb);
+    __syncthreads();
+    for (int32_t s = 0; s < nsteps; s += 2) {
+        const int32_t k0 = kb + s * kMfKs;
+        gload_x(k0 + kMfKs);
+        gload_w(0, k0 + 2 * kMfKs);
+        compute(0);
+        if (s + 1 < nsteps) lstore(1, 1, k0 + kMfKs);
+        __syncthreads();
+        if (s + 1 >= nsteps) break;
+        gload_x(k0 + 2 * kMfKs);
+        gload_w(1, k0 + 3 * kMfKs);
+        compute(1);
+        if (s + 2 < nsteps) lstore(0, 0, k0 + 2 * kMfKs);
+        __syncthreads();
+    }
+    float* dst = gridDim.z > 1 ? part + static_cast<size_t>(blockIdx.z) * b * n : y;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int32_t mm = n0 + wn * 32 * WN + 32 * j + li;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r];
+            }
+        }
+}
+
+// y = sum over the split K ranges, added in range order (deterministic)
+__global__ __launch_bounds__(kThreads) void matbatch_reduce_kernel(const float* __restrict part, int32_t splits,
+                                                                   size_t count, float* __restrict y) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kThreads) {
+        float acc = part[i];
+        for (int32_t z = 1; z < splits; ++z) acc += part[static_cast<size_t>(z) * count + i];
+        y[i] = acc;
+    }
+}
+
+struct MfmaPlan {
+    int wm, wn;
+    int32_t splits, kchunk;
+};
+
+// Largest tile whose grid fills every CU with as many work-groups as its LDS
+// lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for 64 x 64); otherwise
+// 64 x 64 tiles with K split until it does (ranges of at least 256).
+// (A 256 x 128 tile, 478 registers per lane and 110 KB of LDS, is not used:
+// its one launch ended the host process with a segmentation fault whose cause
+// was not found.)
+MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
+    auto tiles = [&](int wm, int wn) {
+        return static_cast<int64_t>((n + 64 * wn - 1) / (64 * wn)) * ((b + 64 * wm - 1) / (64 * wm));
+    };
+    const int cand[3][3] = {{2, 2, 2}, {2, 1, 2}, {1, 1, 4}};
+    for (const auto& c : cand)
+        if (tiles(c[0], c[1]) >= 256 * c[2]) return {c[0], c[1], 1, k};
+    const int64_t t = tiles(1, 1);
+    int32_t splits = static_cast<int32_t>((1024 + t - 1) / t);
+    const int32_t max_splits = k / 256 > 0 ? k / 256 : 1;
+    if (splits > max_splits) splits = max_splits;
+    int32_t kchunk = (k + splits - 1) / splits;
+    kchunk = (kchunk + kMfKs - 1) / kMfKs * kMfKs;
+    splits = (k + kchunk - 1) / kchunk;
+    return {1, 1, splits, kchunk};
+}
+
+template <int TYPE, int WM, int WN>
+hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xh, int32_t b, int32_t k, int32_t n, float* y,
+                         const MfmaPlan& p, float* part, hipStream_t stream) {
+    const dim3 grid((n + 64 * WN - 1) / (64 * WN), (b + 64 * WM - 1) / (64 * WM), p.splits);
+    hipLaunchKernelGGL((matbatch_mfma_kernel<TYPE, WM, WN>), grid, dim3(256), 0, stream, w, row_bytes(TYPE, k), xh,
+                       b, k, n, y, p.kchunk, part);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xh,
+                       float* part, hipStream_t stream) {
+    const dim3 qgrid((k / 4 + kThreads - 1) / kThreads, b);
+    hipLaunchKernelGGL(act_f16_kernel, qgrid, dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xh));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const MfmaPlan p = mfma_plan(b, k, n);
+    if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, b, k, n, y, p, part, stream);
+    else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xh, b, k, n, y, p, part, stream);
+    else e = launch_mfma_t<TYPE, 1, 1>(w, xh, b, k, n, y, p, part, stream);
+    if (e != hipSuccess || p.splits == 1) return e;
+    const size_t count = static_cast<size_t>(b) * n;
+    size_t g = (count + kThreads - 1) / kThreads;
+    if (g > 4096) g = 4096;
+    hipLaunchKernelGGL(matbatch_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(kThreads), 0, stream, part,
+                       p.splits, count, y);
+    return hipGetLastError();
+}
+
 template <int TYPE>
 hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, int8_t* q,
                     ActMeta* meta, hipStream_t stream) {
@@ -63,19 +449,25 @@ hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int3
 
 }  // namespace
 
-size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k) {
+// fp16 quantised activations [B x K], then the split-K partials [splits x B x N]
+static size_t xh_bytes(int32_t b, int32_t k) {
+    return (static_cast<size_t>(b) * k * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
+}
+
+size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n) {
     if (type == kBF16) return 256;
-    const size_t qbytes = (static_cast<size_t>(b) * k + 255) & ~static_cast<size_t>(255);
-    return qbytes + static_cast<size_t>(b) * (k / 32) * sizeof(ActMeta) + 256;
+    const MfmaPlan p = mfma_plan(b, k, n);
+    const size_t parts = p.splits > 1 ? static_cast<size_t>(p.splits) * b * n * sizeof(float) : 0;
+    return xh_bytes(b, k) + parts + 256;
 }
 
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n,
                            float* y, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (b <= 0 || n <= 0) return hipSuccess;
-    if (k <= 0 || b > 65535) return hipErrorInvalidValue;
+    if (k <= 0 || k > (1 << 20) || b > 65535) return hipErrorInvalidValue;  // keeps buffer offsets in int32
     if (type != kBF16 && (k % 32) != 0) return hipErrorInvalidValue;
     if ((type == kQ4_K || type == kQ6_K) && (k % 256) != 0) return hipErrorInvalidValue;
-    if (workspace_bytes < matbatch_workspace_bytes(type, b, k)) return hipErrorInvalidValue;
+    if (workspace_bytes < matbatch_workspace_bytes(type, b, k, n)) return hipErrorInvalidValue;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return hipErrorInvalidValue;
     if (type == kQ4_K || type == kBF16) {
@@ -83,17 +475,15 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     } else if ((wa & 3u) != 0) {
         return hipErrorInvalidValue;
     }
-    int8_t* q = static_cast<int8_t*>(workspace);
-    const size_t qbytes = (static_cast<size_t>(b) * k + 255) & ~static_cast<size_t>(255);
-    ActMeta* meta = reinterpret_cast<ActMeta*>(static_cast<char*>(workspace) + qbytes);
-    if (type != kBF16 && qbytes + static_cast<size_t>(b) * (k / 32) * sizeof(ActMeta) > workspace_bytes)
-        return hipErrorInvalidValue;
+    _Float16* xh = static_cast<_Float16*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k));
+    if ((reinterpret_cast<uintptr_t>(xh) & 255u) != 0) return hipErrorInvalidValue;
     switch (type) {
-    case kQ4_0: return launch_t<kQ4_0>(w, x, b, k, n, y, q, meta, stream);
-    case kQ8_0: return launch_t<kQ8_0>(w, x, b, k, n, y, q, meta, stream);
-    case kQ4_K: return launch_t<kQ4_K>(w, x, b, k, n, y, q, meta, stream);
-    case kQ6_K: return launch_t<kQ6_K>(w, x, b, k, n, y, q, meta, stream);
-    case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, q, meta, stream);
+    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xh, part, stream);
+    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xh, part, stream);
+    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xh, part, stream);
+    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xh, part, stream);
+    case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }
 }

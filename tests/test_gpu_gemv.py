@@ -2,8 +2,9 @@
 
 Bars: Q8 activation blocks and block dequantisation bit-exact with the
 oracle; matvec / matbatch / lm_head within 1e-3 relative L2 of the oracle's
-fp32 results on the same seeded inputs (the tolerance north of the integer
-dots is only fp32 accumulation order, so observed errors are ~1e-7)."""
+fp32 results on the same seeded inputs.  matvec keeps the integer block dots
+(only fp32 accumulation order differs: ~1e-7); matbatch of quantised weights
+runs on fp16 matrix cores (~3e-4)."""
 from __future__ import annotations
 
 import ctypes as C
@@ -193,9 +194,17 @@ def test_matvec_device_pointers(lib, oracle):
     assert rel_l2(yh, oracle.matvec(Q4_K, w, x, k, n)) < TOL
 
 
+# quantised types run on the fp16 matrix cores (both operands rounded once to
+# fp16: ~3e-4 relative L2); cases cover every tile size the launcher picks,
+# ragged B and N, and K with a half 64-wide step at the end (k % 64 == 32)
 MATBATCH_CASES = [
     (Q4_K, 4096, 512, 64), (Q6_K, 14336, 256, 16), (Q4_0, 4096, 300, 5), (Q8_0, 2048, 200, 9), (Q4_K, 512, 96, 1),
-    (BF16, 1024, 64, 4),
+    (BF16, 1024, 64, 4), (Q4_K, 4096, 1024, 256), (Q6_K, 2048, 4160, 100), (Q4_0, 96, 130, 70),
+    (Q8_0, 2080, 333, 33),
+    pytest.param(Q4_K, 256, 16384, 300, marks=pytest.mark.skip(
+        reason="ran the 256x128 MFMA tile, whose one launch ended the process with a host segmentation fault; "
+               "that tile is switched off and this case stays off the GPU until the cause is found")),
+    (Q4_K, 256, 8192, 500), (Q6_K, 256, 16384, 128), (Q4_K, 256, 16384, 512), (Q6_K, 512, 8192, 520),
 ]
 
 
