@@ -28,6 +28,8 @@ namespace {
 
 using namespace dev;
 
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHeadBlock = 4;     // query heads handled per pass (one wave each in the softmax)
@@ -245,6 +247,157 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     }
 }
 
+// Large query-head groups (G = n_heads / n_kv_heads >= 16, head_dim 128),
+// e.g. MQA: the G query heads of one KV head are the M dimension of two small
+// fp32 matrix products per 64-token sub-chunk, S = Q K^T and O += P V
+// (v_mfma_f32_32x32x2f32, fp32 throughout like the reference), so every K/V
+// row is read from HBM once.  One work-group (4 waves) owns (KV head, chunk);
+// it walks the chunk in sub-chunks with an online softmax (running max and sum
+// per head, O rescaled by e^(m_old - m_new)) and leaves the same (o, max, sum)
+// partials as attn_chunk_kernel for attn_merge_kernel.
+//   S: wave w computes tokens 32 (w % 2) .. + 32 over dims 64 (w / 2) .. + 64;
+//      lane l holds Q[l % 32][d] and K[t][d] for the 32 dims d of its half
+//      (the order of d inside a dot is free: half g = l / 32 takes dims
+//      64 (w / 2) + 32 g .. + 32), the two dim halves meet in LDS.
+//   P V: wave w owns output dims 32 w .. + 32; lane l reads P[l % 32][t] from
+//      LDS and V[t][32 w + l % 32] from HBM for tokens t = 32 g + kk.
+// MFMA layouts (32x32x2 f32): A[l % 32][l / 32], B[l / 32][l % 32], accumulator
+// register r of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+constexpr int kMqSub = 64;
+constexpr int kMqHeads = 32;
+constexpr int kMqLd = kMqSub + 4;
+
+__global__ __launch_bounds__(kThreads) void attn_mq_kernel(AttnParams p) {
+    constexpr int HD = 128;
+    __shared__ __align__(16) float spart[2][kMqHeads][kMqLd];
+    __shared__ __align__(16) float pl[kMqHeads][kMqLd];
+    __shared__ float alpha_s[kMqHeads], m_s[kMqHeads], l_s[kMqHeads];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 31, g = lane >> 5;
+    const int G = p.n_heads / p.n_kv;
+    const int hk = blockIdx.x, split = blockIdx.y;
+    const int ta = p.t0 + split * p.chunk;
+    const int tb = min(p.t1, ta + p.chunk);
+    const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
+    const bool have_new = p.use_new != 0;
+
+    // the work-group whose chunk holds `pos` stores the new K/V row; its own
+    // reads of token pos below take k_new / v_new directly
+    if (have_new && p.pos >= ta && p.pos < tb) {
+        float* kd = p.k_cache + static_cast<size_t>(p.pos) * kv_dim + static_cast<size_t>(hk) * HD;
+        float* vd = p.v_cache + static_cast<size_t>(p.pos) * kv_dim + static_cast<size_t>(hk) * HD;
+        for (int i = tid; i < HD; i += kThreads) {
+            kd[i] = p.k_new[static_cast<size_t>(hk) * HD + i];
+            vd[i] = p.v_new[static_cast<size_t>(hk) * HD + i];
+        }
+    }
+    auto krow = [&](int t) -> const float* {
+        return (have_new && t == p.pos) ? p.k_new + static_cast<size_t>(hk) * HD
+                                        : p.k_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD;
+    };
+    auto vrow = [&](int t) -> const float* {
+        return (have_new && t == p.pos) ? p.v_new + static_cast<size_t>(hk) * HD
+                                        : p.v_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD;
+    };
+
+    const int tt = wv & 1, dh = wv >> 1;
+    const int dq = 64 * dh + 32 * g;  // first dim of this lane's half in the S phase
+    float qa[32];
+    if (li < G) {
+        const float* qr = p.q + (static_cast<size_t>(hk) * G + li) * HD + dq;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(qr + 4 * i);
+            qa[4 * i] = v.x; qa[4 * i + 1] = v.y; qa[4 * i + 2] = v.z; qa[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qa[i] = 0.0f;
+    }
+    if (tid < kMqHeads) {
+        m_s[tid] = -1e30f;
+        l_s[tid] = 0.0f;
+    }
+    floatx16 o;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] = 0.0f;
+    __syncthreads();
+
+    for (int sa = ta; sa < tb; sa += kMqSub) {
+        // ---- S partials over this wave's dim half ----
+        {
+            const int tok = sa + 32 * tt + li;
+            const float* kr = krow(tok < tb ? tok : tb - 1) + dq;
+            float kb[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(kr + 4 * i);
+                kb[4 * i] = v.x; kb[4 * i + 1] = v.y; kb[4 * i + 2] = v.z; kb[4 * i + 3] = v.w;
+            }
+            floatx16 sacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[kk], kb[kk], sacc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) spart[dh][8 * (r >> 2) + 4 * g + (r & 3)][32 * tt + li] = sacc[r];
+        }
+        __syncthreads();
+        // ---- online softmax: wave w updates heads 8 w .. 8 w + 7, lane = token ----
+#pragma unroll
+        for (int hh = 0; hh < 8; ++hh) {
+            const int h = 8 * wv + hh;
+            const bool valid = sa + lane < tb;
+            const float sv = valid ? (spart[0][h][lane] + spart[1][h][lane]) * p.scale : -1e30f;
+            float mx = sv;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            const float m_old = m_s[h];
+            const float m_new = fmaxf(m_old, mx);
+            const float e = valid ? expf(sv - m_new) : 0.0f;
+            const float sum = wave_sum(e);
+            pl[h][lane] = e;
+            if (lane == 0) {
+                const float a = expf(m_old - m_new);
+                alpha_s[h] = a;
+                l_s[h] = l_s[h] * a + sum;
+                m_s[h] = m_new;
+            }
+        }
+        __syncthreads();
+        // ---- O = O e^(m_old - m_new) + P V over this wave's 32 dims ----
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[r] *= alpha_s[8 * (r >> 2) + 4 * g + (r & 3)];
+            float pa[32], vb[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(&pl[li][32 * g + 4 * i]);
+                pa[4 * i] = v.x; pa[4 * i + 1] = v.y; pa[4 * i + 2] = v.z; pa[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) {
+                const int t = sa + 32 * g + kk;
+                vb[kk] = vrow(t < tb ? t : tb - 1)[32 * wv + li];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[kk], vb[kk], o, 0, 0, 0);
+        }
+        __syncthreads();  // spart / pl / alpha are rewritten by the next sub-chunk
+    }
+    // partials: unnormalised o, and (max, sum) per head
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int h = 8 * (r >> 2) + 4 * g + (r & 3);
+        if (h < G) p.part_o[(static_cast<size_t>(split) * p.n_heads + hk * G + h) * HD + 32 * wv + li] = o[r];
+    }
+    if (tid < G) {
+        float* ml = p.part_ml + (static_cast<size_t>(split) * p.n_heads + hk * G + tid) * 2;
+        ml[0] = m_s[tid];
+        ml[1] = l_s[tid];
+    }
+}
+
 // out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12), one
 // work-group per query head: the split weights e^(m_j - M) are formed once in
 // LDS, then each thread sums a strided subset of splits for one dimension.
@@ -374,6 +527,47 @@ hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* pa
     return hipGetLastError();
 }
 
+// Chunks of whole 64-token sub-chunks, about one work-group per CU.
+Plan make_mq_plan(int32_t pos, int32_t sw, int32_t n_kv) {
+    Plan pl;
+    pl.t0 = sw > 0 ? (pos - sw + 1 > 0 ? pos - sw + 1 : 0) : 0;
+    pl.t1 = pos + 1;
+    const int32_t win = pl.t1 - pl.t0;
+    int32_t want = 256 / (n_kv > 0 ? n_kv : 1);
+    if (want < 1) want = 1;
+    int32_t chunk = (win + want - 1) / want;
+    chunk = ((chunk + kMqSub - 1) / kMqSub) * kMqSub;
+    while ((win + chunk - 1) / chunk > kMergeMaxSplit) chunk += kMqSub;
+    pl.chunk = chunk;
+    pl.n_split = (win + chunk - 1) / chunk;
+    return pl;
+}
+
+hipError_t launch_mq(const AttnArgs& a, const Plan& pl, float* part_o, float* part_ml, hipStream_t stream) {
+    AttnParams p{};
+    p.q = a.q;
+    p.k_new = a.k_new;
+    p.v_new = a.v_new;
+    p.k_cache = a.k_cache;
+    p.v_cache = a.v_cache;
+    p.part_o = part_o;
+    p.part_ml = part_ml;
+    p.pos = a.pos;
+    p.n_heads = a.n_heads;
+    p.n_kv = a.n_kv_heads;
+    p.t0 = pl.t0;
+    p.t1 = pl.t1;
+    p.chunk = pl.chunk;
+    p.use_new = (a.write_kv && a.k_new && a.v_new) ? 1 : 0;
+    p.scale = a.scale;
+    hipLaunchKernelGGL(attn_mq_kernel, dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml,
+                       pl.n_split, a.n_heads, 128, a.out);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window) {
@@ -390,12 +584,16 @@ hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace
     const uintptr_t al = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k_cache) |
                          reinterpret_cast<uintptr_t>(a.v_cache) | reinterpret_cast<uintptr_t>(a.out);
     if (al & 15u) return hipErrorInvalidValue;
-    const Plan pl = make_plan(a.pos, a.sliding_window, a.n_kv_heads, a.n_heads / a.n_kv_heads, a.head_dim);
+    const int32_t G = a.n_heads / a.n_kv_heads;
+    const bool mq = a.head_dim == 128 && G >= 16 && G <= kMqHeads && !a.norm_qk && !a.rope;
+    const Plan pl = mq ? make_mq_plan(a.pos, a.sliding_window, a.n_kv_heads)
+                       : make_plan(a.pos, a.sliding_window, a.n_kv_heads, G, a.head_dim);
     const size_t need_o = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * a.head_dim;
     const size_t need_ml = sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * 2;
     if (need_o + need_ml > workspace_bytes) return hipErrorInvalidValue;
     float* part_o = static_cast<float*>(workspace);
     float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + need_o);
+    if (mq) return launch_mq(a, pl, part_o, part_ml, stream);
     switch (a.head_dim) {
     case 64: return launch_hd<64>(a, pl, part_o, part_ml, stream);
     case 128: return launch_hd<128>(a, pl, part_o, part_ml, stream);

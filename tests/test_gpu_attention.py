@@ -40,7 +40,11 @@ def test_attention_reference_vectors(lib, golden, tag):
 # config 4: 32 Q / 8 KV heads x 128, ctx 512 / 4096 / 32768, SWA 1024, MQA
 CASES = [(32, 8, 128, 512, 0), (32, 8, 128, 4096, 0), (32, 8, 128, 32768, 0), (32, 8, 128, 4096, 1024),
          (32, 8, 128, 32768, 1024), (32, 1, 128, 4096, 0), (32, 1, 128, 32768, 0), (16, 16, 64, 300, 0),
-         (8, 2, 256, 700, 100), (4, 4, 128, 1, 0)]
+         (8, 2, 256, 700, 100), (4, 4, 128, 1, 0),
+         # query-head groups of 16..32 (matrix-core kernel): one token, ragged
+         # sliding window, 16 heads padded to 32, two KV heads, partial sub-chunk
+         (32, 1, 128, 1, 0), (32, 1, 128, 100, 50), (16, 1, 128, 333, 0), (64, 2, 128, 2000, 0),
+         (32, 2, 128, 129, 0)]
 
 
 @pytest.mark.parametrize("H,KV,hd,ctx,sw", CASES)
@@ -61,9 +65,10 @@ def test_attention_parity(lib, oracle, H, KV, hd, ctx, sw):
     lib.gncx_hip_kv_forget(None)
 
 
-def test_attention_write_kv_off_uses_cached_row(lib, oracle):
+@pytest.mark.parametrize("H,KV", [(8, 2), (32, 1)])
+def test_attention_write_kv_off_uses_cached_row(lib, oracle, H, KV):
     rng = np.random.default_rng(3)
-    H, KV, hd, ctx = 8, 2, 128, 64
+    hd, ctx = 128, 64
     kc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
     vc = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
     q = rng.standard_normal(H * hd, dtype=np.float32)
