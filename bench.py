@@ -11,7 +11,9 @@ rotated so the working set (> 512 MB) cannot sit in the 256 MB Infinity Cache.
 Also reported: `roofline` of that kernel (HIP-event durations on the
 library's stream), `cpu_baseline` (the reference library compiled from its
 own source, timed on this host on a bounded sample), and `extra` figures for
-the other decode GEMV shapes and the decode-attention step.
+the other decode GEMV shapes, the decode-attention step, matbatch at B = 64,
+256 and 512, and decode tok/s of a Qwen3-8B-shaped model (2048-token prompt
+prefilled, then 256 greedy tokens) through the streamer's call sequence.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-extra]
 """
@@ -186,6 +188,55 @@ def time_attention(lib, torch, H, KV, hd, ctx, sw, steps, copies):
     return {"us_per_step": wall_us, "bytes": nbytes, "gbps": nbytes / (wall_us * 1e-6) / 1e9}
 
 
+def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
+    """Qwen3-8B-shaped random-init model (decode.QWEN3_8B): prefill a random
+    prompt through the streamer's prefill call sequence, then greedy decode
+    steps through forward_token's; the unchanged call sequence and the fused
+    attention entry each decode n_tokens.  Wall-clock, synchronised around
+    each timed loop (the greedy argmax synchronises every token anyway)."""
+    import gncx_amd.decode as dec
+    t0 = time.perf_counter()
+    model = dec.build_model(torch, dec.QWEN3_8B, seed=seed)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    s = dec.QWEN3_8B
+    g = torch.Generator().manual_seed(seed + 1)
+    prompt = torch.randint(0, s.vocab, (prompt_len,), generator=g).tolist()
+    d = dec.Decoder(lib, torch, model, max_seq=prompt_len + 2 * n_tokens + 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = d.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    pkg.check(lib)
+    res = {}
+    pos = prompt_len
+    tok = d.greedy(logits)
+    for fused in (False, True):
+        d.fused = fused
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_tokens):
+            tok = d.greedy(d.forward_token(tok, pos))
+            pos += 1
+        torch.cuda.synchronize()
+        res[fused] = (time.perf_counter() - t0) / n_tokens
+        pkg.check(lib)
+    weight_bytes = model.blob.numel()
+    kv_bytes = 2 * s.n_layers * s.kv_dim * 4 * (prompt_len + n_tokens)  # K and V rows read at the mid position
+    del d, model
+    torch.cuda.empty_cache()
+    return {"decode_tok_s": round(1.0 / res[False], 1), "decode_ms_per_token": round(res[False] * 1e3, 3),
+            "decode_tok_s_fused_attention": round(1.0 / res[True], 1),
+            "hbm_gbps_effective": round((weight_bytes + kv_bytes) / res[False] / 1e9, 1),
+            "prefill_tokens": prompt_len, "prefill_s": round(prefill_s, 3),
+            "prefill_tok_s": round(prompt_len / prefill_s, 1), "decode_tokens_each": n_tokens,
+            "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
+            "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
+                     "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",
+            "positions": f"{prompt_len}..{pos - 1}"}
+
+
 def cpu_baseline(pkg, t, k, n, w_host, x_host, seconds=10.0):
     """The reference's own matvec (compiled from its source) on this host's
     cores with its default pool size, clamp(hardware threads, 2, 12)
@@ -230,6 +281,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-prompt", type=int, default=2048)
+    ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -293,6 +347,8 @@ def main() -> int:
             for bb in (64, 256, 512):
                 mb[f"{name}_b{bb}"] = time_matbatch(pkg, lib, torch, tt, kk, nn, bb, 20, 4)
         extra["matbatch"] = mb
+    if not args.no_decode:
+        extra["decode_qwen3_8b"] = time_decode(pkg, lib, torch, args.decode_prompt, args.decode_tokens)
 
     cpu = None if args.no_cpu else cpu_baseline(pkg, t, k, n, head["w_host"], head["x_host"], args.cpu_seconds)
     line = {

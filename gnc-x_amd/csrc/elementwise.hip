@@ -73,6 +73,10 @@ __global__ void swiglu_kernel(const float* __restrict g, const float* __restrict
     }
 }
 
+__global__ void vec_add_kernel(float* __restrict y, const float* __restrict x, int32_t n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] += x[i];
+}
+
 __global__ void softcap_kernel(float* __restrict y, int32_t n, float cap) {
     const float inv = __fdiv_rn(1.0f, cap);
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
@@ -171,6 +175,12 @@ hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_hea
     if (work == 0) return hipSuccess;
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(work, 256)), dim3(256), 0, stream, q, k, table, n_heads,
                        n_kv_heads, head_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_vec_add(float* y, const float* x, int32_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(vec_add_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, y, x, n);
     return hipGetLastError();
 }
 

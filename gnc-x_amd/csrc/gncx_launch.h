@@ -81,6 +81,7 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int3
 hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_heads,
                        int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
 // SiLU(gate)*up (reference cpp:2038-2052).
+hipError_t launch_vec_add(float* y, const float* x, int32_t n, hipStream_t stream);
 hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* out,
                          hipStream_t stream);
 // tanh softcap in place (reference cpp:1726-1731).

@@ -710,6 +710,24 @@ GNCX_API void gncx_swiglu_activation(const float* gate_vec, const float* up_vec,
     finish_out(out_ffn_vec, o, ffn_dim, host, where);
 }
 
+// y[i] += x[i]: the residual adds the streamer does on the host
+// (lua/gncx_streamer.lua:871-873, 906-908), on the device.
+GNCX_API void gncx_hip_vec_add(float* y, const float* x, int32_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_vec_add";
+    if (n <= 0 || !y || !x || !ensure_runtime(where)) return;
+    const float* xd = stage_in(x, n, g_rt.k, where);
+    if (!xd) return;
+    const bool host_y = !is_device_ptr(y);
+    float* yd = y;
+    if (host_y) {
+        yd = const_cast<float*>(stage_in(y, n, g_rt.o, where));
+        if (!yd) return;
+    }
+    if (!check(launch_vec_add(yd, xd, n, g_rt.stream), where)) return;
+    finish_out(y, yd, n, host_y, where);
+}
+
 namespace {
 // cpp:693-780: one row of the embedding table, decoded on the device.
 void fetch_embedding(int32_t type, const uint8_t* base, size_t off, int32_t token, int32_t dim, float scale,

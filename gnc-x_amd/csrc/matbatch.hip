@@ -7,8 +7,9 @@
 //
 // Quantised weights (Q4_0, Q8_0, Q4_K, Q6_K) go through the matrix cores:
 //   1. act_f16_kernel quantises each token row exactly as the reference does
-//      and stores the quantised activations q * d as fp16 [B x K] (one
-//      rounding of an exactly quantised value),
+//      and stores the quantised activations q * d / s as fp16 [B x K] (one
+//      rounding of an exactly quantised value; s is a power-of-two row scale
+//      the MFMA epilogue multiplies back),
 //   2. matbatch_mfma_kernel streams 64-wide K steps: the work-group's weight
 //      rows are dequantised block by block (fp32 arithmetic, one fp16
 //      rounding) into LDS, its token rows are copied into LDS, and each wave
@@ -68,19 +69,42 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
     return lo | (hi << 16);
 }
 
-// fp16(q * d) of the reference's per-32 quantisation of row blockIdx.y of x
-// (cpp:955-995): 8 lanes per block, 4 values per lane.
+// fp16(q * d / s) of the reference's per-32 quantisation of row blockIdx.x of
+// x (cpp:955-995), with s the power of two at or above the row's largest |x|
+// (stored in rscale; the MFMA epilogue multiplies by it again).  The exact
+// rescale puts every value in [-1, 1], so activations far beyond fp16's range
+// (SwiGLU outputs of 1e5 and more) keep fp16's relative precision.  One
+// work-group per row: the row maximum first, then 8 lanes per 32-block,
+// 4 values per lane.
 __global__ __launch_bounds__(kThreads) void act_f16_kernel(const float* __restrict x, int32_t k,
-                                                           uint2* __restrict xh) {
-    const int32_t t = blockIdx.x * kThreads + threadIdx.x;  // task: 4 values
-    if (t >= k / 4) return;  // whole 8-lane groups leave together (k % 32 == 0)
-    const size_t at = static_cast<size_t>(blockIdx.y) * (k / 4) + t;
-    const float4 v = reinterpret_cast<const float4*>(x)[at];
-    int q0, q1, q2, q3;
-    float d;
-    quantize_values(v, q0, q1, q2, q3, d);
-    xh[at] = make_uint2(pack_half2(static_cast<float>(q0) * d, static_cast<float>(q1) * d),
-                        pack_half2(static_cast<float>(q2) * d, static_cast<float>(q3) * d));
+                                                           uint2* __restrict xh, float* __restrict rscale) {
+    __shared__ float red[kThreads / 64];
+    const int32_t row = blockIdx.x, tasks = k / 4;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
+    float m = 0.0f;
+    for (int32_t t = threadIdx.x; t < tasks; t += kThreads) {
+        const float4 v = xr[t];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
+    const float sc = m > 0.0f && m <= 3.0e38f ? ldexpf(1.0f, ilogbf(m) + 1) : 1.0f;  // power of two > m
+    const float inv = 1.0f / sc;                                       // exact
+    if (threadIdx.x == 0) rscale[row] = sc;
+    uint2* out = xh + static_cast<size_t>(row) * tasks;
+    // whole 8-lane groups take the same trip count (tasks and kThreads are multiples of 8)
+    for (int32_t t = threadIdx.x; t < tasks; t += kThreads) {
+        int q0, q1, q2, q3;
+        float d;
+        quantize_values(xr[t], q0, q1, q2, q3, d);
+        out[t] = make_uint2(pack_half2(static_cast<float>(q0) * d * inv, static_cast<float>(q1) * d * inv),
+                            pack_half2(static_cast<float>(q2) * d * inv, static_cast<float>(q3) * d * inv));
+    }
 }
 
 // Weights e0 .. e0 + 31 (e0 a multiple of 32) of one row: raw block bytes
@@ -234,7 +258,8 @@ constexpr int32_t kMfOob = 0x7ffffff0;  // a buffer offset past any resource
 
 template <int TYPE, int WM, int WN>
 __global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __restrict w, size_t rbytes,
-                                                            const _Float16* __restrict xh, int32_t b, int32_t k,
+                                                            const _Float16* __restrict xh,
+                                                            const float* __restrict rscale, int32_t b, int32_t k,
                                                             int32_t n, float* __restrict y, int32_t kchunk,
                                                             float* __restrict part) {
     constexpr int BM = 64 * WM, BN = 64 * WN;
@@ -361,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r];
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rscale[t];
             }
         }
 }
@@ -406,25 +431,24 @@ MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
 }
 
 template <int TYPE, int WM, int WN>
-hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xh, int32_t b, int32_t k, int32_t n, float* y,
-                         const MfmaPlan& p, float* part, hipStream_t stream) {
+hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xh, const float* rscale, int32_t b, int32_t k,
+                         int32_t n, float* y, const MfmaPlan& p, float* part, hipStream_t stream) {
     const dim3 grid((n + 64 * WN - 1) / (64 * WN), (b + 64 * WM - 1) / (64 * WM), p.splits);
     hipLaunchKernelGGL((matbatch_mfma_kernel<TYPE, WM, WN>), grid, dim3(256), 0, stream, w, row_bytes(TYPE, k), xh,
-                       b, k, n, y, p.kchunk, part);
+                       rscale, b, k, n, y, p.kchunk, part);
     return hipGetLastError();
 }
 
 template <int TYPE>
 hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xh,
-                       float* part, hipStream_t stream) {
-    const dim3 qgrid((k / 4 + kThreads - 1) / kThreads, b);
-    hipLaunchKernelGGL(act_f16_kernel, qgrid, dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xh));
+                       float* rscale, float* part, hipStream_t stream) {
+    hipLaunchKernelGGL(act_f16_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xh), rscale);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
-    if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, b, k, n, y, p, part, stream);
-    else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xh, b, k, n, y, p, part, stream);
-    else e = launch_mfma_t<TYPE, 1, 1>(w, xh, b, k, n, y, p, part, stream);
+    if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, rscale, b, k, n, y, p, part, stream);
+    else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
+    else e = launch_mfma_t<TYPE, 1, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     const size_t count = static_cast<size_t>(b) * n;
     size_t g = (count + kThreads - 1) / kThreads;
@@ -449,16 +473,18 @@ hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int3
 
 }  // namespace
 
-// fp16 quantised activations [B x K], then the split-K partials [splits x B x N]
+// fp16 quantised activations [B x K], their row scales [B], then the split-K
+// partials [splits x B x N]
 static size_t xh_bytes(int32_t b, int32_t k) {
     return (static_cast<size_t>(b) * k * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
 }
+static size_t rscale_bytes(int32_t b) { return (static_cast<size_t>(b) * sizeof(float) + 255) & ~static_cast<size_t>(255); }
 
 size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n) {
     if (type == kBF16) return 256;
     const MfmaPlan p = mfma_plan(b, k, n);
     const size_t parts = p.splits > 1 ? static_cast<size_t>(p.splits) * b * n * sizeof(float) : 0;
-    return xh_bytes(b, k) + parts + 256;
+    return xh_bytes(b, k) + rscale_bytes(b) + parts + 256;
 }
 
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n,
@@ -476,13 +502,14 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
         return hipErrorInvalidValue;
     }
     _Float16* xh = static_cast<_Float16*>(workspace);
-    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k));
+    float* rscale = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k));
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xh) & 255u) != 0) return hipErrorInvalidValue;
     switch (type) {
-    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xh, part, stream);
-    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xh, part, stream);
-    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xh, part, stream);
-    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xh, part, stream);
+    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xh, rscale, part, stream);
+    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xh, rscale, part, stream);
+    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xh, rscale, part, stream);
+    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xh, rscale, part, stream);
     case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }

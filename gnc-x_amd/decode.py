@@ -1,0 +1,280 @@
+"""Qwen3-shaped prefill and decode through the reference C-ABI.
+
+A replay driver: it issues, call for call, what GNCXStreamer:forward_token
+(lua/gncx_streamer.lua:759-965) and GNCXStreamer:prefill (:968-1208) issue for
+a Qwen3 model (the `is_qwen` branches: per-head Q/K RMSNorm, NEOX RoPE at
+`rope_freq_base_global`, attention scale 1/sqrt(head_dim), no sliding window,
+SwiGLU, the tied `token_embd.weight` as embedding table and lm_head).  The
+differences are where the streamer works on host memory:
+
+* every buffer is device memory (torch tensors whose data_ptr() goes through
+  the C-ABI, which the library uses in place);
+* the weights are one device blob laid out like a GGUF data section (tensors
+  at 32-byte aligned offsets), addressed as (base, offset) exactly as the
+  streamer addresses its mapped file;
+* the residual loops (`hidden[i] = hidden[i] + proj_out_buf[i]`,
+  lua/gncx_streamer.lua:871-873, 906-908) call gncx_hip_vec_add;
+* the sampler is a greedy device argmax (the streamer's sampler adds a
+  repetition penalty on the host, lua/gncx_streamer.lua:1229-1272);
+* `fused=True` replaces the four prologue+attention calls with
+  gncx_hip_attention_step_fused (same results).
+
+Weights are random-init with the block statistics of the synthetic
+benchmark inputs: fp16 scales |N(0, 0.02)|, uniform random code bytes,
+Q6_K sub-block scales U[-32, 31], RMSNorm gammas 1 + N(0, 0.1).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from . import Q4_K, Q6_K, row_bytes
+
+_ALIGN = 32  # GGUF default data alignment
+
+
+@dataclass(frozen=True)
+class Qwen3Shape:
+    n_layers: int = 36
+    embed: int = 4096
+    n_heads: int = 32
+    n_kv: int = 8
+    head_dim: int = 128
+    ffn: int = 12288
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_base: float = 1e6
+    layer_type: int = Q4_K
+    embd_type: int = Q6_K
+
+    @property
+    def q_dim(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv * self.head_dim
+
+
+QWEN3_8B = Qwen3Shape()
+
+
+@dataclass
+class Model:
+    shape: Qwen3Shape
+    blob: object  # torch uint8 tensor on the device
+    offsets: dict = field(default_factory=dict)  # tensor name -> byte offset in blob
+
+    @property
+    def base(self) -> int:
+        return self.blob.data_ptr()
+
+    def off(self, name: str) -> int:
+        return self.offsets[name]
+
+
+def _layout(s: Qwen3Shape):
+    """(name, kind, rows, cols) in file order; kind is a ggml type or 'f32'."""
+    t = [("token_embd.weight", s.embd_type, s.vocab, s.embed)]
+    for l in range(s.n_layers):
+        p = f"blk.{l}"
+        t += [
+            (f"{p}.attn_norm.weight", "f32", 1, s.embed),
+            (f"{p}.attn_q.weight", s.layer_type, s.q_dim, s.embed),
+            (f"{p}.attn_k.weight", s.layer_type, s.kv_dim, s.embed),
+            (f"{p}.attn_v.weight", s.layer_type, s.kv_dim, s.embed),
+            (f"{p}.attn_q_norm.weight", "f32", 1, s.head_dim),
+            (f"{p}.attn_k_norm.weight", "f32", 1, s.head_dim),
+            (f"{p}.attn_output.weight", s.layer_type, s.embed, s.q_dim),
+            (f"{p}.ffn_norm.weight", "f32", 1, s.embed),
+            (f"{p}.ffn_gate.weight", s.layer_type, s.ffn, s.embed),
+            (f"{p}.ffn_up.weight", s.layer_type, s.ffn, s.embed),
+            (f"{p}.ffn_down.weight", s.layer_type, s.embed, s.ffn),
+        ]
+    t.append(("output_norm.weight", "f32", 1, s.embed))
+    return t
+
+
+def _nbytes(kind, rows, cols) -> int:
+    return 4 * rows * cols if kind == "f32" else row_bytes(kind, cols) * rows
+
+
+def build_model(torch, shape: Qwen3Shape = QWEN3_8B, seed: int = 0, device: str = "cuda") -> Model:
+    """Random-init weights generated on the device into one GGUF-like blob."""
+    layout = _layout(shape)
+    offsets, total = {}, 0
+    for name, kind, rows, cols in layout:
+        total = (total + _ALIGN - 1) // _ALIGN * _ALIGN
+        offsets[name] = total
+        total += _nbytes(kind, rows, cols)
+    blob = torch.empty(total, dtype=torch.uint8, device=device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    for name, kind, rows, cols in layout:
+        o, n = offsets[name], _nbytes(kind, rows, cols)
+        seg = blob[o:o + n]
+        if kind == "f32":
+            v = 1.0 + 0.1 * torch.randn(rows * cols, generator=g, device=device)
+            seg.view(torch.float32).copy_(v)
+            continue
+        bb = 144 if kind == Q4_K else 210
+        blk = seg.view(-1, bb)
+        nb = blk.shape[0]
+        blk.copy_(torch.randint(0, 256, (nb, bb), generator=g, device=device, dtype=torch.uint8))
+        if kind == Q4_K:  # d, dmin fp16 |N(0, 0.02)|; 12 scale bytes and 128 code bytes stay random
+            d = (0.02 * torch.randn(nb, 2, generator=g, device=device)).abs().to(torch.float16)
+            blk[:, 0:4].copy_(d.view(torch.uint8).view(nb, 4))
+        else:  # Q6_K: 16 int8 scales U[-32, 31] at 192, fp16 d |N(0, 0.02)| at 208
+            sc = torch.randint(-32, 32, (nb, 16), generator=g, device=device, dtype=torch.int8)
+            blk[:, 192:208].copy_(sc.view(torch.uint8))
+            d = (0.02 * torch.randn(nb, 1, generator=g, device=device)).abs().to(torch.float16)
+            blk[:, 208:210].copy_(d.view(torch.uint8).view(nb, 2))
+    return Model(shape, blob, offsets)
+
+
+class Decoder:
+    """Device-resident state of one sequence and the streamer's call sequence."""
+
+    def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda"):
+        s = model.shape
+        self.lib, self.torch, self.m, self.s, self.fused = lib, torch, model, s, fused
+        f32 = dict(dtype=torch.float32, device=device)
+        self.hidden = torch.zeros(s.embed, **f32)
+        self.normed = torch.zeros(s.embed, **f32)
+        self.q = torch.zeros(s.q_dim, **f32)
+        self.k = torch.zeros(s.kv_dim, **f32)
+        self.v = torch.zeros(s.kv_dim, **f32)
+        self.attn = torch.zeros(s.q_dim, **f32)
+        self.proj = torch.zeros(s.embed, **f32)
+        self.gate = torch.zeros(s.ffn, **f32)
+        self.up = torch.zeros(s.ffn, **f32)
+        self.act = torch.zeros(s.ffn, **f32)
+        self.logits = torch.zeros(s.vocab, **f32)
+        self.kc = [torch.zeros(max_seq, s.kv_dim, **f32) for _ in range(s.n_layers)]
+        self.vc = [torch.zeros(max_seq, s.kv_dim, **f32) for _ in range(s.n_layers)]
+        self.max_seq = max_seq
+        self.scale = 1.0 / (s.head_dim ** 0.5)
+
+    # -- the pieces shared by forward_token and prefill ----------------------
+    def _matvec(self, name, x, in_dim, out_dim, y):
+        self.lib.gncx_xfold_universal_matvec(self.m.base, self.m.off(name), self.s.layer_type, x, None, in_dim,
+                                             out_dim, y, None)
+
+    def _matbatch(self, name, x, b, in_dim, out_dim, y):
+        self.lib.gncx_xfold_universal_matbatch(self.m.base, self.m.off(name), self.s.layer_type, x, b, in_dim,
+                                               out_dim, y, None)
+
+    def _norm(self, name, x, out):
+        self.lib.gncx_rmsnorm_and_encode_4phase(x, self.m.base, self.m.off(name), self.s.embed, self.s.eps, 0, out,
+                                                None, None)
+
+    def _attention(self, l, q, k, v, pos, out):
+        s, L, m = self.s, self.lib, self.m
+        p = f"blk.{l}"
+        kc, vc = self.kc[l].data_ptr(), self.vc[l].data_ptr()
+        if self.fused:
+            L.gncx_hip_attention_step_fused(q, k, v, kc, vc, pos, s.n_heads, s.n_kv, s.head_dim, self.scale, 0, 1,
+                                            m.base, m.off(f"{p}.attn_q_norm.weight"),
+                                            m.off(f"{p}.attn_k_norm.weight"), 1, s.eps, 0, 0, s.rope_base, out)
+            return
+        L.gncx_rmsnorm_inplace_heads(q, m.base, m.off(f"{p}.attn_q_norm.weight"), 1, s.n_heads, s.head_dim, s.eps)
+        L.gncx_rmsnorm_inplace_heads(k, m.base, m.off(f"{p}.attn_k_norm.weight"), 1, s.n_kv, s.head_dim, s.eps)
+        L.gncx_apply_rope_xor11_ext(q, k, None, None, 0, 0, s.n_heads, s.n_kv, s.head_dim, pos, s.rope_base)
+        L.gncx_mqa_attention_step_ext(q, k, v, kc, vc, pos, s.n_heads, s.n_kv, s.head_dim, self.scale, 0, 1, out)
+
+    def _lm_head(self):
+        s, m = self.s, self.m
+        self._norm("output_norm.weight", self.hidden.data_ptr(), self.normed.data_ptr())
+        self.lib.gncx_universal_lm_head_logits(m.base, m.off("token_embd.weight"), s.embd_type,
+                                               self.normed.data_ptr(), s.embed, s.vocab, 0.0,
+                                               self.logits.data_ptr())
+        return self.logits
+
+    def _embed(self, token, dst):
+        s, m = self.s, self.m
+        fetch = {Q6_K: self.lib.gncx_fetch_token_embedding_q6_k}[s.embd_type]
+        fetch(m.base, m.off("token_embd.weight"), int(token), s.embed, 1.0, dst)
+
+    # -- lua/gncx_streamer.lua:759-965 ------------------------------------------
+    def forward_token(self, token: int, pos: int):
+        s, L = self.s, self.lib
+        if pos >= self.max_seq:
+            raise ValueError("position past the KV cache")
+        h, nrm = self.hidden.data_ptr(), self.normed.data_ptr()
+        q, k, v, a = self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr()
+        pr, ga, up, ac = self.proj.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr()
+        self._embed(token, h)
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            self._norm(f"{p}.attn_norm.weight", h, nrm)
+            self._matvec(f"{p}.attn_q.weight", nrm, s.embed, s.q_dim, q)
+            self._matvec(f"{p}.attn_k.weight", nrm, s.embed, s.kv_dim, k)
+            self._matvec(f"{p}.attn_v.weight", nrm, s.embed, s.kv_dim, v)
+            self._attention(l, q, k, v, pos, a)
+            self._matvec(f"{p}.attn_output.weight", a, s.q_dim, s.embed, pr)
+            L.gncx_hip_vec_add(h, pr, s.embed)
+            self._norm(f"{p}.ffn_norm.weight", h, nrm)
+            self._matvec(f"{p}.ffn_gate.weight", nrm, s.embed, s.ffn, ga)
+            self._matvec(f"{p}.ffn_up.weight", nrm, s.embed, s.ffn, up)
+            L.gncx_swiglu_activation(ga, up, s.ffn, ac)
+            self._matvec(f"{p}.ffn_down.weight", ac, s.ffn, s.embed, pr)
+            L.gncx_hip_vec_add(h, pr, s.embed)
+        return self._lm_head()
+
+    # -- lua/gncx_streamer.lua:968-1208 -----------------------------------------
+    def prefill(self, token_ids):
+        torch, s, L = self.torch, self.s, self.lib
+        B = len(token_ids)
+        if B == 0:
+            return None
+        if B == 1:
+            return self.forward_token(token_ids[0], 0)
+        if B > self.max_seq:
+            raise ValueError("prompt longer than the KV cache")
+        f32 = dict(dtype=torch.float32, device=self.hidden.device)
+        bh = torch.zeros(B, s.embed, **f32)
+        bn = torch.zeros(B, s.embed, **f32)
+        bq = torch.zeros(B, s.q_dim, **f32)
+        bk = torch.zeros(B, s.kv_dim, **f32)
+        bv = torch.zeros(B, s.kv_dim, **f32)
+        ba = torch.zeros(B, s.q_dim, **f32)
+        bp = torch.zeros(B, s.embed, **f32)
+        bg = torch.zeros(B, s.ffn, **f32)
+        bu = torch.zeros(B, s.ffn, **f32)
+        bf = torch.zeros(B, s.ffn, **f32)
+        rowp = lambda t, i: t.data_ptr() + 4 * i * t.shape[1]  # noqa: E731
+        for i, tok in enumerate(token_ids):
+            self._embed(tok, rowp(bh, i))
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            for i in range(B):
+                self._norm(f"{p}.attn_norm.weight", rowp(bh, i), rowp(bn, i))
+            self._matbatch(f"{p}.attn_q.weight", bn.data_ptr(), B, s.embed, s.q_dim, bq.data_ptr())
+            self._matbatch(f"{p}.attn_k.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bk.data_ptr())
+            self._matbatch(f"{p}.attn_v.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bv.data_ptr())
+            for i in range(B):
+                self._attention(l, rowp(bq, i), rowp(bk, i), rowp(bv, i), i, rowp(ba, i))
+            self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
+            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            for i in range(B):
+                self._norm(f"{p}.ffn_norm.weight", rowp(bh, i), rowp(bn, i))
+            self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
+            self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
+            L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
+            self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
+            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+        self.hidden.copy_(bh[B - 1])
+        return self._lm_head()
+
+    def greedy(self, logits) -> int:
+        return int(self.torch.argmax(logits).item())
+
+    def generate(self, prompt, n_new: int):
+        """Prefill `prompt`, then n_new greedy decode steps; returns the new ids."""
+        out = []
+        logits = self.prefill(list(prompt))
+        pos = len(prompt)
+        for _ in range(n_new):
+            tok = self.greedy(logits)
+            out.append(tok)
+            logits = self.forward_token(tok, pos)
+            pos += 1
+        return out

@@ -161,6 +161,10 @@ void gncx_hip_dequantize(const uint8_t* mmap_base, size_t weight_abs_offset, int
  * q[rows*in_dim] and meta[rows*in_dim/32][4] = {d as float bits, sum q[0:16],
  * sum q[16:32], sum q[0:32]}. */
 void gncx_hip_quantize_act(const float* in, int32_t rows, int32_t in_dim, int8_t* q, int32_t* meta);
+/* y[i] += x[i] for i < n: the residual adds that lua/gncx_streamer.lua:871-873
+ * and :906-908 do on the host, for callers whose hidden state stays on the
+ * device. */
+void gncx_hip_vec_add(float* y, const float* x, int32_t n);
 /* One launch doing gncx_rmsnorm_inplace_heads(q), gncx_rmsnorm_inplace_heads(k),
  * gncx_apply_rope_xor11_ext(q, k) and gncx_mqa_attention_step_ext with the
  * same results; q_vec/k_vec receive the normalised, rotated vectors.
