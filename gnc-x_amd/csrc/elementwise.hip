@@ -15,9 +15,35 @@ namespace {
 
 using namespace dev;
 
-// one wave per head; values stay in global memory (hd <= a few hundred)
+// One wave per head: the head is copied into LDS with coalesced loads, then
+// head_inv_rms forms the reference's four sequential fp32 lane sums from the
+// LDS copy (bit-exact with cpp:905-926) and the wave writes the result.  Heads
+// longer than kHeadsMaxHd (whole-vector norms, n_heads = 1) read global memory.
+constexpr int kHeadsMaxHd = 512;
+
 __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict v, const float* __restrict g,
                                                             int32_t n_heads, int32_t hd, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float buf[4][kHeadsMaxHd];
+    const int w = threadIdx.x >> 6;
+    const int h = blockIdx.x * 4 + w;
+    const int lane = threadIdx.x & 63;
+    const bool active = h < n_heads;
+    float* x = v + static_cast<size_t>(active ? h : 0) * hd;
+    float* lx = buf[w];
+    if (active)
+        for (int i = lane; i < hd; i += 64) lx[i] = x[i];
+    __syncthreads();
+    if (!active) return;
+    const float inv = head_inv_rms(lx, hd, eps, lane);
+    for (int i = lane; i < hd; i += 64) {
+        const float y = lx[i] * inv;
+        x[i] = g ? y * g[i] : y;
+    }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_heads_long_kernel(float* __restrict v, const float* __restrict g,
+                                                                 int32_t n_heads, int32_t hd, float eps) {
 #pragma clang fp contract(off)
     const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -30,23 +56,59 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* __restrict v,
     }
 }
 
-// one work-group per row; fp32 per-thread partials, combined in double
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict x, const float* __restrict g,
-                                                      int32_t dim, float eps, float* __restrict out) {
+// RMSNorm of one row per work-group (cpp:789-833): x and gamma are read once
+// as float4 (kept in registers for rows up to 16384 values), the sum of
+// squares is a fp32 tree over the work-group, y = (x * inv) * gamma.
+constexpr int kNormThreads = 1024;
+constexpr int kNormRegs = 4;  // float4 per thread held in registers
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict x, const float* __restrict g,
+                                                               int32_t dim, float eps, float* __restrict out,
+                                                               int32_t vec4) {
 #pragma clang fp contract(off)
-    __shared__ double part[4];
+    __shared__ float part[kNormThreads / 64];
     const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
     float* yr = out + static_cast<size_t>(blockIdx.x) * dim;
+    const int tid = threadIdx.x;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 256) s += xr[i] * xr[i];
-    double d = static_cast<double>(s);
+    float4 xv[kNormRegs], gv[kNormRegs];
+    const int32_t n4 = vec4 ? dim / 4 : 0;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const float4* g4 = reinterpret_cast<const float4*>(g);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = d;
+    for (int j = 0; j < kNormRegs; ++j) {
+        const int32_t t = tid + kNormThreads * j;
+        if (t < n4) {
+            xv[j] = x4[t];
+            gv[j] = g4[t];
+            s += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+        }
+    }
+    for (int32_t t = tid + kNormThreads * kNormRegs; t < n4; t += kNormThreads) {
+        const float4 a = x4[t];
+        s += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) s += xr[i] * xr[i];
+    s = wave_sum(s);
+    if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
-    const double tot = part[0] + part[1] + part[2] + part[3];
-    const float inv = 1.0f / sqrtf(static_cast<float>(tot / dim) + eps);
-    for (int i = threadIdx.x; i < dim; i += 256) yr[i] = xr[i] * inv * g[i];
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) tot += part[w];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
+    float4* y4 = reinterpret_cast<float4*>(yr);
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+        const int32_t t = tid + kNormThreads * j;
+        if (t < n4)
+            y4[t] = make_float4(xv[j].x * inv * gv[j].x, xv[j].y * inv * gv[j].y, xv[j].z * inv * gv[j].z,
+                                xv[j].w * inv * gv[j].w);
+    }
+    for (int32_t t = tid + kNormThreads * kNormRegs; t < n4; t += kNormThreads) {
+        const float4 a = x4[t], b = g4[t];
+        y4[t] = make_float4(a.x * inv * b.x, a.y * inv * b.y, a.z * inv * b.z, a.w * inv * b.w);
+    }
+    for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) yr[i] = xr[i] * inv * g[i];
 }
 
 __global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable t, int32_t n_heads,
@@ -156,15 +218,22 @@ int grid_for(size_t n, int threads) {
 hipError_t launch_rmsnorm_heads(float* v, const float* gamma, int32_t n_heads, int32_t head_dim, float eps,
                                 hipStream_t stream) {
     if (n_heads <= 0 || head_dim <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rmsnorm_heads_kernel, dim3((n_heads + 3) / 4), dim3(256), 0, stream, v, gamma, n_heads,
-                       head_dim, eps);
+    if (head_dim <= kHeadsMaxHd)
+        hipLaunchKernelGGL(rmsnorm_heads_kernel, dim3((n_heads + 3) / 4), dim3(256), 0, stream, v, gamma, n_heads,
+                           head_dim, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_heads_long_kernel, dim3((n_heads + 3) / 4), dim3(256), 0, stream, v, gamma,
+                           n_heads, head_dim, eps);
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int32_t dim, float eps, float* out,
                           hipStream_t stream) {
     if (rows <= 0 || dim <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, gamma, dim, eps, out);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
+                         reinterpret_cast<uintptr_t>(out);
+    const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, stream, x, gamma, dim, eps, out, vec4);
     return hipGetLastError();
 }
 

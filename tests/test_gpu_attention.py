@@ -191,6 +191,30 @@ def test_rmsnorm_heads_bitexact_with_oracle(lib, oracle):
     assert np.array_equal(out, oracle.rmsnorm_heads(v, g, 32, 128, 1e-6))
 
 
+@pytest.mark.parametrize("dim", [4096, 4098, 12288, 20000, 40960, 7])
+def test_rmsnorm_shapes(lib, oracle, dim):
+    """float4 path (registers, and the loop past 16384 values), scalar tail
+    and scalar-only rows"""
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal(dim) * 3).astype(np.float32)
+    g = synth.make_norm_gamma(dim, dim + 1)
+    out = np.zeros_like(x)
+    lib.gncx_rmsnorm_and_encode_4phase(ptr(x), ptr(g), 0, dim, 1e-6, 0, ptr(out), None, None)
+    gncx.check(lib)
+    assert rel_l2(out, oracle.rmsnorm(x, g, 1e-6)) < 1e-6
+
+
+@pytest.mark.parametrize("n_heads,hd", [(1, 4096), (3, 640), (5, 512), (2, 96)])
+def test_rmsnorm_heads_long_and_odd_heads_bitexact(lib, oracle, n_heads, hd):
+    rng = np.random.default_rng(n_heads * hd)
+    v = rng.standard_normal(n_heads * hd, dtype=np.float32)
+    g = synth.make_norm_gamma(hd, 7)
+    out = v.copy()
+    lib.gncx_rmsnorm_inplace_heads(ptr(out), ptr(g), 0, 1, n_heads, hd, 1e-6)
+    gncx.check(lib)
+    assert np.array_equal(out, oracle.rmsnorm_heads(v, g, n_heads, hd, 1e-6))
+
+
 def test_rmsnorm_swiglu_embeddings(lib, golden, oracle):
     x, g = golden["rms_x"].copy(), golden["rms_g"].copy()
     out = np.zeros_like(x)
