@@ -129,32 +129,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Band kernel (the main path): one 1024-thread work-group per CU, so x is
-// quantised into LDS only 256 times per call.  Work-group g owns rows
-// g, g + G, g + 2G, ... (G = number of work-groups): at any moment the whole
-// GPU is sweeping one contiguous stretch of the matrix, which keeps HBM pages
-// and channels busy the way a plain streaming read does (a contiguous band
-// per work-group measured 2x slower).
+// Band kernel (the main path): one work-group per CU, so x is quantised into
+// LDS only 256 times per call.  Work-group g owns rows g, g + G, g + 2G, ...
+// (G = number of work-groups): at any moment the whole GPU is sweeping one
+// contiguous stretch of the matrix, which keeps HBM pages and channels busy
+// the way a plain streaming read does (a contiguous band per work-group
+// measured 2x slower).
 //
 // Waves are arranged nwk x nwr: wave (kw, rw) covers slots [64 kw, 64 kw + 64)
 // of a row (one K-slice, its activations kept in registers).  Rows are handed
-// out R at a time from an LDS counter per K-slice, so waves the memory system
-// serves first take more rows (with a static split the last of a CU's 16
-// waves finished up to 15% after the first).  Each wave keeps two batches in
-// flight in two register buffers used in turn.
+// out one at a time from an LDS counter per K-slice, so waves the memory
+// system serves first take more rows (with a static split the last of a CU's
+// 16 waves finished up to 15% after the first).  Results never depend on
+// which wave took which row: K-slice partials meet in LDS and are added in a
+// fixed order.
 //
-// The first nqw waves quantise x before they touch weights and publish it
-// with an LDS count; the other waves issue their first two batches at once
-// and wait for that count only when they need x, so the quantisation never
-// waits behind weight loads held up in the memory pipeline.
+// Two schedules, picked per shape from measurements on Q4_K / Q6_K / Q8_0 /
+// Q4_0 / BF16 at K = 4096 and 14336:
 //
-// Weight loads go through a per-row buffer resource (base in scalar
-// registers); past-the-end batches use an empty resource, so every wave
-// issues the same loads in the same order and the waitcnt before each use
-// waits only for that use's loads.  With one K-slice per row (nwk == 1) the
-// wave writes y itself; otherwise the slices' partials meet in LDS and are
-// added in a fixed order at the end (results never depend on which wave took
-// which row).
+//   ONE (at least 8 row-waves, i.e. K up to 128 slots with 16 waves): each
+//   wave keeps one row in flight.  With 16 rows of ~2-4 KB in flight per CU a
+//   plain read of the matrix streams fastest (33 MB read in 6.4 us against
+//   6.9 us with two rows per wave).  The single row leaves nothing to cover
+//   the quantisation of x, so the first nqw waves (at least 4, one per SIMD)
+//   issue their x loads first, then their first two rows, then quantise (the
+//   waitcnt for x does not wait for the rows), and every wave starts with two
+//   rows in flight.  Loads are plain global loads: rows past the end and lanes
+//   without a slot re-read valid bytes (local row 0, slot 0) whose results
+//   are unused, so no load sits behind a branch and each waitcnt counts
+//   exactly the loads issued after the one it needs.  y is written from LDS
+//   once all rows are done.
+//
+//   TWO (K-split rows, or 8 waves per CU): each wave keeps two rows in flight
+//   in two register buffers used in turn; the first nqw waves quantise x
+//   before they touch weights and the other waves issue their first two rows
+//   at once.  Loads go through a per-row buffer resource whose past-the-end
+//   form (num_records 0) reads zeros and makes no memory request, so the
+//   steady loop issues the same loads every turn.  With one K-slice per row
+//   the wave writes y itself.
+//
+// The quantised-x count is an LDS counter with relaxed atomics: writers wait
+// for their own q / meta writes (lgkmcnt(0)) before the increment and readers
+// read q only after seeing the count, so LDS ordering is explicit (the
+// release / acquire forms made the compiler wait for every weight load too).
 //
 // Two block sizes: 16 waves per CU for matrices up to kBandStreamBytes per
 // work-group (more loads in flight ramp a short call up faster), 8 waves
@@ -172,28 +189,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 #ifndef GNCX_BAND_GROUPS
 #define GNCX_BAND_GROUPS 256
 #endif
-#ifndef GNCX_Q4K_ROWS
-#define GNCX_Q4K_ROWS 1
-#endif
-#ifndef GNCX_Q40_ROWS
-#define GNCX_Q40_ROWS 1
-#endif
-#ifndef GNCX_Q80_ROWS
-#define GNCX_Q80_ROWS 1
-#endif
-#ifndef GNCX_BF16_ROWS
-#define GNCX_BF16_ROWS 1
-#endif
 constexpr int kBandThreads = GNCX_BAND_THREADS;
 constexpr int kBandThreadsStream = GNCX_BAND_THREADS_STREAM;
 constexpr size_t kBandStreamBytes = static_cast<size_t>(GNCX_BAND_STREAM_KB) * 1024;
 constexpr int32_t kBandGroups = GNCX_BAND_GROUPS;  // one work-group per CU of an MI355X
 constexpr size_t kBandLds = 64 * 1024;
-constexpr int kBandQU = 8;          // x tasks per quantising thread with loads in flight together
 constexpr size_t kBandCtl = 128;    // LDS head: per-K-slice row counters and the quantised count
 constexpr int kCtlQuantised = 31;   // index of the count of waves done quantising
+constexpr int kOneMinRowWaves = 8;  // ONE schedule from this many row-waves (16-wave groups only)
 
-template <int TYPE, int R, int THREADS>
+enum BandSched { kSchedOne = 1, kSchedTwo = 2 };
+
+// x tasks (4 values) per quantising thread with loads in flight together,
+// and the least number of quantising waves
+template <int SCHED>
+struct BandQuant {
+    static constexpr int kU = SCHED == kSchedOne ? 4 : 8;
+    static constexpr int kMinWaves = SCHED == kSchedOne ? 4 : 1;
+};
+
+template <int TYPE, int THREADS, int SCHED>
 __global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __restrict w, uint32_t rbytes,
                                                                  const float* __restrict x, int32_t k,
                                                                  int32_t n, float* __restrict y, int32_t nwk,
@@ -202,24 +217,31 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __res
     using Frag = typename S::Frag;
     using Act = typename S::Act;
     constexpr bool kQuant = TYPE != kBF16;
+    constexpr int kU = BandQuant<SCHED>::kU;
     extern __shared__ __align__(16) uint8_t lds[];
     int32_t* ctl = reinterpret_cast<int32_t*>(lds);
     int8_t* q = reinterpret_cast<int8_t*>(lds + kBandCtl);
     ActMeta* meta = reinterpret_cast<ActMeta*>(lds + kBandCtl + k);
     const size_t qbytes = kQuant ? static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta) : 0;
-    float* part = reinterpret_cast<float*>(lds + kBandCtl + qbytes);  // [local row][nwk], nwk > 1 only
+    float* part = reinterpret_cast<float*>(lds + kBandCtl + qbytes);  // [local row][nwk]
 
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    // ONE branches on the wave index around loads, where a uniform branch keeps
+    // each waitcnt exact; TWO measured faster with the index in a vector register
+    const int wv = SCHED == kSchedOne ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)
+                                      : static_cast<int>(threadIdx.x >> 6);
     const int kw = wv % nwk, rw = wv / nwk;
     const bool active = rw < nwr;
+    const bool qwave = kQuant && wv < nqw;
     const int32_t slots = S::slots(k);
     const int s = kw * 64 + lane;
     const bool has_slot = active && s < slots;
     const int32_t groups = gridDim.x;
     // local row li of this work-group is global row li * groups + blockIdx.x
     const int32_t rows_here = (n - static_cast<int32_t>(blockIdx.x) + groups - 1) / groups;
-    const int32_t nbt = (rows_here + R - 1) / R;  // batches of R local rows
     auto grow = [&](int32_t li) { return static_cast<size_t>(li) * groups + blockIdx.x; };
+    // y straight from the wave only for whole rows under TWO
+    const bool direct = SCHED == kSchedTwo && nwk == 1;
 
     if (threadIdx.x < kBandCtl / sizeof(int32_t)) ctl[threadIdx.x] = 0;
     __syncthreads();
@@ -229,59 +251,94 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __res
         if (lane == 0) g = __hip_atomic_fetch_add(&ctl[kw], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         return __builtin_amdgcn_readfirstlane(g);
     };
-    auto issue = [&](Frag (&f)[R], int32_t j) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int32_t li = j * R + r;
-            const bool ok = j < nbt && li < rows_here;
-            S::load(f[r], BufRow(w + (ok ? grow(li) : 0) * rbytes, rbytes, ok), s);
+    auto issue = [&](Frag& f, int32_t li) {
+        const bool ok = li < rows_here;
+        if constexpr (SCHED == kSchedOne)
+            S::load(f, PtrRow{w + grow(ok ? li : 0) * rbytes}, has_slot ? s : 0);
+        else
+            S::load(f, BufRow(w + (ok ? grow(li) : 0) * rbytes, rbytes, ok), s);
+    };
+    auto reduce = [&](const Frag& f, const Act& a, int32_t li) {
+        float v = has_slot ? S::dot(f, a, s) : 0.0f;
+        v = wave_sum_lane63(v);
+        if (lane == 63) {
+            if (direct) y[grow(li)] = v;
+            else part[li * nwk + kw] = v;
         }
     };
-    auto reduce = [&](const Frag (&f)[R], const Act& a, int32_t j) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int32_t li = j * R + r;
-            if (j < nbt && li < rows_here) {  // wave-uniform
-                float v = has_slot ? S::dot(f[r], a, s) : 0.0f;
-                v = wave_sum_lane63(v);
-                if (lane == 63) {
-                    if (nwk == 1) y[grow(li)] = v;
-                    else part[li * nwk + kw] = v;
-                }
-            }
-        }
-    };
-
-    if (kQuant && wv < nqw) {
-        float4 xv[kBandQU];
-        quant_load<kBandQU>(xv, x, k / 32, threadIdx.x, nqw * 64);
-        quant_finish<kBandQU>(xv, x, k / 32, threadIdx.x, nqw * 64, q, meta);
+    auto quantise = [&](const float4 (&xv)[kU]) {
+        quant_finish<kU>(xv, x, k / 32, threadIdx.x, nqw * 64, q, meta);
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's q / meta writes are done
-        if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    if (active) {
-        Frag fa[R], fb[R];
-        int32_t ja = grab();
-        issue(fa, ja);
-        int32_t jb = grab();
-        issue(fb, jb);
+        asm volatile("" ::: "memory");
+        if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    auto act = [&](Act& a) {
         if (kQuant) {
             // the quantising waves depend on nothing but their own x loads
-            while (__hip_atomic_load(&ctl[kCtlQuantised], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nqw)
+            while (__hip_atomic_load(&ctl[kCtlQuantised], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < nqw)
                 __builtin_amdgcn_s_sleep(1);
+            asm volatile("" ::: "memory");
         }
-        Act a;
         if (has_slot) slot_act<TYPE>(a, s, q, meta, x);
-        while (ja < nbt || jb < nbt) {  // wave-uniform
-            reduce(fa, a, ja);
-            if (ja < nbt) ja = grab();
+    };
+
+    Frag fa, fb;
+    int32_t ja = rows_here, jb = rows_here;
+    if constexpr (SCHED == kSchedOne) {
+        auto start = [&]() {
+            if (active) {
+                ja = grab();
+                jb = grab();
+            }
             issue(fa, ja);
-            reduce(fb, a, jb);
-            if (jb < nbt) jb = grab();
             issue(fb, jb);
+        };
+        if (qwave) {
+            float4 xv[kU];
+            quant_load<kU>(xv, x, k / 32, threadIdx.x, nqw * 64);
+            start();
+            quantise(xv);
+        } else {
+            start();
+        }
+        if (active) {
+            Act a;
+            act(a);
+            if (ja < rows_here) reduce(fa, a, ja);
+            if (jb < rows_here) reduce(fb, a, jb);
+            for (int32_t li = jb < rows_here ? grab() : rows_here; li < rows_here; li = grab()) {
+                issue(fa, li);
+                reduce(fa, a, li);
+            }
+        }
+    } else {
+        if (qwave) {
+            float4 xv[kU];
+            quant_load<kU>(xv, x, k / 32, threadIdx.x, nqw * 64);
+            quantise(xv);
+        }
+        if (active) {
+            ja = grab();
+            issue(fa, ja);
+            jb = grab();
+            issue(fb, jb);
+            Act a;
+            act(a);
+            while (ja < rows_here || jb < rows_here) {  // wave-uniform
+                if (ja < rows_here) {
+                    reduce(fa, a, ja);
+                    ja = grab();
+                }
+                issue(fa, ja);
+                if (jb < rows_here) {
+                    reduce(fb, a, jb);
+                    jb = grab();
+                }
+                issue(fb, jb);
+            }
         }
     }
-    if (nwk == 1) return;
+    if (direct) return;
     __syncthreads();
     for (int32_t li = threadIdx.x; li < rows_here; li += THREADS) {
         float acc = 0.0f;
@@ -328,9 +385,9 @@ hipError_t launch_gemv_t(const uint8_t* w, const float* x, int32_t k, int32_t n,
 }
 
 
-// Band kernel geometry for (type, k, n) with `waves` waves per work-group;
-// false when the shape does not fit it.
-bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t waves, int32_t& groups,
+// Band kernel geometry for (type, k, n) with `waves` waves per work-group
+// under schedule `sched`; false when the shape does not fit it.
+bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t waves, int sched, int32_t& groups,
                int32_t& nwk, int32_t& nwr, int32_t& nqw, size_t& lds) {
     nwk = (slots + 63) / 64;
     if (nwk < 1 || nwk > waves) return false;
@@ -339,31 +396,45 @@ bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t wave
     const int32_t rows_per_wg = (n + groups - 1) / groups;
     groups = (n + rows_per_wg - 1) / rows_per_wg;
     const int32_t tasks = k / 4;  // 4 values of x per quantisation task
-    nqw = quantised ? (tasks + 64 * kBandQU - 1) / (64 * kBandQU) : 0;
+    const int u = sched == kSchedOne ? BandQuant<kSchedOne>::kU : BandQuant<kSchedTwo>::kU;
+    const int min_waves = sched == kSchedOne ? BandQuant<kSchedOne>::kMinWaves : BandQuant<kSchedTwo>::kMinWaves;
+    nqw = quantised ? (tasks + 64 * u - 1) / (64 * u) : 0;
+    if (quantised && nqw < min_waves) nqw = min_waves;
     if (nqw > waves) nqw = waves;
     const size_t qbytes = quantised ? static_cast<size_t>(k) + static_cast<size_t>(k / 32) * sizeof(ActMeta) : 0;
-    lds = kBandCtl + qbytes + (nwk > 1 ? sizeof(float) * static_cast<size_t>(rows_per_wg) * nwk : 0);
+    const bool direct = sched == kSchedTwo && nwk == 1;
+    lds = kBandCtl + qbytes + (direct ? 0 : sizeof(float) * static_cast<size_t>(rows_per_wg) * nwk);
     return lds <= kBandLds && nwk <= static_cast<int32_t>(kCtlQuantised);
 }
 
-template <int TYPE, int R, int THREADS>
-bool try_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+template <int TYPE, int THREADS, int SCHED>
+bool try_band_sched(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
     int32_t groups, nwk, nwr, nqw;
     size_t lds;
-    if (!band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, THREADS / 64, groups, nwk, nwr, nqw, lds))
+    if (!band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, THREADS / 64, SCHED, groups, nwk, nwr, nqw, lds))
         return false;
-    hipLaunchKernelGGL((gemv_band_kernel<TYPE, R, THREADS>), dim3(groups), dim3(THREADS), lds, stream, w,
+    hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED>), dim3(groups), dim3(THREADS), lds, stream, w,
                        static_cast<uint32_t>(row_bytes(TYPE, k)), x, k, n, y, nwk, nwr, nqw);
     return true;
 }
 
-template <int TYPE, int R>
+// ONE for 16-wave groups with at least kOneMinRowWaves row-waves, TWO otherwise
+template <int TYPE, int THREADS>
+bool try_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+    const int32_t nwk = (Slot<TYPE>::slots(k) + 63) / 64;
+    if (THREADS == 1024 && nwk >= 1 && (THREADS / 64) / nwk >= kOneMinRowWaves &&
+        try_band_sched<TYPE, THREADS, kSchedOne>(w, x, k, n, y, stream))
+        return true;
+    return try_band_sched<TYPE, THREADS, kSchedTwo>(w, x, k, n, y, stream);
+}
+
+template <int TYPE>
 hipError_t launch_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream,
                        bool& used) {
     const int32_t groups = n < kBandGroups ? n : kBandGroups;
     const size_t per_group = row_bytes(TYPE, k) * static_cast<size_t>(n) / static_cast<size_t>(groups);
-    used = (per_group > kBandStreamBytes && try_band<TYPE, R, kBandThreadsStream>(w, x, k, n, y, stream)) ||
-           try_band<TYPE, R, kBandThreads>(w, x, k, n, y, stream);
+    used = (per_group > kBandStreamBytes && try_band<TYPE, kBandThreadsStream>(w, x, k, n, y, stream)) ||
+           try_band<TYPE, kBandThreads>(w, x, k, n, y, stream);
     return used ? hipGetLastError() : hipSuccess;
 }
 
@@ -387,11 +458,11 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     bool used = false;
     hipError_t e = hipSuccess;
     switch (type) {
-    case kQ4_0: e = launch_band<kQ4_0, GNCX_Q40_ROWS>(w, x, k, n, y, stream, used); break;
-    case kQ8_0: e = launch_band<kQ8_0, GNCX_Q80_ROWS>(w, x, k, n, y, stream, used); break;
-    case kQ4_K: e = launch_band<kQ4_K, GNCX_Q4K_ROWS>(w, x, k, n, y, stream, used); break;
-    case kQ6_K: e = launch_band<kQ6_K, 1>(w, x, k, n, y, stream, used); break;
-    case kBF16: e = launch_band<kBF16, GNCX_BF16_ROWS>(w, x, k, n, y, stream, used); break;
+    case kQ4_0: e = launch_band<kQ4_0>(w, x, k, n, y, stream, used); break;
+    case kQ8_0: e = launch_band<kQ8_0>(w, x, k, n, y, stream, used); break;
+    case kQ4_K: e = launch_band<kQ4_K>(w, x, k, n, y, stream, used); break;
+    case kQ6_K: e = launch_band<kQ6_K>(w, x, k, n, y, stream, used); break;
+    case kBF16: e = launch_band<kBF16>(w, x, k, n, y, stream, used); break;
     default: return hipErrorInvalidValue;
     }
     if (used || e != hipSuccess) return e;
