@@ -75,7 +75,11 @@ __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope
     }
 }
 
-template <int HD>
+// SHORT: the chunk fits one pass (chunk <= TPP tokens).  Each thread's K and V
+// slices are then loaded at the start, ahead of q, so a work-group waits for
+// HBM once instead of three times in a row (q, then K, then V after the
+// softmax), and head blocks after the first re-read nothing.
+template <int HD, bool SHORT>
 __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     constexpr int LPT = HD / 16;          // lanes per token row (16 dims each)
     constexpr int TPP = kThreads / LPT;   // tokens per pass
@@ -85,6 +89,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     float* red = sc + kHeadBlock * p.chunk;             // [kWaves][kHeadBlock][HD]
     float* qs = red + kWaves * kHeadBlock * HD;         // [G][HD]  (prologue result)
     float* ks = qs + G * HD;                            // [HD]
+    float* vs = ks + HD;                                // SHORT: [TPP][HD], the chunk's V rows
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int hk = blockIdx.x;
@@ -94,11 +99,36 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     const int j = tid % LPT;       // 16-dim slice of the row
     const int ts = tid / LPT;      // token slot within a pass
     const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
+    const bool have_new = p.use_new != 0;
+
+    // SHORT: this thread's token is ta + ts; its K / V slices are loaded now
+    // (the new token's K comes from LDS after the prologue, its V from v_new)
+    float4 kpre[4], vpre[4];
+    const int tok0 = ta + ts;
+    const bool valid0 = tok0 < tb;
+    const bool new0 = have_new && tok0 == p.pos;
+    if constexpr (SHORT) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            kpre[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vpre[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (valid0) {
+            const float* vsrc = new0 ? p.v_new + static_cast<size_t>(hk) * HD
+                                     : p.v_cache + static_cast<size_t>(tok0) * kv_dim + static_cast<size_t>(hk) * HD;
+            if (!new0) {
+                const float* ksrc = p.k_cache + static_cast<size_t>(tok0) * kv_dim + static_cast<size_t>(hk) * HD;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kpre[c] = *reinterpret_cast<const float4*>(ksrc + 4 * (j + LPT * c));
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vpre[c] = *reinterpret_cast<const float4*>(vsrc + 4 * (j + LPT * c));
+        }
+    }
 
     // ---- q (and k_new) into LDS, with the optional prologue ----
     const float* qg = p.q + static_cast<size_t>(hk) * G * HD;
     for (int i = tid; i < G * HD; i += kThreads) qs[i] = qg[i];
-    const bool have_new = p.use_new != 0;
     if (have_new)
         for (int i = tid; i < HD; i += kThreads) ks[i] = p.k_new[static_cast<size_t>(hk) * HD + i];
     __syncthreads();
@@ -142,7 +172,11 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
             const int tok = t + ts;
             const bool valid = tok < tb;
             float4 kf[4];
-            if (valid) {
+            if (SHORT) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    kf[c] = new0 ? *reinterpret_cast<const float4*>(ks + 4 * (j + LPT * c)) : kpre[c];
+            } else if (valid) {
                 const float* src = (have_new && tok == p.pos)
                                        ? ks
                                        : p.k_cache + static_cast<size_t>(tok) * kv_dim + static_cast<size_t>(hk) * HD;
@@ -162,6 +196,10 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
                 for (int o = 1; o < LPT; o <<= 1) s += __shfl_xor(s, o, 64);
                 if (valid && j == 0 && h < nh) sc[h * p.chunk + (tok - ta)] = s * p.scale;
             }
+        }
+        if (SHORT && hb == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) *reinterpret_cast<float4*>(vs + ts * HD + 4 * (j + LPT * c)) = vpre[c];
         }
         __syncthreads();
 
@@ -183,6 +221,49 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
         __syncthreads();
 
         // ---- pass 2: o = sum_t e_t v_t ----
+        if constexpr (SHORT) {
+            // V is in LDS: thread (f, tg) sums float4 f of the head block over
+            // tokens tg, tg + NTG, ...; the NTG partials meet in LDS
+            constexpr int NF = kHeadBlock * HD / 4;
+            constexpr int NTG = kThreads / NF;
+            const int f = tid % NF, tg = tid / NF;
+            const int h = f / (HD / 4), d4 = f % (HD / 4);
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (h < nh) {
+                const float* prow = sc + h * p.chunk;
+                for (int tl = tg; tl < len; tl += NTG) {
+                    const float w = prow[tl];
+                    const float4 v = *reinterpret_cast<const float4*>(vs + tl * HD + 4 * d4);
+                    acc.x += w * v.x;
+                    acc.y += w * v.y;
+                    acc.z += w * v.z;
+                    acc.w += w * v.w;
+                }
+            }
+            float4* r4 = reinterpret_cast<float4*>(red);
+            r4[tg * NF + f] = acc;
+            if (wv < nh && lane == 0) {
+                float* ml = p.part_ml + (static_cast<size_t>(split) * p.n_heads + hk * G + hb + wv) * 2;
+                ml[0] = mx;
+                ml[1] = sum;
+            }
+            __syncthreads();
+            if (tid < NF && h < nh) {
+                float4 t = r4[f];
+#pragma unroll
+                for (int g = 1; g < NTG; ++g) {
+                    const float4 v = r4[g * NF + f];
+                    t.x += v.x;
+                    t.y += v.y;
+                    t.z += v.z;
+                    t.w += v.w;
+                }
+                *reinterpret_cast<float4*>(p.part_o + (static_cast<size_t>(split) * p.n_heads + hk * G + hb + h) * HD +
+                                           4 * d4) = t;
+            }
+            __syncthreads();
+            continue;
+        }
         float4 of[kHeadBlock][4];
 #pragma unroll
         for (int h = 0; h < kHeadBlock; ++h)
@@ -191,12 +272,17 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
         for (int t = ta; t < tb; t += TPP) {
             const int tok = t + ts;
             if (tok < tb) {
-                const float* src = (have_new && tok == p.pos)
-                                       ? p.v_new + static_cast<size_t>(hk) * HD
-                                       : p.v_cache + static_cast<size_t>(tok) * kv_dim + static_cast<size_t>(hk) * HD;
                 float4 vf[4];
+                if (SHORT) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) vf[c] = *reinterpret_cast<const float4*>(src + 4 * (j + LPT * c));
+                    for (int c = 0; c < 4; ++c) vf[c] = vpre[c];
+                } else {
+                    const float* src = (have_new && tok == p.pos)
+                                           ? p.v_new + static_cast<size_t>(hk) * HD
+                                           : p.v_cache + static_cast<size_t>(tok) * kv_dim + static_cast<size_t>(hk) * HD;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) vf[c] = *reinterpret_cast<const float4*>(src + 4 * (j + LPT * c));
+                }
 #pragma unroll
                 for (int h = 0; h < kHeadBlock; ++h) {
                     const float w = h < nh ? sc[h * p.chunk + (tok - ta)] : 0.0f;
@@ -399,59 +485,90 @@ __global__ __launch_bounds__(kThreads) void attn_mq_kernel(AttnParams p) {
 }
 
 // out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12), one
-// work-group per query head: the split weights e^(m_j - M) are formed once in
-// LDS, then each thread sums a strided subset of splits for one dimension.
+// work-group per query head.  Thread (d4, g) owns float4 d4 of the head and
+// splits g, g + ng, ...; its first kMergeU partial loads are issued before the
+// max / sum pass, so the kernel waits on memory about once.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxSplit = 4096;
+constexpr int kMergeU = 8;
 
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict part_o,
                                                                    const float* __restrict part_ml, int32_t n_split,
                                                                    int32_t n_heads, int32_t hd,
                                                                    float* __restrict out) {
     __shared__ float wgt[kMergeMaxSplit];
-    __shared__ float red[kMergeThreads];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    float m = -1e30f;
-    for (int s = tid; s < n_split; s += kMergeThreads)
-        m = fmaxf(m, part_ml[(static_cast<size_t>(s) * n_heads + h) * 2]);
-    red[tid] = m;
-    __syncthreads();
-    for (int o = kMergeThreads / 2; o > 0; o >>= 1) {
-        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
-        __syncthreads();
+    __shared__ float red[2][kMergeThreads / 64];
+    __shared__ float4 accs[kMergeThreads];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nd4 = hd / 4;  // hd in {64, 128, 256}
+    const int ng = kMergeThreads / nd4;
+    const int d4 = tid % nd4, g = tid / nd4;
+    auto po_at = [&](int s) {
+        return *reinterpret_cast<const float4*>(part_o + (static_cast<size_t>(s) * n_heads + h) * hd + 4 * d4);
+    };
+    float4 po[kMergeU];
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+        const int sp = g + u * ng;
+        po[u] = sp < n_split ? po_at(sp) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float M = red[0];
+    float m = -1e30f;
+    for (int sp = tid; sp < n_split; sp += kMergeThreads)
+        m = fmaxf(m, part_ml[(static_cast<size_t>(sp) * n_heads + h) * 2]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) red[0][wv] = m;
     __syncthreads();
+    float M = red[0][0];
+    for (int w = 1; w < kMergeThreads / 64; ++w) M = fmaxf(M, red[0][w]);
     float l = 0.0f;
-    for (int s = tid; s < n_split; s += kMergeThreads) {
-        const float* ml = part_ml + (static_cast<size_t>(s) * n_heads + h) * 2;
+    for (int sp = tid; sp < n_split; sp += kMergeThreads) {
+        const float* ml = part_ml + (static_cast<size_t>(sp) * n_heads + h) * 2;
         const float e = expf(ml[0] - M);
-        wgt[s] = e;
+        wgt[sp] = e;
         l += ml[1] * e;
     }
-    red[tid] = l;
+    l = wave_sum(l);
+    if (lane == 0) red[1][wv] = l;
     __syncthreads();
-    for (int o = kMergeThreads / 2; o > 0; o >>= 1) {
-        if (tid < o) red[tid] += red[tid + o];
-        __syncthreads();
+    float lt = 0.0f;
+    for (int w = 0; w < kMergeThreads / 64; ++w) lt += red[1][w];
+    const float inv = 1.0f / (lt + 1e-12f);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+        const int sp = g + u * ng;
+        const float w = sp < n_split ? wgt[sp] : 0.0f;
+        a.x += po[u].x * w;
+        a.y += po[u].y * w;
+        a.z += po[u].z * w;
+        a.w += po[u].w * w;
     }
-    const float inv = 1.0f / (red[0] + 1e-12f);
-    __syncthreads();
-    // thread (d, lane group) sums splits lg, lg + groups, ...
-    const int groups = kMergeThreads / hd;  // hd <= 256
-    const int d = tid % hd, lg = tid / hd;
-    float acc = 0.0f;
-    if (lg < groups) {
-#pragma unroll 8
-        for (int s = lg; s < n_split; s += groups)
-            acc += part_o[(static_cast<size_t>(s) * n_heads + h) * hd + d] * wgt[s];
+    for (int sp = g + kMergeU * ng; sp < n_split; sp += ng) {
+        const float4 v = po_at(sp);
+        const float w = wgt[sp];
+        a.x += v.x * w;
+        a.y += v.y * w;
+        a.z += v.z * w;
+        a.w += v.w * w;
     }
-    red[tid] = acc;
+    accs[tid] = a;
     __syncthreads();
-    if (tid < hd) {
-        float t = 0.0f;
-        for (int g = 0; g < groups; ++g) t += red[g * hd + tid];
-        out[static_cast<size_t>(h) * hd + tid] = t * inv;
+    if (tid < nd4) {
+        float4 t = accs[tid];
+        for (int gg = 1; gg < ng; ++gg) {
+            const float4 v = accs[gg * nd4 + tid];
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+        }
+        float4 r;
+        r.x = t.x * inv;
+        r.y = t.y * inv;
+        r.z = t.z * inv;
+        r.w = t.w * inv;
+        *reinterpret_cast<float4*>(out + static_cast<size_t>(h) * hd + 4 * tid) = r;
     }
 }
 
@@ -459,15 +576,23 @@ struct Plan {
     int32_t t0, t1, chunk, n_split;
 };
 
-size_t lds_bytes(int32_t chunk, int32_t G, int32_t hd);
-
 // LDS per work-group: scores [kHeadBlock][chunk] + wave partials + q + k_new,
-// kept within 64 KB by capping the chunk.
+// plus the chunk's V rows for a one-pass chunk (kThreads * 16 floats), kept
+// within 64 KB by capping the chunk.
 constexpr size_t kLdsBudget = 64 * 1024;
 
-size_t lds_bytes(int32_t chunk, int32_t G, int32_t hd) {
+size_t lds_base(int32_t chunk, int32_t G, int32_t hd) {
     return sizeof(float) * (static_cast<size_t>(kHeadBlock) * chunk + static_cast<size_t>(kWaves) * kHeadBlock * hd +
                             static_cast<size_t>(G) * hd + hd);
+}
+
+// the chunk fits one pass of the work-group and its V rows fit beside the rest
+bool one_pass(int32_t chunk, int32_t G, int32_t hd) {
+    return chunk <= kThreads / (hd / 16) && lds_base(chunk, G, hd) + sizeof(float) * kThreads * 16 <= kLdsBudget;
+}
+
+size_t lds_bytes(int32_t chunk, int32_t G, int32_t hd) {
+    return lds_base(chunk, G, hd) + (one_pass(chunk, G, hd) ? sizeof(float) * kThreads * 16 : 0);
 }
 
 Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv, int32_t G, int32_t hd) {
@@ -491,7 +616,7 @@ Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv, int32_t G, int32_t hd) {
 
 template <int HD>
 hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* part_ml, hipStream_t stream) {
-    AttnParams p;
+    AttnParams p{};
     p.q = a.q;
     p.k_new = a.k_new;
     p.v_new = a.v_new;
@@ -519,7 +644,12 @@ hipError_t launch_hd(const AttnArgs& a, const Plan& pl, float* part_o, float* pa
     const int G = a.n_heads / a.n_kv_heads;
     const size_t lds = lds_bytes(pl.chunk, G, HD);
     if (lds > kLdsBudget || pl.chunk > kMaxChunk) return hipErrorInvalidValue;  // window too long for one step
-    hipLaunchKernelGGL(attn_chunk_kernel<HD>, dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), lds, stream, p);
+    if (one_pass(pl.chunk, G, HD))
+        hipLaunchKernelGGL((attn_chunk_kernel<HD, true>), dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), lds, stream,
+                           p);
+    else
+        hipLaunchKernelGGL((attn_chunk_kernel<HD, false>), dim3(a.n_kv_heads, pl.n_split), dim3(kThreads), lds,
+                           stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml,

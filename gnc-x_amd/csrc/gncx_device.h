@@ -103,8 +103,18 @@ __device__ __forceinline__ float head_inv_rms(const float* v, int hd, float eps,
 #pragma clang fp contract(off)
     const int full = hd & ~3;
     float part = 0.0f;
-    if (lane < 4)
-        for (int i = lane; i < full; i += 4) part += v[i] * v[i];
+    if (lane < 4) {
+        // eight loads in flight ahead of the ordered adds (the order is the sum's)
+        int i = lane;
+        for (; i + 28 < full; i += 32) {
+            float a[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = v[i + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) part += a[u] * a[u];
+        }
+        for (; i < full; i += 4) part += v[i] * v[i];
+    }
     const float p0 = __shfl(part, 0, 64), p1 = __shfl(part, 1, 64);
     const float p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
     double s = static_cast<double>(p0) + static_cast<double>(p1) + static_cast<double>(p2) + static_cast<double>(p3);
