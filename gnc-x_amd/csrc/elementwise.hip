@@ -62,9 +62,14 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_long_kernel(float* __restri
 constexpr int kNormThreads = 1024;
 constexpr int kNormRegs = 4;  // float4 per thread held in registers
 
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict x, const float* __restrict g,
-                                                               int32_t dim, float eps, float* __restrict out,
-                                                               int32_t vec4) {
+// ADD: x is the residual stream h (one row), updated in place to h + r
+// before it is normalised -- the fp32 add of the separate vec_add kernel, so
+// the result is the same bit for bit.
+template <bool ADD>
+// (x and xo are the same row under ADD: no __restrict on the row pointers)
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* __restrict g,
+                                                               int32_t dim, float eps, float* out, int32_t vec4,
+                                                               const float* r, float* xo) {
 #pragma clang fp contract(off)
     __shared__ float part[kNormThreads / 64];
     const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
@@ -75,20 +80,43 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     const int32_t n4 = vec4 ? dim / 4 : 0;
     const float4* x4 = reinterpret_cast<const float4*>(xr);
     const float4* g4 = reinterpret_cast<const float4*>(g);
+    const float4* r4 = reinterpret_cast<const float4*>(r);
+    float4* xo4 = reinterpret_cast<float4*>(xo);
+    auto add4 = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
 #pragma unroll
     for (int j = 0; j < kNormRegs; ++j) {
         const int32_t t = tid + kNormThreads * j;
         if (t < n4) {
             xv[j] = x4[t];
+            if (ADD) {
+                xv[j] = add4(xv[j], r4[t]);
+                xo4[t] = xv[j];
+            }
             gv[j] = g4[t];
             s += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
         }
     }
     for (int32_t t = tid + kNormThreads * kNormRegs; t < n4; t += kNormThreads) {
-        const float4 a = x4[t];
+        float4 a = x4[t];
+        if (ADD) {
+            a = add4(a, r4[t]);
+            xo4[t] = a;
+        }
         s += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
     }
-    for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) s += xr[i] * xr[i];
+    for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) {
+        float a = xr[i];
+        if (ADD) {
+            a = a + r[i];
+            xo[i] = a;
+        }
+        s += a * a;
+    }
+    // rows past the registers are read again below: from xo, which now holds h + r
+    if (ADD) {
+        xr = xo;
+        x4 = reinterpret_cast<const float4*>(xo);
+    }
     s = wave_sum(s);
     if ((tid & 63) == 0) part[tid >> 6] = s;
     __syncthreads();
@@ -233,7 +261,19 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int3
     const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
                          reinterpret_cast<uintptr_t>(out);
     const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, stream, x, gamma, dim, eps, out, vec4);
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormThreads), 0, stream, x, gamma, dim, eps, out,
+                       vec4, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(float* h, const float* r, const float* gamma, int32_t dim, float eps, float* out,
+                              hipStream_t stream) {
+    if (dim <= 0) return hipSuccess;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(r) |
+                         reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(out);
+    const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(1), dim3(kNormThreads), 0, stream, h, gamma, dim, eps, out, vec4, r,
+                       h);
     return hipGetLastError();
 }
 

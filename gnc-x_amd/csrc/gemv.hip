@@ -208,11 +208,52 @@ struct BandQuant {
     static constexpr int kMinWaves = SCHED == kSchedOne ? 4 : 1;
 };
 
-template <int TYPE, int THREADS, int SCHED>
-__global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __restrict w, uint32_t rbytes,
+// The matrices of one launch: rows [end[i-1], end[i]) of the launch's row
+// space are rows of W_i, written to y_i (end[] < 2^31).  MULTI = false is
+// the single matrix of a plain matvec, with no lookup at all; with MULTI a
+// row lookup is a chain of 32-bit scalar compares and selects over kernel
+// arguments at fixed offsets (an indexed w[m] became a scalar memory load per
+// row, and 64-bit select chains at every lookup cost 0.5-1.5 us on short
+// rows, hence the separate instantiation).
+struct BandMats {
+    const uint8_t* w[kMaxGemvMats];
+    float* y[kMaxGemvMats];
+    int32_t end[kMaxGemvMats];
+    int32_t count;
+    template <bool MULTI, class P>
+    __device__ __forceinline__ P pick(size_t g, const P (&a)[kMaxGemvMats], size_t& first) const {
+        P p = a[0];
+        first = 0;
+        if constexpr (MULTI) {
+            const int32_t gi = static_cast<int32_t>(g);
+#pragma unroll
+            for (int m = 1; m < kMaxGemvMats; ++m) {
+                if (count > m && gi >= end[m - 1]) {
+                    p = a[m];
+                    first = static_cast<size_t>(end[m - 1]);
+                }
+            }
+        }
+        return p;
+    }
+    template <bool MULTI>
+    __device__ __forceinline__ const uint8_t* row(size_t g, uint32_t rbytes) const {
+        size_t first;
+        const uint8_t* p = pick<MULTI>(g, w, first);
+        return p + (g - first) * rbytes;
+    }
+    template <bool MULTI>
+    __device__ __forceinline__ float* out(size_t g) const {
+        size_t first;
+        float* p = pick<MULTI>(g, y, first);
+        return p + (g - first);
+    }
+};
+
+template <int TYPE, int THREADS, int SCHED, bool MULTI>
+__global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint32_t rbytes,
                                                                  const float* __restrict x, int32_t k,
-                                                                 int32_t n, float* __restrict y, int32_t nwk,
-                                                                 int32_t nwr, int32_t nqw) {
+                                                                 int32_t n, int32_t nwk, int32_t nwr, int32_t nqw) {
     using S = Slot<TYPE>;
     using Frag = typename S::Frag;
     using Act = typename S::Act;
@@ -254,15 +295,15 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __res
     auto issue = [&](Frag& f, int32_t li) {
         const bool ok = li < rows_here;
         if constexpr (SCHED == kSchedOne)
-            S::load(f, PtrRow{w + grow(ok ? li : 0) * rbytes}, has_slot ? s : 0);
+            S::load(f, PtrRow{mats.template row<MULTI>(grow(ok ? li : 0), rbytes)}, has_slot ? s : 0);
         else
-            S::load(f, BufRow(w + (ok ? grow(li) : 0) * rbytes, rbytes, ok), s);
+            S::load(f, BufRow(mats.template row<MULTI>(ok ? grow(li) : 0, rbytes), rbytes, ok), s);
     };
     auto reduce = [&](const Frag& f, const Act& a, int32_t li) {
         float v = has_slot ? S::dot(f, a, s) : 0.0f;
         v = wave_sum_lane63(v);
         if (lane == 63) {
-            if (direct) y[grow(li)] = v;
+            if (direct) *mats.template out<MULTI>(grow(li)) = v;
             else part[li * nwk + kw] = v;
         }
     };
@@ -343,7 +384,7 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(const uint8_t* __res
     for (int32_t li = threadIdx.x; li < rows_here; li += THREADS) {
         float acc = 0.0f;
         for (int j = 0; j < nwk; ++j) acc += part[li * nwk + j];
-        y[grow(li)] = acc;
+        *mats.template out<MULTI>(grow(li)) = acc;
     }
 }
 
@@ -408,41 +449,55 @@ bool band_plan(int32_t slots, int32_t k, int32_t n, bool quantised, int32_t wave
 }
 
 template <int TYPE, int THREADS, int SCHED>
-bool try_band_sched(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+bool try_band_sched(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream) {
     int32_t groups, nwk, nwr, nqw;
     size_t lds;
     if (!band_plan(Slot<TYPE>::slots(k), k, n, TYPE != kBF16, THREADS / 64, SCHED, groups, nwk, nwr, nqw, lds))
         return false;
-    hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED>), dim3(groups), dim3(THREADS), lds, stream, w,
-                       static_cast<uint32_t>(row_bytes(TYPE, k)), x, k, n, y, nwk, nwr, nqw);
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE, k));
+    if (m.count > 1)
+        hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED, true>), dim3(groups), dim3(THREADS), lds, stream, m,
+                           rb, x, k, n, nwk, nwr, nqw);
+    else
+        hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED, false>), dim3(groups), dim3(THREADS), lds, stream,
+                           m, rb, x, k, n, nwk, nwr, nqw);
     return true;
 }
 
 // ONE for 16-wave groups with at least kOneMinRowWaves row-waves, TWO otherwise
 template <int TYPE, int THREADS>
-bool try_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream) {
+bool try_band(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream) {
     const int32_t nwk = (Slot<TYPE>::slots(k) + 63) / 64;
     if (THREADS == 1024 && nwk >= 1 && (THREADS / 64) / nwk >= kOneMinRowWaves &&
-        try_band_sched<TYPE, THREADS, kSchedOne>(w, x, k, n, y, stream))
+        try_band_sched<TYPE, THREADS, kSchedOne>(m, x, k, n, stream))
         return true;
-    return try_band_sched<TYPE, THREADS, kSchedTwo>(w, x, k, n, y, stream);
+    return try_band_sched<TYPE, THREADS, kSchedTwo>(m, x, k, n, stream);
 }
 
+// n = total rows of the matrices in m
 template <int TYPE>
-hipError_t launch_band(const uint8_t* w, const float* x, int32_t k, int32_t n, float* y, hipStream_t stream,
-                       bool& used) {
+hipError_t launch_band(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream, bool& used) {
     const int32_t groups = n < kBandGroups ? n : kBandGroups;
     const size_t per_group = row_bytes(TYPE, k) * static_cast<size_t>(n) / static_cast<size_t>(groups);
-    used = (per_group > kBandStreamBytes && try_band<TYPE, kBandThreadsStream>(w, x, k, n, y, stream)) ||
-           try_band<TYPE, kBandThreads>(w, x, k, n, y, stream);
+    used = (per_group > kBandStreamBytes && try_band<TYPE, kBandThreadsStream>(m, x, k, n, stream)) ||
+           try_band<TYPE, kBandThreads>(m, x, k, n, stream);
     return used ? hipGetLastError() : hipSuccess;
 }
 
-}  // namespace
+hipError_t launch_band_type(int32_t type, const BandMats& m, const float* x, int32_t k, int32_t n,
+                            hipStream_t stream, bool& used) {
+    switch (type) {
+    case kQ4_0: return launch_band<kQ4_0>(m, x, k, n, stream, used);
+    case kQ8_0: return launch_band<kQ8_0>(m, x, k, n, stream, used);
+    case kQ4_K: return launch_band<kQ4_K>(m, x, k, n, stream, used);
+    case kQ6_K: return launch_band<kQ6_K>(m, x, k, n, stream, used);
+    case kBF16: return launch_band<kBF16>(m, x, k, n, stream, used);
+    default: used = false; return hipErrorInvalidValue;
+    }
+}
 
-hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n, float* y,
-                       hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
+// shape and alignment rules shared by the single and multi launchers
+hipError_t check_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k) {
     if (k <= 0 || k > kMaxGemvK) return hipErrorInvalidValue;
     if (type != kBF16 && (k % 32) != 0) return hipErrorInvalidValue;
     if ((type == kQ4_K || type == kQ6_K) && (k % 256) != 0) return hipErrorInvalidValue;
@@ -455,16 +510,23 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     } else if ((wa & 3u) != 0) {
         return hipErrorInvalidValue;
     }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n, float* y,
+                       hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipError_t e = check_gemv(type, w, x, k);
+    if (e != hipSuccess) return e;
+    BandMats m{};
+    m.w[0] = w;
+    m.y[0] = y;
+    m.end[0] = n;
+    m.count = 1;
     bool used = false;
-    hipError_t e = hipSuccess;
-    switch (type) {
-    case kQ4_0: e = launch_band<kQ4_0>(w, x, k, n, y, stream, used); break;
-    case kQ8_0: e = launch_band<kQ8_0>(w, x, k, n, y, stream, used); break;
-    case kQ4_K: e = launch_band<kQ4_K>(w, x, k, n, y, stream, used); break;
-    case kQ6_K: e = launch_band<kQ6_K>(w, x, k, n, y, stream, used); break;
-    case kBF16: e = launch_band<kBF16>(w, x, k, n, y, stream, used); break;
-    default: return hipErrorInvalidValue;
-    }
+    e = launch_band_type(type, m, x, k, n, stream, used);
     if (used || e != hipSuccess) return e;
     switch (type) {
     case kQ4_0: return launch_gemv_t<kQ4_0, 4>(w, x, k, n, y, stream);
@@ -474,6 +536,33 @@ hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k
     case kBF16: return launch_gemv_t<kBF16, 4>(w, x, k, n, y, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                             const float* x, int32_t k, float* const* ys, hipStream_t stream) {
+    if (count <= 0 || count > kMaxGemvMats) return hipErrorInvalidValue;
+    BandMats m{};
+    int64_t total = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (ns[i] < 0) return hipErrorInvalidValue;
+        hipError_t e = check_gemv(type, ws[i], x, k);
+        if (e != hipSuccess) return e;
+        total += ns[i];
+        m.w[i] = ws[i];
+        m.y[i] = ys[i];
+        m.end[i] = static_cast<int32_t>(total);
+    }
+    if (total == 0) return hipSuccess;
+    if (total > INT32_MAX) return hipErrorInvalidValue;
+    m.count = count;
+    bool used = false;
+    hipError_t e = launch_band_type(type, m, x, k, static_cast<int32_t>(total), stream, used);
+    if (used || e != hipSuccess) return e;
+    for (int32_t i = 0; i < count; ++i) {
+        e = launch_gemv(type, ws[i], x, k, ns[i], ys[i], stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, ActMeta* meta,

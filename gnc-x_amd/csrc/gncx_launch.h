@@ -21,6 +21,13 @@ constexpr int32_t kMaxGemvK = 40960;
 hipError_t launch_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n,
                        float* y, hipStream_t stream);
 
+// ys[i][ns[i]] = W_i[ns[i] x k] . Q8(x[k]) for up to kMaxGemvMats matrices of one
+// type and k, in one launch when the band kernel takes the shape (x is
+// quantised once per work-group for all of them); otherwise one launch each.
+constexpr int32_t kMaxGemvMats = 4;
+hipError_t launch_gemv_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                             const float* x, int32_t k, float* const* ys, hipStream_t stream);
+
 // Per-32 Q8 quantisation of `rows` rows of k floats into q[rows*k] and
 // meta[rows*k/32] (used by matbatch and the dequant tests).
 hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, ActMeta* meta,
@@ -77,6 +84,10 @@ hipError_t launch_rmsnorm_heads(float* v, const float* gamma, int32_t n_heads, i
 // RMSNorm of `rows` vectors of dim (reference cpp:789-833).
 hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int32_t dim, float eps,
                           float* out, hipStream_t stream);
+// h += r, then out = RMSNorm(h) * gamma, one row of dim, in one kernel (the
+// same arithmetic as launch_vec_add followed by launch_rmsnorm).
+hipError_t launch_add_rmsnorm(float* h, const float* r, const float* gamma, int32_t dim, float eps, float* out,
+                              hipStream_t stream);
 // NEOX RoPE with a host-computed cos/sin table (reference cpp:1797-1862).
 hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_heads,
                        int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);

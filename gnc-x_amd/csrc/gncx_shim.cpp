@@ -728,6 +728,74 @@ GNCX_API void gncx_hip_vec_add(float* y, const float* x, int32_t n) {
     finish_out(y, yd, n, host_y, where);
 }
 
+// Several matrices of one type and in_dim applied to the same x in one launch.
+GNCX_API void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
+                                    int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_vecs) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_matvec_multi";
+    if (count <= 0 || count > kMaxGemvMats || !weights || !out_dims || !out_vecs || !in_vec || in_dim <= 0) {
+        set_error(where, "count must be 1..4, with weights, out_dims, in_vec and out_vecs given", -1);
+        return;
+    }
+    if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    // x staged here is not the vector the matvec act-quant cache rule refers to
+    g_act.last_in = nullptr;
+    g_act.staged_on_device = false;
+    const uint8_t* ws[kMaxGemvMats];
+    float* ys[kMaxGemvMats];
+    bool host[kMaxGemvMats];
+    size_t host_total = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (out_dims[i] <= 0 || !weights[i] || !out_vecs[i]) {
+            set_error(where, "every matrix needs weights, out_dims > 0 and an output", -1);
+            return;
+        }
+        ws[i] = device_weights(weights[i], row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dims[i]), where);
+        if (!ws[i]) return;
+        host[i] = !is_device_ptr(out_vecs[i]);
+        if (host[i]) host_total += static_cast<size_t>(out_dims[i]);
+    }
+    const float* x = stage_in(in_vec, static_cast<size_t>(in_dim), g_rt.x, where);
+    if (!x) return;
+    // host outputs share one staging buffer
+    if (host_total && !g_rt.y.ensure(sizeof(float) * host_total, where)) return;
+    size_t off = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        ys[i] = host[i] ? g_rt.y.as<float>() + off : out_vecs[i];
+        if (host[i]) off += static_cast<size_t>(out_dims[i]);
+    }
+    if (!check(launch_gemv_multi(ggml_type, count, ws, out_dims, x, in_dim, ys, g_rt.stream), where)) return;
+    for (int32_t i = 0; i < count; ++i)
+        if (host[i] && !finish_out(out_vecs[i], ys[i], static_cast<size_t>(out_dims[i]), true, where)) return;
+}
+
+// hidden += delta, then the RMSNorm of gncx_rmsnorm_and_encode_4phase (no tokens)
+// of the new hidden into out_normed_fp32, in one kernel.
+GNCX_API void gncx_hip_add_rmsnorm(float* hidden, const float* delta, const uint8_t* mmap_base,
+                                   size_t norm_weight_offset, int32_t dim, float eps, float* out_normed_fp32) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_add_rmsnorm";
+    g_norm_epoch++;
+    if (dim <= 0 || !hidden || !delta || !out_normed_fp32 || !ensure_runtime(where)) return;
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
+    if (!g) return;
+    const float* dd = stage_in(delta, static_cast<size_t>(dim), g_rt.k, where);
+    if (!dd) return;
+    const bool host_h = !is_device_ptr(hidden);
+    float* hd = hidden;
+    if (host_h) {
+        hd = const_cast<float*>(stage_in(hidden, static_cast<size_t>(dim), g_rt.q, where));
+        if (!hd) return;
+    }
+    bool host_o = false;
+    float* o = out_target(out_normed_fp32, static_cast<size_t>(dim), g_rt.o, host_o, where);
+    if (!o) return;
+    if (!check(launch_add_rmsnorm(hd, dd, g, dim, eps, o, g_rt.stream), where)) return;
+    if (!finish_out(hidden, hd, static_cast<size_t>(dim), host_h, where)) return;
+    finish_out(out_normed_fp32, o, static_cast<size_t>(dim), host_o, where);
+}
+
 namespace {
 // cpp:693-780: one row of the embedding table, decoded on the device.
 void fetch_embedding(int32_t type, const uint8_t* base, size_t off, int32_t token, int32_t dim, float scale,

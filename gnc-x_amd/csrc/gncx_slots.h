@@ -6,7 +6,9 @@
 //                        BufRow below),
 //   Act                  the Q8 activation registers the slot multiplies,
 //   load_act(a, s, ...)  reads them (LDS q + ActMeta, or fp32 x for BF16),
-//   dot(f, a, s)         the slot's fp32 share of the row sum,
+//   dot(f, a, s)         the slot's fp32 share of the row sum (no contraction, so
+//                        every inlined copy rounds alike and a row's result does
+//                        not depend on which loop of a kernel computed it),
 // so kernels can put several slots' weight loads in flight before touching
 // any, and keep a slot's activations in registers across rows.
 //   Q4_K  4 slots per 144 B super-block: 16 B header + 32 B of nibbles each
@@ -167,6 +169,7 @@ struct Slot<kQ4_K> {
         a.sh = mh.sum;
     }
     __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int s) {
+#pragma clang fp contract(off)
         const int c = s & 3;
         const uint32_t M = 0x0f0f0f0fu;
         int dl = 0, dh = 0;
@@ -233,6 +236,7 @@ struct Slot<kQ6_K> {
         }
     }
     __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int s) {
+#pragma clang fp contract(off)
         const int g = s & 1;
         const uint4 pa = raw16_get(f.pa, f.sh), pb = raw16_get(f.pb, f.sh), ph = raw16_get(f.ph, f.sh);
         const uint32_t sc_lo = __builtin_amdgcn_alignbyte(f.sv.y, f.sv.x, f.sh);  // sc[8n+0..3]
@@ -293,6 +297,7 @@ struct Slot<kQ4_0> {
         a.sum = m.sum;
     }
     __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int) {
+#pragma clang fp contract(off)
         const uint4 qs = raw16_get(f.qs, f.sh);
         const uint32_t M = 0x0f0f0f0fu;
         int dot = 0;
@@ -333,6 +338,7 @@ struct Slot<kQ8_0> {
         a.d = meta[b].d;
     }
     __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int) {
+#pragma clang fp contract(off)
         const uint4 w0 = raw16_get(f.lo, f.sh), w1 = raw16_get(f.hi, f.sh);
         int dot = 0;
         dot = sdot4(w0.x, a.x0.x, dot); dot = sdot4(w0.y, a.x0.y, dot);
@@ -365,6 +371,7 @@ struct Slot<kBF16> {
         a.b = *reinterpret_cast<const float4*>(x + 8 * s + 4);
     }
     __device__ static __forceinline__ float dot(const Frag& f, const Act& x, int) {
+#pragma clang fp contract(off)
         return bf16_bits(f.w.x & 0xffffu) * x.a.x + bf16_bits(f.w.x >> 16) * x.a.y +
                bf16_bits(f.w.y & 0xffffu) * x.a.z + bf16_bits(f.w.y >> 16) * x.a.w +
                bf16_bits(f.w.z & 0xffffu) * x.b.x + bf16_bits(f.w.z >> 16) * x.b.y +

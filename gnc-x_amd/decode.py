@@ -16,8 +16,10 @@ differences are where the streamer works on host memory:
   lua/gncx_streamer.lua:871-873, 906-908) call gncx_hip_vec_add;
 * the sampler is a greedy device argmax (the streamer's sampler adds a
   repetition penalty on the host, lua/gncx_streamer.lua:1229-1272);
-* `fused=True` replaces the four prologue+attention calls with
-  gncx_hip_attention_step_fused (same results).
+* `fused=True` uses the library's launch-saving extensions, with the same
+  results: gncx_hip_attention_step_fused for the four prologue+attention
+  calls, gncx_hip_matvec_multi for Q/K/V and for gate/up (one launch each),
+  and gncx_hip_add_rmsnorm for each residual add and the RMSNorm after it.
 
 Weights are random-init with the block statistics of the synthetic
 benchmark inputs: fp16 scales |N(0, 0.02)|, uniform random code bytes,
@@ -25,6 +27,7 @@ Q6_K sub-block scales U[-32, 31], RMSNorm gammas 1 + N(0, 0.1).
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, field
 
 from . import Q4_K, Q6_K, row_bytes
@@ -152,6 +155,21 @@ class Decoder:
         self.vc = [torch.zeros(max_seq, s.kv_dim, **f32) for _ in range(s.n_layers)]
         self.max_seq = max_seq
         self.scale = 1.0 / (s.head_dim ** 0.5)
+        self._qkv = self._gu = None  # gncx_hip_matvec_multi arguments, built on first fused use
+
+    def _fused_tables(self):
+        """ctypes argument arrays of gncx_hip_matvec_multi, per layer."""
+        s, m = self.s, self.m
+        P, I = C.c_void_p, C.c_int32
+        self._qkv, self._gu = [], []
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            w = (P * 3)(*(m.base + m.off(f"{p}.attn_{n}.weight") for n in "qkv"))
+            y = (P * 3)(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr())
+            self._qkv.append((w, (I * 3)(s.q_dim, s.kv_dim, s.kv_dim), y))
+            w = (P * 2)(m.base + m.off(f"{p}.ffn_gate.weight"), m.base + m.off(f"{p}.ffn_up.weight"))
+            y = (P * 2)(self.gate.data_ptr(), self.up.data_ptr())
+            self._gu.append((w, (I * 2)(s.ffn, s.ffn), y))
 
     # -- the pieces shared by forward_token and prefill ----------------------
     def _matvec(self, name, x, in_dim, out_dim, y):
@@ -180,9 +198,10 @@ class Decoder:
         L.gncx_apply_rope_xor11_ext(q, k, None, None, 0, 0, s.n_heads, s.n_kv, s.head_dim, pos, s.rope_base)
         L.gncx_mqa_attention_step_ext(q, k, v, kc, vc, pos, s.n_heads, s.n_kv, s.head_dim, self.scale, 0, 1, out)
 
-    def _lm_head(self):
+    def _lm_head(self, normed_ready: bool = False):
         s, m = self.s, self.m
-        self._norm("output_norm.weight", self.hidden.data_ptr(), self.normed.data_ptr())
+        if not normed_ready:
+            self._norm("output_norm.weight", self.hidden.data_ptr(), self.normed.data_ptr())
         self.lib.gncx_universal_lm_head_logits(m.base, m.off("token_embd.weight"), s.embd_type,
                                                self.normed.data_ptr(), s.embed, s.vocab, 0.0,
                                                self.logits.data_ptr())
@@ -202,6 +221,8 @@ class Decoder:
         q, k, v, a = self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr()
         pr, ga, up, ac = self.proj.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr()
         self._embed(token, h)
+        if self.fused:
+            return self._forward_fused(pos)
         for l in range(s.n_layers):
             p = f"blk.{l}"
             self._norm(f"{p}.attn_norm.weight", h, nrm)
@@ -218,6 +239,30 @@ class Decoder:
             self._matvec(f"{p}.ffn_down.weight", ac, s.ffn, s.embed, pr)
             L.gncx_hip_vec_add(h, pr, s.embed)
         return self._lm_head()
+
+    def _forward_fused(self, pos: int):
+        """forward_token's layers with the extensions: 8 calls per layer."""
+        s, L, m = self.s, self.lib, self.m
+        h, nrm = self.hidden.data_ptr(), self.normed.data_ptr()
+        q, k, v, a = self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr()
+        pr, ga, up, ac = self.proj.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr()
+        if self._qkv is None:
+            self._fused_tables()
+        self._norm("blk.0.attn_norm.weight", h, nrm)
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            w, n, y = self._qkv[l]
+            L.gncx_hip_matvec_multi(3, w, n, s.layer_type, nrm, s.embed, y)
+            self._attention(l, q, k, v, pos, a)
+            self._matvec(f"{p}.attn_output.weight", a, s.q_dim, s.embed, pr)
+            L.gncx_hip_add_rmsnorm(h, pr, m.base, m.off(f"{p}.ffn_norm.weight"), s.embed, s.eps, nrm)
+            w, n, y = self._gu[l]
+            L.gncx_hip_matvec_multi(2, w, n, s.layer_type, nrm, s.embed, y)
+            L.gncx_swiglu_activation(ga, up, s.ffn, ac)
+            self._matvec(f"{p}.ffn_down.weight", ac, s.ffn, s.embed, pr)
+            nxt = f"blk.{l + 1}.attn_norm.weight" if l + 1 < s.n_layers else "output_norm.weight"
+            L.gncx_hip_add_rmsnorm(h, pr, m.base, m.off(nxt), s.embed, s.eps, nrm)
+        return self._lm_head(normed_ready=True)
 
     # -- lua/gncx_streamer.lua:968-1208 -----------------------------------------
     def prefill(self, token_ids):

@@ -176,6 +176,23 @@ void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_ve
                                    int32_t has_norm_weight, float norm_eps, size_t rope_freqs_offset,
                                    int32_t has_rope_freqs, float rope_base, float* out_attn_vec);
 
+/* Extensions with no counterpart in the reference, for callers that keep the
+ * hidden state on the device and want fewer launches per token (the streamer
+ * issues one gncx_xfold_universal_matvec per matrix, lua/gncx_streamer.lua:
+ * 806-809 and 890-891, and adds residuals on the host, :871-873 and :906-908).
+ *
+ * out_vecs[i][out_dims[i]] = W_i . x for count (1..4) matrices of one
+ * ggml_type and in_dim, e.g. Q/K/V or gate/up; weights[i] points at each
+ * tensor (host or device, like mmap_base + offset), x is quantised once.  Each
+ * output equals what gncx_xfold_universal_matvec gives for that matrix. */
+void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
+                           int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_vecs);
+/* hidden[i] += delta[i], then out_normed_fp32 = the RMSNorm of
+ * gncx_rmsnorm_and_encode_4phase (cpp:789-833) of the new hidden, in one
+ * kernel; the same values as gncx_hip_vec_add followed by that call. */
+void gncx_hip_add_rmsnorm(float* hidden, const float* delta, const uint8_t* mmap_base, size_t norm_weight_offset,
+                          int32_t dim, float eps, float* out_normed_fp32);
+
 #ifdef __cplusplus
 }
 #endif

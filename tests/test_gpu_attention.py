@@ -204,6 +204,29 @@ def test_rmsnorm_shapes(lib, oracle, dim):
     assert rel_l2(out, oracle.rmsnorm(x, g, 1e-6)) < 1e-6
 
 
+@pytest.mark.parametrize("dim", [4096, 4098, 20000, 7])
+def test_add_rmsnorm_equals_vec_add_then_rmsnorm(lib, oracle, dim):
+    """gncx_hip_add_rmsnorm = gncx_hip_vec_add then gncx_rmsnorm_and_encode_4phase,
+    bit for bit, for the new hidden and the normalised output (host buffers)."""
+    rng = np.random.default_rng(dim + 5)
+    h0 = (rng.standard_normal(dim) * 3).astype(np.float32)
+    d = rng.standard_normal(dim).astype(np.float32)
+    g = synth.make_norm_gamma(dim, dim + 2)
+    h1 = h0.copy()
+    lib.gncx_hip_vec_add(ptr(h1), ptr(d), dim)
+    want = np.zeros_like(h0)
+    lib.gncx_rmsnorm_and_encode_4phase(ptr(h1), ptr(g), 0, dim, 1e-6, 0, ptr(want), None, None)
+    gncx.check(lib)
+    h2 = h0.copy()
+    got = np.zeros_like(h0)
+    lib.gncx_hip_add_rmsnorm(ptr(h2), ptr(d), ptr(g), 0, dim, 1e-6, ptr(got))
+    gncx.check(lib)
+    assert np.array_equal(h2, h1)
+    assert np.array_equal(h2, h0 + d)
+    assert np.array_equal(got, want)
+    assert rel_l2(got, oracle.rmsnorm(h0 + d, g, 1e-6)) < 1e-6
+
+
 @pytest.mark.parametrize("n_heads,hd", [(1, 4096), (3, 640), (5, 512), (2, 96)])
 def test_rmsnorm_heads_long_and_odd_heads_bitexact(lib, oracle, n_heads, hd):
     rng = np.random.default_rng(n_heads * hd)

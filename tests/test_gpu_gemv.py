@@ -230,3 +230,51 @@ def test_lm_head_and_softcap(lib, golden):
     lib.gncx_universal_lm_head_logits(ptr(w), 0, Q6_K, ptr(x), k, v, 30.0, ptr(y))
     gncx.check(lib)
     assert rel_l2(y, golden["lm_y_cap"]) < TOL
+
+
+MULTI_CASES = [
+    # (type, k, out_dims): Q/K/V and gate/up of the Qwen3-8B-shaped model, other types,
+    # a K-split shape, and one the band kernel does not take (one launch per matrix)
+    (Q4_K, 4096, (4096, 1024, 1024)),
+    (Q4_K, 4096, (12288, 12288)),
+    (Q4_K, 14336, (4096, 33)),
+    (Q6_K, 4096, (300, 1, 77, 4096)),
+    (Q8_0, 4096, (1024, 512)),
+    (Q4_0, 2048, (5, 700)),
+    (BF16, 1024, (256, 128, 64)),
+    (Q4_0, 40960, (8, 3)),
+]
+
+
+@pytest.mark.parametrize("t,k,dims", MULTI_CASES)
+def test_matvec_multi_equals_separate_matvecs(lib, t, k, dims):
+    """gncx_hip_matvec_multi: each output bit-identical to the same matrix's
+    gncx_xfold_universal_matvec (every row's dot runs the same arithmetic)."""
+    ws = [synth.make_weights(t, n, k, seed=300 + i + t) for i, n in enumerate(dims)]
+    x = synth.make_activations(1, k, seed=400 + t + k)
+    want = []
+    for w, n in zip(ws, dims):
+        y = np.full(n, np.nan, np.float32)
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, t, ptr(x), None, k, n, ptr(y), None)
+        gncx.check(lib)
+        want.append(y)
+    outs = [np.full(n, np.nan, np.float32) for n in dims]
+    cnt = len(dims)
+    lib.gncx_hip_matvec_multi(cnt, (C.c_void_p * cnt)(*[ptr(w) for w in ws]), (C.c_int32 * cnt)(*dims), t, ptr(x),
+                              k, (C.c_void_p * cnt)(*[ptr(o) for o in outs]))
+    gncx.check(lib)
+    for i, (got, w) in enumerate(zip(outs, want)):
+        assert np.array_equal(got, w), (i, float(np.abs(got - w).max()))
+    for w in ws:
+        lib.gncx_hip_weight_forget(ptr(w))
+
+
+def test_matvec_multi_rejects_bad_counts(lib):
+    x = np.zeros(256, np.float32)
+    y = np.zeros(8, np.float32)
+    w = synth.make_weights(Q4_K, 8, 256, seed=1)
+    for cnt in (0, 5):
+        lib.gncx_hip_matvec_multi(cnt, (C.c_void_p * 5)(*[ptr(w)] * 5), (C.c_int32 * 5)(*[8] * 5), Q4_K, ptr(x), 256,
+                                  (C.c_void_p * 5)(*[ptr(y)] * 5))
+        assert lib.gncx_hip_last_status() != 0
+    lib.gncx_hip_weight_forget(ptr(w))
