@@ -204,6 +204,17 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     s = dec.QWEN3_8B
     g = torch.Generator().manual_seed(seed + 1)
     prompt = torch.randint(0, s.vocab, (prompt_len,), generator=g).tolist()
+    # prefill through the library's batched extensions (own KV caches), timed
+    # beside the streamer's per-token call sequence below
+    d2 = dec.Decoder(lib, torch, model, max_seq=prompt_len + 1, fused=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits_f = d2.prefill(prompt).clone()
+    torch.cuda.synchronize()
+    prefill_fused_s = time.perf_counter() - t0
+    pkg.check(lib)
+    del d2
+    torch.cuda.empty_cache()
     d = dec.Decoder(lib, torch, model, max_seq=prompt_len + 2 * n_tokens + 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -211,6 +222,7 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     pkg.check(lib)
+    prefill_rel = float(torch.linalg.vector_norm(logits_f - logits) / torch.linalg.vector_norm(logits))
     res = {}
     pos = prompt_len
     tok = d.greedy(logits)
@@ -232,7 +244,9 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             "decode_tok_s_fused": round(1.0 / res[True], 1), "decode_ms_per_token_fused": round(res[True] * 1e3, 3),
             "hbm_gbps_effective": round((weight_bytes + kv_bytes) / res[False] / 1e9, 1),
             "prefill_tokens": prompt_len, "prefill_s": round(prefill_s, 3),
-            "prefill_tok_s": round(prompt_len / prefill_s, 1), "decode_tokens_each": n_tokens,
+            "prefill_tok_s": round(prompt_len / prefill_s, 1),
+            "prefill_s_fused": round(prefill_fused_s, 3), "prefill_tok_s_fused": round(prompt_len / prefill_fused_s, 1),
+            "prefill_fused_vs_unfused_logits_rel_l2": round(prefill_rel, 7), "decode_tokens_each": n_tokens,
             "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
             "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
                      "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",

@@ -56,7 +56,7 @@ struct AttnParams {
 // Per-head RMSNorm then RoPE of one head held in LDS; one wave.
 template <int HD>
 __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope, float eps,
-                              const RopeTable& t, int lane) {
+                              const float* __restrict rc, const float* __restrict rs, int lane) {
 #pragma clang fp contract(off)
     if (norm) {
         const float inv = head_inv_rms(v, HD, eps, lane);
@@ -69,8 +69,8 @@ __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope
         constexpr int H = HD / 2;
         for (int i = lane; i < H; i += 64) {
             const float x1 = v[i], x2 = v[i + H];
-            v[i] = x1 * t.c[i] - x2 * t.s[i];
-            v[i + H] = x2 * t.c[i] + x1 * t.s[i];
+            v[i] = x1 * rc[i] - x2 * rs[i];
+            v[i + H] = x2 * rc[i] + x1 * rs[i];
         }
     }
 }
@@ -134,8 +134,8 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     __syncthreads();
     if (p.norm_qk || p.has_rope) {
         for (int h = wv; h < G + (have_new ? 1 : 0); h += kWaves) {
-            if (h < G) prologue_head<HD>(qs + h * HD, p.q_gamma, p.norm_qk, p.has_rope, p.eps, p.rope, lane);
-            else prologue_head<HD>(ks, p.k_gamma, p.norm_qk, p.has_rope, p.eps, p.rope, lane);
+            if (h < G) prologue_head<HD>(qs + h * HD, p.q_gamma, p.norm_qk, p.has_rope, p.eps, p.rope.c, p.rope.s, lane);
+            else prologue_head<HD>(ks, p.k_gamma, p.norm_qk, p.has_rope, p.eps, p.rope.c, p.rope.s, lane);
         }
         __syncthreads();
         if (split == 0) {
@@ -484,6 +484,187 @@ __global__ __launch_bounds__(kThreads) void attn_mq_kernel(AttnParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Causal prefill: B query tokens at positions pos0 .. pos0 + B - 1, each with
+// the semantics of one decode step at its position (write its K/V row, then
+// attend over its window).  Two launches:
+//   attn_prefill_prologue_kernel: per token, the heads-RMSNorm + RoPE
+//     prologue of q and k in LDS (the decode prologue's arithmetic, with the
+//     token's own host-made cos/sin row), q written back, K/V rows stored;
+//   attn_prefill_kernel (head_dim 128, G = n_heads / n_kv dividing 32): the
+//     32 M-rows of the MFMA tiles are TQ = 32 / G query tokens x G heads of
+//     one KV head; the work-group walks the block's whole key range in
+//     64-token sub-chunks with the MQA kernel's S = Q K^T, online softmax and
+//     O += P V (fp32 MFMA), masking each row to its own causal window, and
+//     writes out = O / (l + 1e-12) directly (no split, no merge).
+struct PrefillParams {
+    float* q;             // [B][n_heads * HD], prologue result in place
+    float* k;             // [B][n_kv * HD], prologue result in place
+    const float* v;       // [B][n_kv * HD]
+    float* k_cache;
+    float* v_cache;
+    float* out;           // [B][n_heads * HD]
+    const float* q_gamma;
+    const float* k_gamma;
+    const float* rope;    // [B][2][HD / 2] cos then sin rows, or null
+    int32_t pos0, batch, n_heads, n_kv, sw, norm_qk;
+    float scale, eps;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attn_prefill_prologue_kernel(PrefillParams p) {
+    extern __shared__ __align__(16) float smem[];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int qn = p.n_heads * HD, kn = p.n_kv * HD;
+    float* qr = p.q + static_cast<size_t>(t) * qn;
+    float* kr = p.k + static_cast<size_t>(t) * kn;
+    const float* vr = p.v + static_cast<size_t>(t) * kn;
+    float* qs = smem;        // [n_heads][HD]
+    float* ks = smem + qn;   // [n_kv][HD]
+    const bool rope = p.rope != nullptr;
+    if (p.norm_qk || rope) {
+        for (int i = tid; i < qn; i += kThreads) qs[i] = qr[i];
+        for (int i = tid; i < kn; i += kThreads) ks[i] = kr[i];
+        __syncthreads();
+        const float* rc = rope ? p.rope + static_cast<size_t>(t) * HD : nullptr;
+        const float* rs = rope ? rc + HD / 2 : nullptr;
+        for (int h = wv; h < p.n_heads + p.n_kv; h += kWaves) {
+            if (h < p.n_heads) prologue_head<HD>(qs + h * HD, p.q_gamma, p.norm_qk, rope, p.eps, rc, rs, lane);
+            else prologue_head<HD>(ks + (h - p.n_heads) * HD, p.k_gamma, p.norm_qk, rope, p.eps, rc, rs, lane);
+        }
+        __syncthreads();
+        for (int i = tid; i < qn; i += kThreads) qr[i] = qs[i];
+        for (int i = tid; i < kn; i += kThreads) kr[i] = ks[i];
+    } else {
+        ks = kr;  // K unchanged: stored straight from the input
+    }
+    const size_t row = static_cast<size_t>(p.pos0 + t) * kn;
+    for (int i = tid; i < kn; i += kThreads) {
+        p.k_cache[row + i] = ks[i];
+        p.v_cache[row + i] = vr[i];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p) {
+    constexpr int HD = 128;
+    constexpr int R = 32;  // MFMA M-rows: (query token, head) pairs
+    __shared__ __align__(16) float spart[2][R][kMqLd];
+    __shared__ __align__(16) float pl[R][kMqLd];
+    __shared__ float alpha_s[R], m_s[R], l_s[R];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int li = lane & 31, g = lane >> 5;
+    const int G = p.n_heads / p.n_kv, TQ = R / G;
+    const int hk = blockIdx.x;
+    const int blk = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);  // longest key ranges first
+    const int q0 = blk * TQ;
+    const int nq = min(TQ, p.batch - q0);
+    const int hi_last = p.pos0 + q0 + nq - 1;
+    const int lo_first = p.sw > 0 ? max(0, p.pos0 + q0 - p.sw + 1) : 0;
+    const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
+    const size_t q_dim = static_cast<size_t>(p.n_heads) * HD;
+    auto krow = [&](int t) { return p.k_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD; };
+    auto vrow = [&](int t) { return p.v_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD; };
+
+    const int tt = wv & 1, dh = wv >> 1;
+    const int dq = 64 * dh + 32 * g;
+    float qa[32];
+    {
+        const int qt = li / G, h = li % G;
+        if (qt < nq) {
+            const float* qr = p.q + static_cast<size_t>(q0 + qt) * q_dim + (static_cast<size_t>(hk) * G + h) * HD + dq;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(qr + 4 * i);
+                qa[4 * i] = v.x; qa[4 * i + 1] = v.y; qa[4 * i + 2] = v.z; qa[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) qa[i] = 0.0f;
+        }
+    }
+    if (tid < R) {
+        m_s[tid] = -1e30f;
+        l_s[tid] = 0.0f;
+    }
+    floatx16 o;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] = 0.0f;
+    __syncthreads();
+
+    for (int sa = lo_first; sa <= hi_last; sa += kMqSub) {
+        {
+            const int tok = sa + 32 * tt + li;
+            const float* kr = krow(tok <= hi_last ? tok : hi_last) + dq;
+            float kb[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(kr + 4 * i);
+                kb[4 * i] = v.x; kb[4 * i + 1] = v.y; kb[4 * i + 2] = v.z; kb[4 * i + 3] = v.w;
+            }
+            floatx16 sacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[kk], kb[kk], sacc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) spart[dh][8 * (r >> 2) + 4 * g + (r & 3)][32 * tt + li] = sacc[r];
+        }
+        __syncthreads();
+        // online softmax: wave w updates rows 8 w .. 8 w + 7, lane = key
+#pragma unroll
+        for (int rr = 0; rr < 8; ++rr) {
+            const int r = 8 * wv + rr;
+            const int qt = r / G;
+            const int hi = p.pos0 + q0 + qt;
+            const int lo = p.sw > 0 ? max(0, hi - p.sw + 1) : 0;
+            const int key = sa + lane;
+            const bool valid = qt < nq && key >= lo && key <= hi;
+            const float sv = valid ? (spart[0][r][lane] + spart[1][r][lane]) * p.scale : -1e30f;
+            float mx = sv;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            const float m_old = m_s[r];
+            const float m_new = fmaxf(m_old, mx);
+            const float e = valid ? expf(sv - m_new) : 0.0f;
+            const float sum = wave_sum(e);
+            pl[r][lane] = e;
+            if (lane == 0) {
+                const float a = expf(m_old - m_new);
+                alpha_s[r] = a;
+                l_s[r] = l_s[r] * a + sum;
+                m_s[r] = m_new;
+            }
+        }
+        __syncthreads();
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[r] *= alpha_s[8 * (r >> 2) + 4 * g + (r & 3)];
+            float pa[32], vb[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(&pl[li][32 * g + 4 * i]);
+                pa[4 * i] = v.x; pa[4 * i + 1] = v.y; pa[4 * i + 2] = v.z; pa[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) {
+                const int t = sa + 32 * g + kk;
+                vb[kk] = vrow(t <= hi_last ? t : hi_last)[32 * wv + li];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 32; ++kk) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[kk], vb[kk], o, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int qt = row / G, h = row % G;
+        if (qt < nq)
+            p.out[static_cast<size_t>(q0 + qt) * q_dim + (static_cast<size_t>(hk) * G + h) * HD + 32 * wv + li] =
+                o[r] * (1.0f / (l_s[row] + 1e-12f));
+    }
+}
+
 // out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12), one
 // work-group per query head.  Thread (d4, g) owns float4 d4 of the head and
 // splits g, g + ng, ...; its first kMergeU partial loads are issued before the
@@ -699,6 +880,49 @@ hipError_t launch_mq(const AttnArgs& a, const Plan& pl, float* part_o, float* pa
 }
 
 }  // namespace
+
+bool attention_prefill_supported(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0) return false;
+    const int32_t G = n_heads / n_kv_heads;
+    if (G > 32 || 32 % G != 0) return false;
+    return sizeof(float) * static_cast<size_t>(n_heads + n_kv_heads) * head_dim <= kLdsBudget;
+}
+
+hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream) {
+    if (a.batch <= 0) return hipSuccess;
+    if (!attention_prefill_supported(a.n_heads, a.n_kv_heads, a.head_dim) || a.pos0 < 0) return hipErrorInvalidValue;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
+                         reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out) |
+                         reinterpret_cast<uintptr_t>(a.k_cache) | reinterpret_cast<uintptr_t>(a.v_cache);
+    if (al & 15u) return hipErrorInvalidValue;
+    const int32_t G = a.n_heads / a.n_kv_heads, TQ = 32 / G;
+    const int32_t nblk = (a.batch + TQ - 1) / TQ;
+    if (nblk > 65535) return hipErrorInvalidValue;
+    PrefillParams p{};
+    p.q = a.q;
+    p.k = a.k;
+    p.v = a.v;
+    p.k_cache = a.k_cache;
+    p.v_cache = a.v_cache;
+    p.out = a.out;
+    p.q_gamma = a.q_gamma;
+    p.k_gamma = a.k_gamma;
+    p.rope = a.rope;
+    p.pos0 = a.pos0;
+    p.batch = a.batch;
+    p.n_heads = a.n_heads;
+    p.n_kv = a.n_kv_heads;
+    p.sw = a.sliding_window;
+    p.norm_qk = a.norm_qk;
+    p.scale = a.scale;
+    p.eps = a.eps;
+    const size_t lds = (a.norm_qk || a.rope) ? sizeof(float) * static_cast<size_t>(a.n_heads + a.n_kv_heads) * 128 : 0;
+    hipLaunchKernelGGL(attn_prefill_prologue_kernel<128>, dim3(a.batch), dim3(kThreads), lds, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_kv_heads, nblk), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+}
 
 size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window) {
     // upper bound over n_kv: chunks of at least 32 tokens, at most kMergeMaxSplit of them

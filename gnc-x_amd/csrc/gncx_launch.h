@@ -75,6 +75,29 @@ struct AttnArgs {
     float* k_out;             // prologue result for k_new written back (optional)
 };
 size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window);
+
+// Causal prefill of `batch` tokens at positions pos0 .. pos0 + batch - 1: per
+// token the heads-RMSNorm + RoPE prologue (q and k in place), its K/V row
+// stored, then attention over its own window, all tokens at once.
+struct PrefillArgs {
+    float* q;        // [batch][n_heads * head_dim]
+    float* k;        // [batch][n_kv_heads * head_dim]
+    const float* v;  // [batch][n_kv_heads * head_dim]
+    float* k_cache;  // rows [0, pos0) already filled
+    float* v_cache;
+    float* out;      // [batch][n_heads * head_dim]
+    int32_t pos0, batch, n_heads, n_kv_heads, head_dim;
+    float scale;
+    int32_t sliding_window;
+    int32_t norm_qk;
+    const float* q_gamma;
+    const float* k_gamma;
+    float eps;
+    const float* rope;  // device [batch][head_dim]: cos[head_dim / 2] then sin, or null
+};
+// shapes the batched kernels take: head_dim 128, n_heads / n_kv_heads dividing 32
+bool attention_prefill_supported(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim);
+hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace_bytes,
                             hipStream_t stream);
 

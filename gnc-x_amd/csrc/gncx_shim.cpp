@@ -1034,15 +1034,14 @@ GNCX_API void gncx_hip_quantize_act(const float* in, int32_t rows, int32_t in_di
 // the normalised, rotated vectors as those calls leave them.  Norm weights are
 // addressed like the reference's (base + offset, has_weight); rope_base <= 0
 // skips the rotation.
-GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
-                                            float* v_cache_layer, int32_t pos, int32_t n_heads,
-                                            int32_t n_kv_heads, int32_t head_dim, float attn_scale,
-                                            int32_t sliding_window, int32_t write_kv, const uint8_t* mmap_base,
-                                            size_t q_norm_offset, size_t k_norm_offset, int32_t has_norm_weight,
-                                            float norm_eps, size_t rope_freqs_offset, int32_t has_rope_freqs,
-                                            float rope_base, float* out_attn_vec) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    const char* where = "gncx_hip_attention_step_fused";
+namespace {
+// the body of gncx_hip_attention_step_fused; the caller holds g_mu
+void attention_step_fused_impl(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
+                               float* v_cache_layer, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
+                               int32_t head_dim, float attn_scale, int32_t sliding_window, int32_t write_kv,
+                               const uint8_t* mmap_base, size_t q_norm_offset, size_t k_norm_offset,
+                               int32_t has_norm_weight, float norm_eps, size_t rope_freqs_offset,
+                               int32_t has_rope_freqs, float rope_base, float* out_attn_vec, const char* where) {
     if (!ensure_runtime(where)) return;
     const float* qg = nullptr;
     const float* kg = nullptr;
@@ -1079,4 +1078,181 @@ GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const fl
     c.q_back = q_vec;
     c.k_back = k_vec;
     attention_impl(c, where);
+}
+
+// RoPE rows of positions pos0 .. pos0 + batch - 1 ([batch][head_dim]: cos
+// then sin, host libm like the single-position table), kept on the device
+// for the next call with the same key (every layer of one prefill)
+struct RopeRows {
+    DevBuf buf;
+    int32_t pos0 = -1, batch = 0, head_dim = 0;
+    float base = 0.0f;
+    std::array<float, kMaxRopeHalf> fac{};
+    bool has_fac = false;
+} g_rope_rows;
+
+const float* rope_rows(int32_t pos0, int32_t batch, int32_t head_dim, float base, const float* factors,
+                       const char* where) {
+    RopeRows& r = g_rope_rows;
+    const int32_t half = head_dim / 2;
+    const bool same = r.pos0 == pos0 && r.batch == batch && r.head_dim == head_dim && r.base == base &&
+                      r.has_fac == (factors != nullptr) &&
+                      (!factors || std::memcmp(r.fac.data(), factors, sizeof(float) * half) == 0);
+    if (same) return r.buf.as<float>();
+    std::vector<float> tab(static_cast<size_t>(batch) * head_dim);
+    RopeTable t;
+    for (int32_t i = 0; i < batch; ++i) {
+        if (!rope_table(pos0 + i, head_dim, base, factors, t)) {
+            set_error(where, "head_dim must be even and at most 512", -1);
+            return nullptr;
+        }
+        std::memcpy(&tab[static_cast<size_t>(i) * head_dim], t.c, sizeof(float) * half);
+        std::memcpy(&tab[static_cast<size_t>(i) * head_dim + half], t.s, sizeof(float) * half);
+    }
+    r.pos0 = -1;
+    // a kernel queued with the previous rows may still read them
+    if (!check(hipStreamSynchronize(g_rt.stream), where)) return nullptr;
+    if (!r.buf.ensure(sizeof(float) * tab.size(), where)) return nullptr;
+    if (!check(hipMemcpy(r.buf.p, tab.data(), sizeof(float) * tab.size(), hipMemcpyHostToDevice), where))
+        return nullptr;
+    r.pos0 = pos0;
+    r.batch = batch;
+    r.head_dim = head_dim;
+    r.base = base;
+    r.has_fac = factors != nullptr;
+    if (factors) std::memcpy(r.fac.data(), factors, sizeof(float) * half);
+    return r.buf.as<float>();
+}
+}  // namespace
+
+GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
+                                            float* v_cache_layer, int32_t pos, int32_t n_heads,
+                                            int32_t n_kv_heads, int32_t head_dim, float attn_scale,
+                                            int32_t sliding_window, int32_t write_kv, const uint8_t* mmap_base,
+                                            size_t q_norm_offset, size_t k_norm_offset, int32_t has_norm_weight,
+                                            float norm_eps, size_t rope_freqs_offset, int32_t has_rope_freqs,
+                                            float rope_base, float* out_attn_vec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    attention_step_fused_impl(q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim,
+                              attn_scale, sliding_window, write_kv, mmap_base, q_norm_offset, k_norm_offset,
+                              has_norm_weight, norm_eps, rope_freqs_offset, has_rope_freqs, rope_base, out_attn_vec,
+                              "gncx_hip_attention_step_fused");
+}
+
+// gncx_hip_attention_step_fused for tokens pos0 .. pos0 + batch - 1 in turn
+// (write_kv = 1), as one batched causal pass where the kernels take the shape
+GNCX_API void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const float* v_batch, float* k_cache_layer,
+                                         float* v_cache_layer, int32_t pos0, int32_t batch, int32_t n_heads,
+                                         int32_t n_kv_heads, int32_t head_dim, float attn_scale,
+                                         int32_t sliding_window, const uint8_t* mmap_base, size_t q_norm_offset,
+                                         size_t k_norm_offset, int32_t has_norm_weight, float norm_eps,
+                                         size_t rope_freqs_offset, int32_t has_rope_freqs, float rope_base,
+                                         float* out_batch) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_attention_prefill";
+    if (!ensure_runtime(where) || batch <= 0) return;
+    if (pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_heads % n_kv_heads != 0 || !q_batch ||
+        !k_batch || !v_batch || !k_cache_layer || !v_cache_layer || !out_batch) {
+        set_error(where, "invalid head geometry, position or pointer", -1);
+        return;
+    }
+    const size_t qn = static_cast<size_t>(n_heads) * head_dim, kn = static_cast<size_t>(n_kv_heads) * head_dim;
+    if (!attention_prefill_supported(n_heads, n_kv_heads, head_dim)) {
+        for (int32_t t = 0; t < batch; ++t)
+            attention_step_fused_impl(q_batch + t * qn, k_batch + t * kn, v_batch + t * kn, k_cache_layer,
+                                      v_cache_layer, pos0 + t, n_heads, n_kv_heads, head_dim, attn_scale,
+                                      sliding_window, 1, mmap_base, q_norm_offset, k_norm_offset, has_norm_weight,
+                                      norm_eps, rope_freqs_offset, has_rope_freqs, rope_base, out_batch + t * qn,
+                                      where);
+        return;
+    }
+    const float* qg = nullptr;
+    const float* kg = nullptr;
+    if (has_norm_weight) {
+        qg = reinterpret_cast<const float*>(
+            device_weights(mmap_base + q_norm_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
+        kg = reinterpret_cast<const float*>(
+            device_weights(mmap_base + k_norm_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
+        if (!qg || !kg) return;
+    }
+    const float* rope = nullptr;
+    if (rope_base > 0.0f) {
+        std::array<float, kMaxRopeHalf> fac{};
+        const float* factors = nullptr;
+        if (has_rope_freqs) {
+            if (!read_factors(mmap_base, rope_freqs_offset, head_dim / 2, fac, where)) return;
+            factors = fac.data();
+        }
+        rope = rope_rows(pos0, batch, head_dim, rope_base, factors, where);
+        if (!rope) return;
+    }
+    const size_t nq = static_cast<size_t>(batch) * qn, nk = static_cast<size_t>(batch) * kn;
+    const bool host_q = !is_device_ptr(q_batch), host_k = !is_device_ptr(k_batch);
+    float* qd = host_q ? const_cast<float*>(stage_in(q_batch, nq, g_rt.q, where)) : q_batch;
+    float* kd = host_k ? const_cast<float*>(stage_in(k_batch, nk, g_rt.k, where)) : k_batch;
+    const float* vd = stage_in(v_batch, nk, g_rt.v, where);
+    if (!qd || !kd || !vd) return;
+    const int32_t kv_dim = static_cast<int32_t>(kn);
+    const bool host_kc = !is_device_ptr(k_cache_layer), host_vc = !is_device_ptr(v_cache_layer);
+    float* kc = host_kc ? kv_twin(k_cache_layer, kv_dim, pos0, pos0 + batch, where) : k_cache_layer;
+    if (!kc) return;
+    float* vc = host_vc ? kv_twin(v_cache_layer, kv_dim, pos0, pos0 + batch, where) : v_cache_layer;
+    if (!vc) return;
+    bool host_out = false;
+    float* od = out_target(out_batch, nq, g_rt.o, host_out, where);
+    if (!od) return;
+    PrefillArgs a{};
+    a.q = qd;
+    a.k = kd;
+    a.v = vd;
+    a.k_cache = kc;
+    a.v_cache = vc;
+    a.out = od;
+    a.pos0 = pos0;
+    a.batch = batch;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.scale = attn_scale;
+    a.sliding_window = sliding_window;
+    a.norm_qk = 1;
+    a.q_gamma = qg;
+    a.k_gamma = kg;
+    a.eps = norm_eps;
+    a.rope = rope;
+    if (!check(launch_attention_prefill(a, g_rt.stream), where)) return;
+    // host copies: the caches' new rows (the reference writes them in the call), q / k (prologue results), out
+    const size_t row0 = static_cast<size_t>(pos0) * kn;
+    auto back = [&](float* host, const float* dev, size_t n) {
+        return check(hipMemcpyAsync(host, dev, sizeof(float) * n, hipMemcpyDeviceToHost, g_rt.stream), where);
+    };
+    if (host_kc && !back(k_cache_layer + row0, kc + row0, nk)) return;
+    if (host_vc && !back(v_cache_layer + row0, vc + row0, nk)) return;
+    if (host_q && !back(q_batch, qd, nq)) return;
+    if (host_k && !back(k_batch, kd, nk)) return;
+    if (host_out && !back(out_batch, od, nq)) return;
+    if ((host_kc || host_vc || host_q || host_k || host_out) && !check(hipStreamSynchronize(g_rt.stream), where))
+        return;
+    if (host_kc) kv_mark_written(k_cache_layer, pos0 + batch - 1);
+    if (host_vc) kv_mark_written(v_cache_layer, pos0 + batch - 1);
+}
+
+// RMSNorm of `rows` contiguous vectors of dim with one gamma
+GNCX_API void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t* mmap_base,
+                                    size_t norm_weight_offset, int32_t dim, float eps, float* out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_rmsnorm_rows";
+    g_norm_epoch++;
+    if (rows <= 0 || dim <= 0 || !in || !out || !ensure_runtime(where)) return;
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
+    if (!g) return;
+    const size_t n = static_cast<size_t>(rows) * dim;
+    const float* x = stage_in(in, n, g_rt.q, where);
+    if (!x) return;
+    bool host = false;
+    float* o = out_target(out, n, g_rt.o, host, where);
+    if (!o) return;
+    if (!check(launch_rmsnorm(x, g, rows, dim, eps, o, g_rt.stream), where)) return;
+    finish_out(out, o, n, host, where);
 }

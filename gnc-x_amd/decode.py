@@ -17,9 +17,12 @@ differences are where the streamer works on host memory:
 * the sampler is a greedy device argmax (the streamer's sampler adds a
   repetition penalty on the host, lua/gncx_streamer.lua:1229-1272);
 * `fused=True` uses the library's launch-saving extensions, with the same
-  results: gncx_hip_attention_step_fused for the four prologue+attention
-  calls, gncx_hip_matvec_multi for Q/K/V and for gate/up (one launch each),
-  and gncx_hip_add_rmsnorm for each residual add and the RMSNorm after it.
+  results: in decode, gncx_hip_attention_step_fused for the four
+  prologue+attention calls, gncx_hip_matvec_multi for Q/K/V and for gate/up
+  (one launch each) and gncx_hip_add_rmsnorm for each residual add and the
+  RMSNorm after it; in prefill, gncx_hip_rmsnorm_rows for the per-token
+  RMSNorm loops and gncx_hip_attention_prefill for the per-token prologue +
+  attention loop (one causal batch).
 
 Weights are random-init with the block statistics of the synthetic
 benchmark inputs: fp16 scales |N(0, 0.02)|, uniform random code bytes,
@@ -288,6 +291,8 @@ class Decoder:
         rowp = lambda t, i: t.data_ptr() + 4 * i * t.shape[1]  # noqa: E731
         for i, tok in enumerate(token_ids):
             self._embed(tok, rowp(bh, i))
+        if self.fused:
+            return self._prefill_fused(B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf)
         for l in range(s.n_layers):
             p = f"blk.{l}"
             for i in range(B):
@@ -301,6 +306,34 @@ class Decoder:
             L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
             for i in range(B):
                 self._norm(f"{p}.ffn_norm.weight", rowp(bh, i), rowp(bn, i))
+            self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
+            self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
+            L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
+            self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
+            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+        self.hidden.copy_(bh[B - 1])
+        return self._lm_head()
+
+    def _prefill_fused(self, B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf):
+        """prefill's layers with the extensions: every token's RMSNorm in one
+        launch, and the per-token prologue + attention loop as one causal
+        batch (gncx_hip_attention_prefill)."""
+        s, L, m = self.s, self.lib, self.m
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"), s.embed, s.eps,
+                                    bn.data_ptr())
+            self._matbatch(f"{p}.attn_q.weight", bn.data_ptr(), B, s.embed, s.q_dim, bq.data_ptr())
+            self._matbatch(f"{p}.attn_k.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bk.data_ptr())
+            self._matbatch(f"{p}.attn_v.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bv.data_ptr())
+            L.gncx_hip_attention_prefill(bq.data_ptr(), bk.data_ptr(), bv.data_ptr(), self.kc[l].data_ptr(),
+                                         self.vc[l].data_ptr(), 0, B, s.n_heads, s.n_kv, s.head_dim, self.scale, 0,
+                                         m.base, m.off(f"{p}.attn_q_norm.weight"), m.off(f"{p}.attn_k_norm.weight"),
+                                         1, s.eps, 0, 0, s.rope_base, ba.data_ptr())
+            self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
+            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"), s.embed, s.eps,
+                                    bn.data_ptr())
             self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
             self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
             L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())

@@ -187,6 +187,23 @@ void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_ve
  * output equals what gncx_xfold_universal_matvec gives for that matrix. */
 void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
                            int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_vecs);
+/* gncx_hip_attention_step_fused (write_kv = 1) for tokens pos0 .. pos0 +
+ * batch - 1 in turn, as one causal batch: q_batch [batch][n_heads*head_dim],
+ * k_batch / v_batch [batch][n_kv_heads*head_dim] (q and k receive the
+ * normalised, rotated rows), out_batch [batch][n_heads*head_dim], cache rows
+ * [0, pos0) already filled.  For the streamer's per-token prefill loop
+ * (lua/gncx_streamer.lua:1079-1109). */
+void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const float* v_batch, float* k_cache_layer,
+                                float* v_cache_layer, int32_t pos0, int32_t batch, int32_t n_heads,
+                                int32_t n_kv_heads, int32_t head_dim, float attn_scale, int32_t sliding_window,
+                                const uint8_t* mmap_base, size_t q_norm_offset, size_t k_norm_offset,
+                                int32_t has_norm_weight, float norm_eps, size_t rope_freqs_offset,
+                                int32_t has_rope_freqs, float rope_base, float* out_batch);
+/* The RMSNorm of gncx_rmsnorm_and_encode_4phase (no tokens) of each of `rows`
+ * contiguous vectors of dim, one launch (the streamer normalises prefill
+ * rows one call each, lua/gncx_streamer.lua:1059-1065 and 1126-1132). */
+void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t* mmap_base, size_t norm_weight_offset,
+                           int32_t dim, float eps, float* out);
 /* hidden[i] += delta[i], then out_normed_fp32 = the RMSNorm of
  * gncx_rmsnorm_and_encode_4phase (cpp:789-833) of the new hidden, in one
  * kernel; the same values as gncx_hip_vec_add followed by that call. */

@@ -258,3 +258,102 @@ def test_rmsnorm_swiglu_embeddings(lib, golden, oracle):
         assert np.array_equal(e, golden[f"emb_{name}_y5"])
         fn(ptr(tab), 0, 11, 512, 0.37, ptr(e))
         assert np.array_equal(e, golden[f"emb_{name}_y11s"])
+
+
+PREFILL_CASES = [
+    # (H, KV, hd, pos0, B, sw): fresh prompt, a cache prefix, a sliding window,
+    # MQA (32 heads on one KV head), one head per KV head, and a head_dim the
+    # batched kernels do not take (one fused step per token inside the call)
+    (32, 8, 128, 0, 100, 0),
+    (32, 8, 128, 37, 70, 0),
+    (32, 8, 128, 5, 50, 16),
+    (32, 1, 128, 3, 20, 0),
+    (16, 16, 128, 0, 40, 0),
+    (8, 2, 64, 2, 10, 0),
+]
+
+
+def _prefill_inputs(H, KV, hd, pos0, B, seed):
+    rng = np.random.default_rng(seed)
+    rows = pos0 + B
+    kc = np.zeros((rows, KV * hd), np.float32)
+    vc = np.zeros((rows, KV * hd), np.float32)
+    kc[:pos0] = rng.standard_normal((pos0, KV * hd), dtype=np.float32)
+    vc[:pos0] = rng.standard_normal((pos0, KV * hd), dtype=np.float32)
+    q = rng.standard_normal((B, H * hd), dtype=np.float32)
+    k = rng.standard_normal((B, KV * hd), dtype=np.float32)
+    v = rng.standard_normal((B, KV * hd), dtype=np.float32)
+    norms = np.concatenate([synth.make_norm_gamma(hd, 3), synth.make_norm_gamma(hd, 4)]).astype(np.float32)
+    return kc, vc, q, k, v, norms
+
+
+@pytest.mark.parametrize("H,KV,hd,pos0,B,sw", PREFILL_CASES)
+def test_attention_prefill_equals_fused_steps(lib, H, KV, hd, pos0, B, sw):
+    """gncx_hip_attention_prefill == gncx_hip_attention_step_fused per token in
+    turn (host buffers): q/k prologue results and the new cache rows bit for
+    bit, outputs within 1e-5 (online softmax against split-K plus merge)."""
+    kc, vc, q, k, v, norms = _prefill_inputs(H, KV, hd, pos0, B, H * 1000 + B + pos0)
+    eps, base, scale = 1e-6, 1e6, 1 / np.sqrt(hd)
+    q1, k1, kc1, vc1 = q.copy(), k.copy(), kc.copy(), vc.copy()
+    out1 = np.zeros((B, H * hd), np.float32)
+    for t in range(B):
+        lib.gncx_hip_attention_step_fused(ptr(q1[t]), ptr(k1[t]), ptr(v[t]), ptr(kc1), ptr(vc1), pos0 + t, H, KV, hd,
+                                          scale, sw, 1, ptr(norms), 0, hd * 4, 1, eps, 0, 0, base, ptr(out1[t]))
+    gncx.check(lib)
+    lib.gncx_hip_kv_forget(None)
+    q2, k2, kc2, vc2 = q.copy(), k.copy(), kc.copy(), vc.copy()
+    out2 = np.zeros((B, H * hd), np.float32)
+    lib.gncx_hip_attention_prefill(ptr(q2), ptr(k2), ptr(v), ptr(kc2), ptr(vc2), pos0, B, H, KV, hd, scale, sw,
+                                   ptr(norms), 0, hd * 4, 1, eps, 0, 0, base, ptr(out2))
+    gncx.check(lib)
+    lib.gncx_hip_kv_forget(None)
+    assert np.array_equal(q1, q2) and np.array_equal(k1, k2)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+    errs = [rel_l2(out2[t], out1[t]) for t in range(B)]
+    print(f"prefill H={H} KV={KV} hd={hd} pos0={pos0} B={B} sw={sw} max row rel_l2={max(errs):.2e}")
+    assert max(errs) < 1e-5
+
+
+def test_attention_prefill_device_buffers(lib, oracle):
+    """Device-resident buffers (used in place), against the oracle's
+    per-token prologue + attention sequence."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    H, KV, hd, pos0, B = 32, 8, 128, 10, 64
+    kc, vc, q, k, v, norms = _prefill_inputs(H, KV, hd, pos0, B, 99)
+    eps, base, scale = 1e-6, 1e6, 1 / np.sqrt(hd)
+    gq, gk = norms[:hd], norms[hd:]
+    okc, ovc = kc.copy(), vc.copy()
+    want = np.zeros((B, H * hd), np.float32)
+    for t in range(B):
+        oq = oracle.rmsnorm_heads(q[t], gq, H, hd, eps)
+        ok = oracle.rmsnorm_heads(k[t], gk, KV, hd, eps)
+        oq, ok = oracle.rope(oq, ok, H, KV, hd, pos0 + t, base)
+        want[t], okc, ovc = oracle.attention(oq, ok, v[t], okc, ovc, pos0 + t, H, KV, hd, scale, 0, 1)
+    d = {n: torch.from_numpy(a.copy()).cuda() for n, a in
+         dict(q=q, k=k, v=v, kc=kc, vc=vc, norms=norms).items()}
+    out = torch.zeros(B, H * hd, device="cuda")
+    lib.gncx_hip_attention_prefill(d["q"].data_ptr(), d["k"].data_ptr(), d["v"].data_ptr(), d["kc"].data_ptr(),
+                                   d["vc"].data_ptr(), pos0, B, H, KV, hd, scale, 0, d["norms"].data_ptr(), 0,
+                                   hd * 4, 1, eps, 0, 0, base, out.data_ptr())
+    gncx.check(lib)
+    got = out.cpu().numpy()
+    errs = [rel_l2(got[t], want[t]) for t in range(B)]
+    print(f"prefill device vs oracle: max row rel_l2={max(errs):.2e}")
+    assert max(errs) < TOL
+    assert rel_l2(d["kc"].cpu().numpy(), okc) < 1e-6
+
+
+@pytest.mark.parametrize("rows,dim", [(5, 4096), (3, 4098), (2, 20000)])
+def test_rmsnorm_rows_equals_per_row_calls(lib, rows, dim):
+    rng = np.random.default_rng(rows * dim)
+    x = (rng.standard_normal((rows, dim)) * 2).astype(np.float32)
+    g = synth.make_norm_gamma(dim, 11)
+    want = np.zeros_like(x)
+    for r in range(rows):
+        lib.gncx_rmsnorm_and_encode_4phase(ptr(x[r]), ptr(g), 0, dim, 1e-6, 0, ptr(want[r]), None, None)
+    got = np.zeros_like(x)
+    lib.gncx_hip_rmsnorm_rows(ptr(x), rows, ptr(g), 0, dim, 1e-6, ptr(got))
+    gncx.check(lib)
+    assert np.array_equal(got, want)

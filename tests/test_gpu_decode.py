@@ -96,12 +96,18 @@ def test_decode_steps_match_oracle(lib, oracle, torch_mod, fused):
         assert err < TOL, (pos, err)
 
 
-def test_prefill_then_decode_matches_oracle(lib, oracle, torch_mod):
-    """prefill (matbatch projections on fp16 matrix cores, per-token attention)
-    then greedy decode steps, teacher-forced on both sides."""
+@pytest.mark.parametrize("fused,hd", [(False, 64), (True, 64), (True, 128)])
+def test_prefill_then_decode_matches_oracle(lib, oracle, torch_mod, fused, hd):
+    """prefill (matbatch projections on fp16 matrix cores; per-token norms and
+    attention, or with fused=True batched norms and one causal attention pass:
+    the batched kernels at head_dim 128, one step per token at 64) then greedy
+    decode steps, teacher-forced on both sides."""
     import gncx_amd.decode as dec
-    model = dec.build_model(torch_mod, small_shape(), seed=9)
-    d = dec.Decoder(lib, torch_mod, model, max_seq=64)
+    shape = small_shape()
+    if hd != shape.head_dim:
+        shape = dec.Qwen3Shape(n_layers=2, embed=256, n_heads=4, n_kv=2, head_dim=hd, ffn=512, vocab=600)
+    model = dec.build_model(torch_mod, shape, seed=9)
+    d = dec.Decoder(lib, torch_mod, model, max_seq=64, fused=fused)
     ref = OracleModel(oracle, model)
     prompt = [11, 22, 33, 44, 55, 66, 77, 88, 99, 123, 321, 456]
     got = d.prefill(prompt).cpu().numpy()
@@ -109,7 +115,7 @@ def test_prefill_then_decode_matches_oracle(lib, oracle, torch_mod):
     for pos, tok in enumerate(prompt):
         want = ref.step(tok, pos)
     err = rel_l2(got, want)
-    print(f"prefill rel_l2={err:.2e}")
+    print(f"prefill fused={fused} rel_l2={err:.2e}")
     assert err < TOL_PREFILL
     tok = d.greedy(d.logits)
     for pos in range(len(prompt), len(prompt) + 3):
