@@ -67,12 +67,15 @@ QWEN3_8B = Qwen3Shape()
 @dataclass
 class Model:
     shape: Qwen3Shape
-    blob: object  # torch uint8 tensor on the device
+    blob: object  # torch uint8 tensor on the device, or a host mapping of a GGUF file
     offsets: dict = field(default_factory=dict)  # tensor name -> byte offset in blob
 
     @property
     def base(self) -> int:
-        return self.blob.data_ptr()
+        """Address of byte 0: device memory for a torch blob, host memory for
+        a mapped GGUF file (the streamer's mmap base, which the library
+        uploads from once per tensor)."""
+        return self.blob.data_ptr() if hasattr(self.blob, "data_ptr") else self.blob.ctypes.data
 
     def off(self, name: str) -> int:
         return self.offsets[name]
@@ -134,6 +137,94 @@ def build_model(torch, shape: Qwen3Shape = QWEN3_8B, seed: int = 0, device: str 
             d = (0.02 * torch.randn(nb, 1, generator=g, device=device)).abs().to(torch.float16)
             blk[:, 208:210].copy_(d.view(torch.uint8).view(nb, 2))
     return Model(shape, blob, offsets)
+
+
+# -- GGUF model files ---------------------------------------------------------
+def _gguf_dims(kind, rows, cols):
+    return (cols,) if kind == "f32" else (cols, rows)  # ggml order: row length first
+
+
+def write_model_gguf(path, shape: Qwen3Shape = QWEN3_8B, seed: int = 0) -> dict:
+    """A qwen3 GGUF file with the metadata keys the streamer reads
+    (lua/gncx_streamer.lua:345-366, 444-451) and random-init tensors with the
+    block statistics of build_model, generated on the host one tensor at a
+    time.  The vocabulary is `shape.vocab` dummy tokens (the streamer takes
+    the vocabulary size from their count).  Returns {name: file offset}."""
+    import numpy as np
+
+    from . import gguf as G
+
+    rng = np.random.default_rng(seed)
+    a = "qwen3"
+    meta = [
+        ("general.architecture", G.STRING, a),
+        ("general.alignment", G.UINT32, _ALIGN),
+        (f"{a}.block_count", G.UINT32, shape.n_layers),
+        (f"{a}.context_length", G.UINT32, 40960),
+        (f"{a}.embedding_length", G.UINT32, shape.embed),
+        (f"{a}.feed_forward_length", G.UINT32, shape.ffn),
+        (f"{a}.attention.head_count", G.UINT32, shape.n_heads),
+        (f"{a}.attention.head_count_kv", G.UINT32, shape.n_kv),
+        (f"{a}.attention.key_length", G.UINT32, shape.head_dim),
+        (f"{a}.attention.value_length", G.UINT32, shape.head_dim),
+        (f"{a}.attention.layer_norm_rms_epsilon", G.FLOAT32, shape.eps),
+        (f"{a}.rope.freq_base", G.FLOAT32, shape.rope_base),
+        ("tokenizer.ggml.model", G.STRING, "gpt2"),
+        ("tokenizer.ggml.tokens", G.ARRAY, (G.STRING, [f"<t{i}>" for i in range(shape.vocab)])),
+        ("tokenizer.ggml.token_type", G.ARRAY, (G.INT32, [1] * shape.vocab)),
+        ("tokenizer.ggml.merges", G.ARRAY, (G.STRING, [])),
+        ("tokenizer.ggml.eos_token_id", G.UINT32, 151645),
+    ]
+
+    def writer(kind, rows, cols):
+        def w(f):
+            if kind == "f32":
+                f.write((1.0 + 0.1 * rng.standard_normal(rows * cols)).astype(np.float32).tobytes())
+                return
+            bb = 144 if kind == Q4_K else 210
+            nb_row = row_bytes(kind, cols) // bb
+            for r0 in range(0, rows, 1024):  # bounded host memory per chunk
+                nb = min(1024, rows - r0) * nb_row
+                blk = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+                if kind == Q4_K:
+                    blk[:, 0:4] = np.abs(0.02 * rng.standard_normal((nb, 2))).astype(np.float16).view(np.uint8)
+                else:
+                    blk[:, 192:208] = rng.integers(-32, 32, (nb, 16), dtype=np.int8).view(np.uint8)
+                    blk[:, 208:210] = np.abs(0.02 * rng.standard_normal((nb, 1))).astype(np.float16).view(np.uint8)
+                f.write(blk.tobytes())
+        return w
+
+    specs = []
+    for name, kind, rows, cols in _layout(shape):
+        t = G.F32 if kind == "f32" else kind
+        specs.append(G.TensorSpec(name, t, _gguf_dims(kind, rows, cols), writer(kind, rows, cols)))
+    return G.write_gguf(path, meta, specs)
+
+
+def load_model_gguf(path) -> Model:
+    """Map a GGUF file (read-only, host memory) and read the shape from its
+    metadata as GNCXStreamer.new does (lua/gncx_streamer.lua:345-366): the
+    Model's base is the mapping's address and its offsets the tensors'
+    absolute file offsets, so every weight reaches the library as the
+    streamer passes it, a host pointer (base, offset)."""
+    import numpy as np
+
+    from . import gguf as G
+
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    meta, tensors, _ = G.read_gguf(mm)
+    a = meta.get("general.architecture", "qwen3")
+    n_heads = int(meta[f"{a}.attention.head_count"])
+    embed = int(meta[f"{a}.embedding_length"])
+    shape = Qwen3Shape(
+        n_layers=int(meta[f"{a}.block_count"]), embed=embed, n_heads=n_heads,
+        n_kv=int(meta.get(f"{a}.attention.head_count_kv", n_heads)),
+        head_dim=int(meta.get(f"{a}.attention.key_length", embed // n_heads)),
+        ffn=int(meta[f"{a}.feed_forward_length"]), vocab=len(meta.get("tokenizer.ggml.tokens", [])),
+        eps=float(meta.get(f"{a}.attention.layer_norm_rms_epsilon", 1e-6)),
+        rope_base=float(meta.get(f"{a}.rope.freq_base", 10000.0)),
+        layer_type=tensors["blk.0.attn_q.weight"].ggml_type, embd_type=tensors["token_embd.weight"].ggml_type)
+    return Model(shape, mm, {n: t.abs_file_offset for n, t in tensors.items()})
 
 
 class Decoder:
