@@ -236,9 +236,25 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
         torch.cuda.synchronize()
         res[fused] = (time.perf_counter() - t0) / n_tokens
         pkg.check(lib)
+    # the unchanged streamer's contract: every buffer and KV cache in host
+    # memory, so each call stages its inputs and writes its outputs back
+    # before returning (short prompt: its per-token prefill alone syncs
+    # ~10 times per token and layer)
+    host_prompt, host_tokens = 128, 32
+    del d
+    torch.cuda.empty_cache()
+    dh = dec.Decoder(lib, torch, model, max_seq=host_prompt + host_tokens + 1, device="cpu")
+    tok_h = dh.greedy(dh.prefill(prompt[:host_prompt]))
+    t0 = time.perf_counter()
+    for i in range(host_tokens):
+        tok_h = dh.greedy(dh.forward_token(tok_h, host_prompt + i))
+    host_s = (time.perf_counter() - t0) / host_tokens
+    pkg.check(lib)
+    del dh
+    lib.gncx_hip_kv_forget(None)
     weight_bytes = model.blob.numel()
     kv_bytes = 2 * s.n_layers * s.kv_dim * 4 * (prompt_len + n_tokens)  # K and V rows read at the mid position
-    del d, model
+    del model
     torch.cuda.empty_cache()
     return {"decode_tok_s": round(1.0 / res[False], 1), "decode_ms_per_token": round(res[False] * 1e3, 3),
             "decode_tok_s_fused": round(1.0 / res[True], 1), "decode_ms_per_token_fused": round(res[True] * 1e3, 3),
@@ -247,6 +263,9 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             "prefill_tok_s": round(prompt_len / prefill_s, 1),
             "prefill_s_fused": round(prefill_fused_s, 3), "prefill_tok_s_fused": round(prompt_len / prefill_fused_s, 1),
             "prefill_fused_vs_unfused_logits_rel_l2": round(prefill_rel, 7), "decode_tokens_each": n_tokens,
+            "decode_tok_s_host_buffers": round(1.0 / host_s, 1),
+            "host_buffers_positions": f"{host_prompt}..{host_prompt + host_tokens - 1} (every call's inputs and "
+                                      "outputs in host memory, as the unchanged streamer passes them)",
             "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
             "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
                      "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",

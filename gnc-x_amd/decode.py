@@ -7,13 +7,16 @@ a Qwen3 model (the `is_qwen` branches: per-head Q/K RMSNorm, NEOX RoPE at
 SwiGLU, the tied `token_embd.weight` as embedding table and lm_head).  The
 differences are where the streamer works on host memory:
 
-* every buffer is device memory (torch tensors whose data_ptr() goes through
-  the C-ABI, which the library uses in place);
+* by default every buffer is device memory (torch tensors whose data_ptr()
+  goes through the C-ABI, which the library uses in place); with
+  Decoder(device="cpu") they are host memory, as in the streamer, and every
+  call takes the library's host-pointer path;
 * the weights are one device blob laid out like a GGUF data section (tensors
   at 32-byte aligned offsets), addressed as (base, offset) exactly as the
   streamer addresses its mapped file;
 * the residual loops (`hidden[i] = hidden[i] + proj_out_buf[i]`,
-  lua/gncx_streamer.lua:871-873, 906-908) call gncx_hip_vec_add;
+  lua/gncx_streamer.lua:871-873, 906-908) call gncx_hip_vec_add on device
+  buffers and run on the host for host buffers;
 * the sampler is a greedy device argmax (the streamer's sampler adds a
   repetition penalty on the host, lua/gncx_streamer.lua:1229-1272);
 * `fused=True` uses the library's launch-saving extensions, with the same
@@ -228,7 +231,12 @@ def load_model_gguf(path) -> Model:
 
 
 class Decoder:
-    """Device-resident state of one sequence and the streamer's call sequence."""
+    """State of one sequence and the streamer's call sequence.  device="cuda"
+    keeps every buffer in device memory (the library uses them in place);
+    device="cpu" keeps them in host memory as the streamer does (its buffers
+    and KV caches are host RAM), so every call goes through the library's
+    host-pointer path: inputs staged, outputs written back before return, KV
+    caches mirrored by device twins, residual adds on the host."""
 
     def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda"):
         s = model.shape
@@ -250,6 +258,14 @@ class Decoder:
         self.max_seq = max_seq
         self.scale = 1.0 / (s.head_dim ** 0.5)
         self._qkv = self._gu = None  # gncx_hip_matvec_multi arguments, built on first fused use
+
+    def _add(self, dst, src):
+        """hidden += delta: the streamer's host loop (lua/gncx_streamer.lua:871-873,
+        906-908) for host buffers, gncx_hip_vec_add for device ones."""
+        if dst.is_cuda:
+            self.lib.gncx_hip_vec_add(dst.data_ptr(), src.data_ptr(), dst.numel())
+        else:
+            dst += src
 
     def _fused_tables(self):
         """ctypes argument arrays of gncx_hip_matvec_multi, per layer."""
@@ -325,13 +341,13 @@ class Decoder:
             self._matvec(f"{p}.attn_v.weight", nrm, s.embed, s.kv_dim, v)
             self._attention(l, q, k, v, pos, a)
             self._matvec(f"{p}.attn_output.weight", a, s.q_dim, s.embed, pr)
-            L.gncx_hip_vec_add(h, pr, s.embed)
+            self._add(self.hidden, self.proj)
             self._norm(f"{p}.ffn_norm.weight", h, nrm)
             self._matvec(f"{p}.ffn_gate.weight", nrm, s.embed, s.ffn, ga)
             self._matvec(f"{p}.ffn_up.weight", nrm, s.embed, s.ffn, up)
             L.gncx_swiglu_activation(ga, up, s.ffn, ac)
             self._matvec(f"{p}.ffn_down.weight", ac, s.ffn, s.embed, pr)
-            L.gncx_hip_vec_add(h, pr, s.embed)
+            self._add(self.hidden, self.proj)
         return self._lm_head()
 
     def _forward_fused(self, pos: int):
@@ -394,14 +410,14 @@ class Decoder:
             for i in range(B):
                 self._attention(l, rowp(bq, i), rowp(bk, i), rowp(bv, i), i, rowp(ba, i))
             self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
-            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            self._add(bh, bp)
             for i in range(B):
                 self._norm(f"{p}.ffn_norm.weight", rowp(bh, i), rowp(bn, i))
             self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
             self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
             L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
             self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
-            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            self._add(bh, bp)
         self.hidden.copy_(bh[B - 1])
         return self._lm_head()
 
@@ -422,14 +438,14 @@ class Decoder:
                                          m.base, m.off(f"{p}.attn_q_norm.weight"), m.off(f"{p}.attn_k_norm.weight"),
                                          1, s.eps, 0, 0, s.rope_base, ba.data_ptr())
             self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
-            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            self._add(bh, bp)
             L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"), s.embed, s.eps,
                                     bn.data_ptr())
             self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
             self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
             L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
             self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
-            L.gncx_hip_vec_add(bh.data_ptr(), bp.data_ptr(), B * s.embed)
+            self._add(bh, bp)
         self.hidden.copy_(bh[B - 1])
         return self._lm_head()
 

@@ -151,3 +151,34 @@ def test_decode_from_gguf_file_host_pointers(lib, oracle, torch_mod, tmp_path):
         assert lib.gncx_hip_weight_bytes() > 0
     finally:
         lib.gncx_hip_weight_forget(None)  # the mapping goes away with the test
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_host_buffers_match_device_buffers(lib, torch_mod, tmp_path, fused):
+    """The unchanged streamer's contract end to end: weights from a mapped GGUF
+    file, and every activation buffer and KV cache in host memory (inputs
+    staged, outputs written back before each call returns, caches mirrored on
+    the device, residual adds on the host).  Prefill and decode logits equal
+    those of device-resident buffers bit for bit."""
+    import gncx_amd.decode as dec
+    dec.write_model_gguf(tmp_path / "m.gguf", small_shape(), seed=33)
+    m = dec.load_model_gguf(tmp_path / "m.gguf")
+    dh = dec.Decoder(lib, torch_mod, m, max_seq=32, fused=fused, device="cpu")
+    dd = dec.Decoder(lib, torch_mod, m, max_seq=32, fused=fused, device="cuda")
+    try:
+        prompt = [7, 8, 9, 300, 599, 1]
+        a = dh.prefill(prompt).numpy().copy()
+        gncx.check(lib)
+        b = dd.prefill(prompt).cpu().numpy()
+        assert np.array_equal(a, b)
+        tok = int(np.argmax(a))
+        for pos in range(len(prompt), len(prompt) + 3):
+            a = dh.forward_token(tok, pos).numpy().copy()
+            gncx.check(lib)
+            b = dd.forward_token(tok, pos).cpu().numpy()
+            assert np.array_equal(a, b), pos
+            tok = int(np.argmax(a))
+        assert np.array_equal(dh.kc[1].numpy()[:pos + 1], dd.kc[1].cpu().numpy()[:pos + 1])
+    finally:
+        lib.gncx_hip_weight_forget(None)
+        lib.gncx_hip_kv_forget(None)
