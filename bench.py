@@ -215,7 +215,7 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     pkg.check(lib)
     del d2
     torch.cuda.empty_cache()
-    d = dec.Decoder(lib, torch, model, max_seq=prompt_len + 2 * n_tokens + 1)
+    d = dec.Decoder(lib, torch, model, max_seq=prompt_len + 4 * n_tokens + 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     logits = d.prefill(prompt)
@@ -226,16 +226,24 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     res = {}
     pos = prompt_len
     tok = d.greedy(logits)
-    for fused in (False, True):
-        d.fused = fused
+    for mode in ("streamer", "fused", "native"):
+        d.fused, d.native = mode != "streamer", mode == "native"
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(n_tokens):
             tok = d.greedy(d.forward_token(tok, pos))
             pos += 1
         torch.cuda.synchronize()
-        res[fused] = (time.perf_counter() - t0) / n_tokens
+        res[mode] = (time.perf_counter() - t0) / n_tokens
         pkg.check(lib)
+    # the native step feeding its own device argmax back: no host round trip per token
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = d.decode_greedy(tok, pos, n_tokens)
+    res["native_greedy"] = (time.perf_counter() - t0) / n_tokens
+    pkg.check(lib)
+    pos += n_tokens
+    assert len(toks) == n_tokens and all(0 <= t < s.vocab for t in toks)
     # the unchanged streamer's contract: every buffer and KV cache in host
     # memory, so each call stages its inputs and writes its outputs back
     # before returning (short prompt: its per-token prefill alone syncs
@@ -256,9 +264,16 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     kv_bytes = 2 * s.n_layers * s.kv_dim * 4 * (prompt_len + n_tokens)  # K and V rows read at the mid position
     del model
     torch.cuda.empty_cache()
-    return {"decode_tok_s": round(1.0 / res[False], 1), "decode_ms_per_token": round(res[False] * 1e3, 3),
-            "decode_tok_s_fused": round(1.0 / res[True], 1), "decode_ms_per_token_fused": round(res[True] * 1e3, 3),
-            "hbm_gbps_effective": round((weight_bytes + kv_bytes) / res[False] / 1e9, 1),
+    best = res["native_greedy"]
+    return {"decode_tok_s": round(1.0 / res["streamer"], 1), "decode_ms_per_token": round(res["streamer"] * 1e3, 3),
+            "decode_tok_s_fused": round(1.0 / res["fused"], 1),
+            "decode_ms_per_token_fused": round(res["fused"] * 1e3, 3),
+            "decode_tok_s_native": round(1.0 / res["native"], 1),
+            "decode_ms_per_token_native": round(res["native"] * 1e3, 3),
+            "decode_tok_s_native_device_greedy": round(1.0 / best, 1),
+            "decode_ms_per_token_native_device_greedy": round(best * 1e3, 3),
+            "hbm_gbps_effective_native_device_greedy": round((weight_bytes + kv_bytes) / best / 1e9, 1),
+            "hbm_gbps_effective": round((weight_bytes + kv_bytes) / res["streamer"] / 1e9, 1),
             "prefill_tokens": prompt_len, "prefill_s": round(prefill_s, 3),
             "prefill_tok_s": round(prompt_len / prefill_s, 1),
             "prefill_s_fused": round(prefill_fused_s, 3), "prefill_tok_s_fused": round(prompt_len / prefill_fused_s, 1),
@@ -269,7 +284,11 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
             "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
                      "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",
-            "positions": f"{prompt_len}..{pos - 1}"}
+            "positions": f"{prompt_len}..{pos - 1}",
+            "modes": "decode_tok_s: the streamer's call sequence issued from Python; _fused: the launch-saving "
+                     "extensions from Python; _native: gncx_hip_decode_step (the library issues the token, "
+                     "add+RMSNorm and SwiGLU fused into the matvecs), host argmax per token; "
+                     "_native_device_greedy: the same steps feeding their own device argmax back"}
 
 
 def cpu_baseline(pkg, t, k, n, w_host, x_host, seconds=10.0):

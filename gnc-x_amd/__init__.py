@@ -102,7 +102,36 @@ SIGNATURES = {
         [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp, _sz, _sz, _i32, _f32, _sz, _i32,
          _f32, _fp],
     ),
+    "gncx_hip_matvec_multi_addnorm": (None, [_fp, _fp, _vp, _sz, _f32, _fp, _i32, _vp, _vp, _i32, _i32, _vp]),
+    "gncx_hip_matvec_swiglu": (None, [_vp, _vp, _i32, _fp, _i32, _i32, _fp]),
+    "gncx_hip_decode_step": (C.c_int, [_vp, _vp, _i32, _i32, _i32]),
+    "gncx_hip_argmax": (None, [_fp, _i32, _vp]),
 }
+
+
+# ctypes mirrors of the native decode step's structs (include/gncx_llm_core.h)
+class DecodeTensor(C.Structure):
+    _fields_ = [("offset", C.c_size_t), ("ggml_type", C.c_int32)]
+
+
+class DecodeLayer(C.Structure):
+    _fields_ = [(n, DecodeTensor) for n in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_q_norm", "attn_k_norm",
+                                            "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")]
+
+
+class DecodeModel(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("layers", C.POINTER(DecodeLayer)), ("token_embd", DecodeTensor),
+                ("output_norm", DecodeTensor)] + \
+               [(n, C.c_int32) for n in ("n_layers", "embed", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab",
+                                         "qk_norm")] + \
+               [("eps", C.c_float), ("rope_base", C.c_float), ("attn_scale", C.c_float)]
+
+
+class DecodeState(C.Structure):
+    _fields_ = [("hidden", C.c_void_p * 2)] + \
+               [(n, C.c_void_p) for n in ("q", "k", "v", "attn", "proj", "normed", "gate", "up", "act", "logits")] + \
+               [("k_cache", C.POINTER(C.c_void_p)), ("v_cache", C.POINTER(C.c_void_p)), ("max_seq", C.c_int32),
+                ("token", C.c_void_p), ("token_log", C.c_void_p)]
 
 
 class GncxLibraryMissing(RuntimeError):

@@ -235,6 +235,103 @@ __global__ void fetch_embedding_kernel(int32_t type, const uint8_t* __restrict r
         out[e] = decode_elem(type, row, e, scale);
 }
 
+// The row of a token read from device memory (a decode loop that feeds its
+// own argmax back without a host round trip).  Rows of tokens outside
+// [0, vocab) are not read: the output is left as it is.
+__global__ void fetch_embedding_dev_kernel(int32_t type, const uint8_t* __restrict table, const int32_t* token,
+                                           int32_t vocab, size_t rbytes, int32_t dim, float scale,
+                                           float* __restrict out) {
+    const int32_t t = *token;
+    if (t < 0 || t >= vocab) return;
+    const uint8_t* row = table + static_cast<size_t>(t) * rbytes;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < dim; e += gridDim.x * blockDim.x)
+        out[e] = decode_elem(type, row, e, scale);
+}
+
+// Index of the largest value (the first one among equal maxima; NaN never
+// wins), as torch.argmax and the greedy pick of the streamer's sampler take
+// it.  Two launches: argmax_part_kernel reduces contiguous chunks of
+// kArgmaxChunk values (coalesced float4 loads, several in flight per thread)
+// to (value, index) pairs, argmax_final_kernel reduces the pairs.
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxChunk = 4096;
+constexpr int kArgmaxMaxParts = 1024;
+
+struct ArgBest {
+    float v;
+    int32_t i;  // INT32_MAX: no candidate
+};
+__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
+    // b replaces a when it is larger, or equal with a smaller index; NaN never wins
+    const bool take = b.i != INT32_MAX && (a.i == INT32_MAX || b.v > a.v || (b.v == a.v && b.i < a.i));
+    return take ? b : a;
+}
+__device__ ArgBest block_argmax(ArgBest b) {
+    __shared__ float sv[kArgmaxThreads];
+    __shared__ int32_t si[kArgmaxThreads];
+    sv[threadIdx.x] = b.v;
+    si[threadIdx.x] = b.i;
+    __syncthreads();
+    for (int h = kArgmaxThreads / 2; h > 0; h >>= 1) {
+        if (static_cast<int>(threadIdx.x) < h) {
+            const ArgBest r = arg_better({sv[threadIdx.x], si[threadIdx.x]}, {sv[threadIdx.x + h], si[threadIdx.x + h]});
+            sv[threadIdx.x] = r.v;
+            si[threadIdx.x] = r.i;
+        }
+        __syncthreads();
+    }
+    return {sv[0], si[0]};
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float* __restrict x, int32_t n,
+                                                                     float* __restrict pv, int32_t* __restrict pi) {
+    const int32_t base = blockIdx.x * kArgmaxChunk;
+    const int32_t end = min(n, base + kArgmaxChunk);
+    ArgBest b{-INFINITY, INT32_MAX};
+    // 4 values per thread per step, 4 steps: the whole chunk in flight at once
+    float vals[kArgmaxChunk / kArgmaxThreads];
+#pragma unroll
+    for (int s = 0; s < kArgmaxChunk / (4 * kArgmaxThreads); ++s) {
+        const int32_t i = base + 4 * (s * kArgmaxThreads + static_cast<int32_t>(threadIdx.x));
+        if (i + 3 < end && (n & 3) == 0) {
+            const float4 v = *reinterpret_cast<const float4*>(x + i);
+            vals[4 * s] = v.x;
+            vals[4 * s + 1] = v.y;
+            vals[4 * s + 2] = v.z;
+            vals[4 * s + 3] = v.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vals[4 * s + c] = i + c < end ? x[i + c] : NAN;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < kArgmaxChunk / (4 * kArgmaxThreads); ++s)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int32_t i = base + 4 * (s * kArgmaxThreads + static_cast<int32_t>(threadIdx.x)) + c;
+            const float v = vals[4 * s + c];
+            if (v == v) b = arg_better(b, {v, i});
+        }
+    b = block_argmax(b);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = b.v;
+        pi[blockIdx.x] = b.i;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(const float* __restrict pv,
+                                                                      const int32_t* __restrict pi, int32_t parts,
+                                                                      int32_t* __restrict out, int32_t* __restrict log) {
+    ArgBest b{-INFINITY, INT32_MAX};
+    for (int32_t p = threadIdx.x; p < parts; p += kArgmaxThreads) b = arg_better(b, {pv[p], pi[p]});
+    b = block_argmax(b);
+    if (threadIdx.x == 0) {
+        const int32_t r = b.i == INT32_MAX ? 0 : b.i;
+        *out = r;
+        if (log) *log = r;
+    }
+}
+
 int grid_for(size_t n, int threads) {
     size_t g = (n + threads - 1) / threads;
     if (g > 4096) g = 4096;
@@ -322,6 +419,31 @@ hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t to
     const uint8_t* row = table + static_cast<size_t>(token) * row_bytes(type, dim);
     hipLaunchKernelGGL(fetch_embedding_kernel, dim3(grid_for(dim, 256)), dim3(256), 0, stream, type, row, dim,
                        scale, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fetch_embedding_dev(int32_t type, const uint8_t* table, const int32_t* token, int32_t vocab,
+                                      int32_t dim, float scale, float* out, hipStream_t stream) {
+    if (dim <= 0 || vocab <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fetch_embedding_dev_kernel, dim3(grid_for(dim, 256)), dim3(256), 0, stream, type, table, token,
+                       vocab, row_bytes(type, dim), dim, scale, out);
+    return hipGetLastError();
+}
+
+size_t argmax_workspace_bytes(int32_t n) {
+    const size_t parts = n > 0 ? (static_cast<size_t>(n) + kArgmaxChunk - 1) / kArgmaxChunk : 0;
+    return parts * (sizeof(float) + sizeof(int32_t));
+}
+
+hipError_t launch_argmax(const float* x, int32_t n, int32_t* out, int32_t* log, void* workspace, size_t ws_bytes,
+                         hipStream_t stream) {
+    if (n <= 0 || (reinterpret_cast<uintptr_t>(x) & 15u) != 0) return hipErrorInvalidValue;
+    const int32_t parts = (n + kArgmaxChunk - 1) / kArgmaxChunk;
+    if (parts > kArgmaxMaxParts || ws_bytes < argmax_workspace_bytes(n)) return hipErrorInvalidValue;
+    float* pv = static_cast<float*>(workspace);
+    int32_t* pi = reinterpret_cast<int32_t*>(pv + parts);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(parts), dim3(kArgmaxThreads), 0, stream, x, n, pv, pi);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, stream, pv, pi, parts, out, log);
     return hipGetLastError();
 }
 

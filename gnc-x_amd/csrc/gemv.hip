@@ -157,8 +157,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 //   rows in flight.  Loads are plain global loads: rows past the end and lanes
 //   without a slot re-read valid bytes (local row 0, slot 0) whose results
 //   are unused, so no load sits behind a branch and each waitcnt counts
-//   exactly the loads issued after the one it needs.  y is written from LDS
-//   once all rows are done.
+//   exactly the loads issued after the one it needs.  With one K-slice per
+//   row each wave keeps its results in registers and stores them once it has
+//   no loads left (0.1-0.3 us faster than writing y from LDS after a barrier);
+//   K-split rows meet in LDS and y is written once all rows are done.
 //
 //   TWO (K-split rows, or 8 waves per CU): each wave keeps two rows in flight
 //   in two register buffers used in turn; the first nqw waves quantise x
@@ -194,8 +196,10 @@ constexpr int kBandThreadsStream = GNCX_BAND_THREADS_STREAM;
 constexpr size_t kBandStreamBytes = static_cast<size_t>(GNCX_BAND_STREAM_KB) * 1024;
 constexpr int32_t kBandGroups = GNCX_BAND_GROUPS;  // one work-group per CU of an MI355X
 constexpr size_t kBandLds = 64 * 1024;
-constexpr size_t kBandCtl = 128;    // LDS head: per-K-slice row counters and the quantised count
+constexpr size_t kBandCtl = 256;    // LDS head: per-K-slice row counters, the quantised count, norm partials
 constexpr int kCtlQuantised = 31;   // index of the count of waves done quantising
+constexpr int kCtlNormPart = 32;    // [16] per-wave sums of squares of the add+RMSNorm prologue
+constexpr int kCtlNormCount = 48;   // count of waves that stored their sum of squares
 constexpr int kOneMinRowWaves = 8;  // ONE schedule from this many row-waves (16-wave groups only)
 
 enum BandSched { kSchedOne = 1, kSchedTwo = 2 };
@@ -250,10 +254,35 @@ struct BandMats {
     }
 };
 
-template <int TYPE, int THREADS, int SCHED, bool MULTI>
+// Fused prologue / epilogue of the decode chain (ONE schedule, 1024 threads,
+// one K-slice per row, k <= 4096):
+//   kExtNorm    x = RMSNorm(h + r) * gamma, formed by every work-group from h,
+//               r and gamma with the arithmetic of rmsnorm_kernel<true> (the
+//               same per-thread float4, wave sums and ordered sum of the 16
+//               wave partials), so the quantised x is the one the separate
+//               add+RMSNorm kernel feeds a plain matvec; work-group 0 stores
+//               h + r to h_out (h_out != h: other work-groups still read h);
+//   kExtSwiglu  two matrices of N rows each (gate, up) with N a multiple of the
+//               grid: work-group g holds gate row i and up row i in its LDS
+//               results and writes act[i] = SiLU(gate[i]) * up[i] with the
+//               arithmetic of swiglu_kernel; gate and up are not stored.
+enum BandExt { kExtNone = 0, kExtNorm = 1, kExtSwiglu = 2 };
+struct BandExtra {
+    const float* h;
+    const float* r;  // may be null: x = RMSNorm(h) * gamma
+    const float* gamma;
+    float* h_out;    // may be null
+    float* act;
+    float eps;
+};
+
+template <int TYPE, int THREADS, int SCHED, bool MULTI, int EXT = kExtNone>
 __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint32_t rbytes,
                                                                  const float* __restrict x, int32_t k,
-                                                                 int32_t n, int32_t nwk, int32_t nwr, int32_t nqw) {
+                                                                 int32_t n, int32_t nwk, int32_t nwr, int32_t nqw,
+                                                                 BandExtra ex) {
+    static_assert(EXT == kExtNone || (SCHED == kSchedOne && THREADS == 1024 && TYPE != kBF16),
+                  "fused prologue / epilogue: ONE schedule, 1024 threads, quantised weights");
     using S = Slot<TYPE>;
     using Frag = typename S::Frag;
     using Act = typename S::Act;
@@ -281,8 +310,19 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
     // local row li of this work-group is global row li * groups + blockIdx.x
     const int32_t rows_here = (n - static_cast<int32_t>(blockIdx.x) + groups - 1) / groups;
     auto grow = [&](int32_t li) { return static_cast<size_t>(li) * groups + blockIdx.x; };
-    // y straight from the wave only for whole rows under TWO
+    // whole rows (one K-slice): under TWO the wave stores y itself after each
+    // row; under ONE it keeps its results in registers (lane i: its i-th row)
+    // and stores them with one instruction once it has no loads left, since a
+    // store issued between loads holds up the vmcnt wait of every later load
     const bool direct = SCHED == kSchedTwo && nwk == 1;
+    const bool wstore = SCHED == kSchedOne && nwk == 1 && !(EXT & kExtSwiglu);
+    int32_t nres = 0;
+    float res = 0.0f;
+    int32_t res_row = 0;
+    auto flush = [&]() {
+        if (lane < nres) *mats.template out<MULTI>(grow(res_row)) = res;
+        nres = 0;
+    };
 
     if (threadIdx.x < kBandCtl / sizeof(int32_t)) ctl[threadIdx.x] = 0;
     __syncthreads();
@@ -302,6 +342,14 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
     auto reduce = [&](const Frag& f, const Act& a, int32_t li) {
         float v = has_slot ? S::dot(f, a, s) : 0.0f;
         v = wave_sum_lane63(v);
+        if (wstore) {
+            const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+            const bool mine = lane == nres;
+            res = mine ? sv : res;
+            res_row = mine ? li : res_row;
+            if (++nres == 64) flush();
+            return;
+        }
         if (lane == 63) {
             if (direct) *mats.template out<MULTI>(grow(li)) = v;
             else part[li * nwk + kw] = v;
@@ -334,7 +382,39 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
             issue(fa, ja);
             issue(fb, jb);
         };
-        if (qwave) {
+        float4 hsum = make_float4(0.f, 0.f, 0.f, 0.f);  // h + r of this thread (kExtNorm)
+        const int32_t n4 = k / 4;
+        const int32_t t4 = static_cast<int32_t>(threadIdx.x) < n4 ? static_cast<int32_t>(threadIdx.x) : n4 - 1;
+        if constexpr ((EXT & kExtNorm) != 0) {
+#pragma clang fp contract(off)
+            // h, r and gamma first, so their waitcnt does not wait for the rows
+            const float4 hv = reinterpret_cast<const float4*>(ex.h)[t4];
+            const float4 rv = ex.r ? reinterpret_cast<const float4*>(ex.r)[t4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 gv = reinterpret_cast<const float4*>(ex.gamma)[t4];
+            start();
+            hsum = ex.r ? make_float4(hv.x + rv.x, hv.y + rv.y, hv.z + rv.z, hv.w + rv.w) : hv;
+            const bool mine = static_cast<int32_t>(threadIdx.x) < n4;
+            float ss = mine ? hsum.x * hsum.x + hsum.y * hsum.y + hsum.z * hsum.z + hsum.w * hsum.w : 0.0f;
+            ss = wave_sum(ss);
+            float* npart = reinterpret_cast<float*>(ctl + kCtlNormPart);
+            if (lane == 0) npart[wv] = ss;
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlNormCount], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            while (__hip_atomic_load(&ctl[kCtlNormCount], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < THREADS / 64)
+                __builtin_amdgcn_s_sleep(1);
+            asm volatile("" ::: "memory");
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < THREADS / 64; ++w) tot += npart[w];
+            const float inv = 1.0f / sqrtf(tot / static_cast<float>(k) + ex.eps);
+            const float4 xn = make_float4(hsum.x * inv * gv.x, hsum.y * inv * gv.y, hsum.z * inv * gv.z,
+                                          hsum.w * inv * gv.w);
+            if (mine) quantize_task(xn, threadIdx.x >> 3, threadIdx.x & 7, q, meta);
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            asm volatile("" ::: "memory");
+            if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else if (qwave) {
             float4 xv[kU];
             quant_load<kU>(xv, x, k / 32, threadIdx.x, nqw * 64);
             start();
@@ -351,6 +431,10 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
                 issue(fa, li);
                 reduce(fa, a, li);
             }
+        }
+        if constexpr ((EXT & kExtNorm) != 0) {
+            if (blockIdx.x == 0 && ex.h_out && static_cast<int32_t>(threadIdx.x) < n4)
+                reinterpret_cast<float4*>(ex.h_out)[threadIdx.x] = hsum;
         }
     } else {
         if (qwave) {
@@ -380,7 +464,20 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
         }
     }
     if (direct) return;
+    if (wstore) {
+        flush();
+        return;
+    }
     __syncthreads();
+    if constexpr ((EXT & kExtSwiglu) != 0) {
+#pragma clang fp contract(off)
+        const int32_t half = rows_here / 2;  // local row li + half is up row li
+        for (int32_t li = threadIdx.x; li < half; li += THREADS) {
+            const float g = part[li], u = part[li + half];
+            ex.act[grow(li)] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        }
+        return;
+    }
     for (int32_t li = threadIdx.x; li < rows_here; li += THREADS) {
         float acc = 0.0f;
         for (int j = 0; j < nwk; ++j) acc += part[li * nwk + j];
@@ -457,11 +554,50 @@ bool try_band_sched(const BandMats& m, const float* x, int32_t k, int32_t n, hip
     const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE, k));
     if (m.count > 1)
         hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED, true>), dim3(groups), dim3(THREADS), lds, stream, m,
-                           rb, x, k, n, nwk, nwr, nqw);
+                           rb, x, k, n, nwk, nwr, nqw, BandExtra{});
     else
         hipLaunchKernelGGL((gemv_band_kernel<TYPE, THREADS, SCHED, false>), dim3(groups), dim3(THREADS), lds, stream,
-                           m, rb, x, k, n, nwk, nwr, nqw);
+                           m, rb, x, k, n, nwk, nwr, nqw, BandExtra{});
     return true;
+}
+
+// The fused forms (BandExt): ONE schedule with 16 waves and whole rows only;
+// false when the shape does not fit (the caller runs the separate kernels).
+template <int TYPE, int EXT>
+bool try_band_ext(const BandMats& m, const float* x, int32_t k, int32_t n, const BandExtra& ex, hipStream_t stream) {
+    int32_t groups, nwk, nwr, nqw;
+    size_t lds;
+    if (!band_plan(Slot<TYPE>::slots(k), k, n, true, 16, kSchedOne, groups, nwk, nwr, nqw, lds)) return false;
+    if (nwk != 1 || nwr < kOneMinRowWaves) return false;
+    if constexpr ((EXT & kExtNorm) != 0) {
+        if (k % 4 != 0 || k > 4 * 1024) return false;
+        nqw = 16;  // every thread normalises and quantises one float4
+    }
+    if constexpr ((EXT & kExtSwiglu) != 0) {
+        if (m.count != 2 || 2 * m.end[0] != n || m.end[0] % groups != 0) return false;
+    }
+    const uint32_t rb = static_cast<uint32_t>(row_bytes(TYPE, k));
+    if (m.count > 1)
+        hipLaunchKernelGGL((gemv_band_kernel<TYPE, 1024, kSchedOne, true, EXT>), dim3(groups), dim3(1024), lds, stream,
+                           m, rb, x, k, n, nwk, nwr, nqw, ex);
+    else if constexpr ((EXT & kExtSwiglu) == 0)
+        hipLaunchKernelGGL((gemv_band_kernel<TYPE, 1024, kSchedOne, false, EXT>), dim3(groups), dim3(1024), lds,
+                           stream, m, rb, x, k, n, nwk, nwr, nqw, ex);
+    else
+        return false;
+    return true;
+}
+
+template <int EXT>
+bool try_band_ext_type(int32_t type, const BandMats& m, const float* x, int32_t k, int32_t n, const BandExtra& ex,
+                       hipStream_t stream) {
+    switch (type) {
+    case kQ4_0: return try_band_ext<kQ4_0, EXT>(m, x, k, n, ex, stream);
+    case kQ8_0: return try_band_ext<kQ8_0, EXT>(m, x, k, n, ex, stream);
+    case kQ4_K: return try_band_ext<kQ4_K, EXT>(m, x, k, n, ex, stream);
+    case kQ6_K: return try_band_ext<kQ6_K, EXT>(m, x, k, n, ex, stream);
+    default: return false;
+    }
 }
 
 // ONE for 16-wave groups with at least kOneMinRowWaves row-waves, TWO otherwise
@@ -563,6 +699,40 @@ hipError_t launch_gemv_multi(int32_t type, int32_t count, const uint8_t* const* 
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_gemv_fused(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns, int32_t k,
+                             float* const* ys, const GemvFusion& f, hipStream_t stream) {
+    const bool norm = f.gamma != nullptr, glu = f.act != nullptr;
+    if (count <= 0 || count > kMaxGemvMats || (!norm && !glu)) return hipErrorInvalidValue;
+    if (norm && (!f.h || f.h == f.h_out)) return hipErrorInvalidValue;
+    if (!norm && !f.x) return hipErrorInvalidValue;
+    const float* xin = norm ? f.h : f.x;  // alignment and shape checks
+    const uintptr_t al = reinterpret_cast<uintptr_t>(f.h) | reinterpret_cast<uintptr_t>(f.r) |
+                         reinterpret_cast<uintptr_t>(f.gamma) | reinterpret_cast<uintptr_t>(f.h_out);
+    if (norm && (al & 15u) != 0) return hipErrorInvalidValue;
+    BandMats m{};
+    int64_t total = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (ns[i] <= 0) return hipErrorInvalidValue;
+        hipError_t e = check_gemv(type, ws[i], xin, k);
+        if (e != hipSuccess) return e;
+        total += ns[i];
+        m.w[i] = ws[i];
+        m.y[i] = ys ? ys[i] : nullptr;
+        m.end[i] = static_cast<int32_t>(total);
+    }
+    if (total > INT32_MAX) return hipErrorInvalidValue;
+    if (glu && (count != 2 || ns[0] != ns[1])) return hipErrorInvalidValue;
+    if (!glu && !ys) return hipErrorInvalidValue;
+    m.count = count;
+    const BandExtra ex{f.h, f.r, f.gamma, f.h_out, f.act, f.eps};
+    const int32_t n = static_cast<int32_t>(total);
+    bool ok;
+    if (norm && glu) ok = try_band_ext_type<kExtNorm | kExtSwiglu>(type, m, nullptr, k, n, ex, stream);
+    else if (norm) ok = try_band_ext_type<kExtNorm>(type, m, nullptr, k, n, ex, stream);
+    else ok = try_band_ext_type<kExtSwiglu>(type, m, f.x, k, n, ex, stream);
+    return ok ? hipGetLastError() : hipErrorNotSupported;
 }
 
 hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, ActMeta* meta,

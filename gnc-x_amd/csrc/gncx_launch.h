@@ -28,6 +28,27 @@ constexpr int32_t kMaxGemvMats = 4;
 hipError_t launch_gemv_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
                              const float* x, int32_t k, float* const* ys, hipStream_t stream);
 
+// A matvec(_multi) with the decode chain's neighbours fused in (ONE schedule
+// shapes: 16 waves, whole rows, k <= 4096 for the prologue):
+//   gamma != null  x = RMSNorm(h + r) * gamma (r may be null) is formed in
+//                  every work-group, bit-identical with launch_add_rmsnorm;
+//                  h + r is stored to h_out when given (h_out != h);
+//   gamma == null  x is the input vector, as for launch_gemv_multi;
+//   act != null    two matrices (gate, up) of equal rows: act = SiLU(gate.x) *
+//                  (up.x), bit-identical with launch_swiglu; ys may be null.
+// Returns hipErrorNotSupported when the shape does not fit (nothing launched).
+struct GemvFusion {
+    const float* x = nullptr;
+    const float* h = nullptr;
+    const float* r = nullptr;
+    const float* gamma = nullptr;
+    float eps = 0.0f;
+    float* h_out = nullptr;
+    float* act = nullptr;
+};
+hipError_t launch_gemv_fused(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns, int32_t k,
+                             float* const* ys, const GemvFusion& f, hipStream_t stream);
+
 // Per-32 Q8 quantisation of `rows` rows of k floats into q[rows*k] and
 // meta[rows*k/32] (used by matbatch and the dequant tests).
 hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, ActMeta* meta,
@@ -123,5 +144,14 @@ hipError_t launch_softcap(float* y, int32_t n, float softcap, hipStream_t stream
 // One embedding row (reference cpp:693-780), scale folded like the reference.
 hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim,
                                   float scale, float* out, hipStream_t stream);
+// The same with the token read from device memory (tokens outside [0, vocab)
+// leave out untouched).
+hipError_t launch_fetch_embedding_dev(int32_t type, const uint8_t* table, const int32_t* token, int32_t vocab,
+                                      int32_t dim, float scale, float* out, hipStream_t stream);
+// *out = index of the first largest of x[0..n) (NaN never wins); also *log when
+// given.  x 16-byte aligned, n up to 4M; workspace of argmax_workspace_bytes(n).
+size_t argmax_workspace_bytes(int32_t n);
+hipError_t launch_argmax(const float* x, int32_t n, int32_t* out, int32_t* log, void* workspace, size_t ws_bytes,
+                         hipStream_t stream);
 
 }  // namespace gncx

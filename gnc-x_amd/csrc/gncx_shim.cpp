@@ -39,24 +39,10 @@
 
 #include "gncx_formats.h"
 #include "gncx_launch.h"
+// the public declarations: every definition below must match them
+#include "../../include/gncx_llm_core.h"
 
 #define GNCX_API extern "C" __attribute__((visibility("default")))
-
-#pragma pack(push, 1)
-// cpp:267-271
-struct GNCXCompactToken {
-    uint8_t phase_2bit;
-    uint8_t diag_d;
-    uint16_t abs_delta;
-};
-// cpp:308-313
-struct GNCXTelemetryStats {
-    uint64_t total_macs_equivalent;
-    uint64_t zero_origin_cancellations;
-    uint64_t zero_weight_skips;
-    uint64_t xfold_bucket_merges;
-};
-#pragma pack(pop)
 
 namespace {
 
@@ -1324,4 +1310,416 @@ GNCX_API void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t
     if (!o) return;
     if (!check(launch_rmsnorm(x, g, rows, dim, eps, o, g_rt.stream), where)) return;
     finish_out(out, o, n, host, where);
+}
+
+// ---- fused decode-chain matvecs ------------------------------------------
+// Device pointers only (these are for callers whose hidden state lives in
+// HBM); weights may be host (uploaded once) or device memory.
+
+namespace {
+bool all_device(std::initializer_list<const void*> ps) {
+    for (const void* p : ps)
+        if (p && !is_device_ptr(p)) return false;
+    return true;
+}
+}  // namespace
+
+GNCX_API void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* delta, const uint8_t* mmap_base,
+                                            size_t norm_weight_offset, float eps, float* hidden_out, int32_t count,
+                                            const uint8_t* const* weights, const int32_t* out_dims,
+                                            int32_t ggml_type, int32_t in_dim, float* const* out_vecs) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_matvec_multi_addnorm";
+    g_norm_epoch++;
+    if (count <= 0 || count > kMaxGemvMats || !weights || !out_dims || !out_vecs || !hidden || in_dim <= 0 ||
+        hidden_out == hidden) {
+        set_error(where, "count 1..4 with weights, out_dims and outputs; hidden_out must differ from hidden", -1);
+        return;
+    }
+    if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    if (!all_device({hidden, delta, hidden_out})) {
+        set_error(where, "hidden, delta and hidden_out must be device memory", -1);
+        return;
+    }
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(in_dim), where));
+    if (!g) return;
+    const uint8_t* ws[kMaxGemvMats];
+    for (int32_t i = 0; i < count; ++i) {
+        if (out_dims[i] <= 0 || !weights[i] || !out_vecs[i] || !is_device_ptr(out_vecs[i])) {
+            set_error(where, "every matrix needs weights, out_dims > 0 and a device output", -1);
+            return;
+        }
+        ws[i] = device_weights(weights[i], row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dims[i]), where);
+        if (!ws[i]) return;
+    }
+    GemvFusion f;
+    f.h = hidden;
+    f.r = delta;
+    f.gamma = g;
+    f.eps = eps;
+    f.h_out = hidden_out;
+    hipError_t e = launch_gemv_fused(ggml_type, count, ws, out_dims, in_dim, out_vecs, f, g_rt.stream);
+    if (e != hipErrorNotSupported) {
+        check(e, where);
+        return;
+    }
+    // the separate kernels, same results: h_out = h + delta, normed into the staging buffer
+    if (!g_rt.x.ensure(sizeof(float) * static_cast<size_t>(in_dim), where)) return;
+    float* xn = g_rt.x.as<float>();
+    if (delta) {
+        if (!hidden_out) {
+            set_error(where, "this shape needs hidden_out for the separate add+RMSNorm", -1);
+            return;
+        }
+        if (!check(hipMemcpyAsync(hidden_out, hidden, sizeof(float) * in_dim, hipMemcpyDeviceToDevice, g_rt.stream),
+                   where) ||
+            !check(launch_add_rmsnorm(hidden_out, delta, g, in_dim, eps, xn, g_rt.stream), where))
+            return;
+    } else {
+        if (!check(launch_rmsnorm(hidden, g, 1, in_dim, eps, xn, g_rt.stream), where)) return;
+        if (hidden_out && !check(hipMemcpyAsync(hidden_out, hidden, sizeof(float) * in_dim, hipMemcpyDeviceToDevice,
+                                                g_rt.stream),
+                                 where))
+            return;
+    }
+    check(launch_gemv_multi(ggml_type, count, ws, out_dims, xn, in_dim, out_vecs, g_rt.stream), where);
+}
+
+GNCX_API void gncx_hip_matvec_swiglu(const uint8_t* gate_weights, const uint8_t* up_weights, int32_t ggml_type,
+                                     const float* in_vec, int32_t in_dim, int32_t ffn_dim, float* out_act) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_matvec_swiglu";
+    if (!gate_weights || !up_weights || !in_vec || !out_act || in_dim <= 0 || ffn_dim <= 0) {
+        set_error(where, "weights, in_vec, out_act and positive dims are required", -1);
+        return;
+    }
+    if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    if (!all_device({in_vec, out_act})) {
+        set_error(where, "in_vec and out_act must be device memory", -1);
+        return;
+    }
+    const size_t wb = row_bytes(ggml_type, in_dim) * static_cast<size_t>(ffn_dim);
+    const uint8_t* ws[2] = {device_weights(gate_weights, wb, where), nullptr};
+    if (!ws[0]) return;
+    ws[1] = device_weights(up_weights, wb, where);
+    if (!ws[1]) return;
+    const int32_t ns[2] = {ffn_dim, ffn_dim};
+    GemvFusion f;
+    f.x = in_vec;
+    f.act = out_act;
+    hipError_t e = launch_gemv_fused(ggml_type, 2, ws, ns, in_dim, nullptr, f, g_rt.stream);
+    if (e != hipErrorNotSupported) {
+        check(e, where);
+        return;
+    }
+    // the separate kernels, same results
+    if (!g_rt.y.ensure(sizeof(float) * 2 * static_cast<size_t>(ffn_dim), where)) return;
+    float* ys[2] = {g_rt.y.as<float>(), g_rt.y.as<float>() + ffn_dim};
+    check(launch_gemv_multi(ggml_type, 2, ws, ns, in_vec, in_dim, ys, g_rt.stream), where) &&
+        check(launch_swiglu(ys[0], ys[1], ffn_dim, out_act, g_rt.stream), where);
+}
+
+// ---- native decode step --------------------------------------------------
+// One token of GNCXStreamer:forward_token (lua/gncx_streamer.lua:759-965)
+// for a Qwen3/Llama-shaped model, every launch issued from here: per layer
+//   Q/K/V      one launch, x = RMSNorm(h + delta) * attn_norm in its prologue
+//              (delta: the previous layer's down projection; none at layer 0)
+//   attention  Q/K head RMSNorm + RoPE prologue, KV row store, split-K scan,
+//              merge (gncx_hip_attention_step_fused)
+//   O          matvec of the attention output
+//   gate/up    one launch, x = RMSNorm(h + O) * ffn_norm in its prologue,
+//              act = SiLU(gate) * up in its epilogue
+//   down       matvec of act
+// then the final residual add + RMSNorm and the tied lm_head.  The residual
+// stream alternates between the two hidden buffers (a prologue reads h while
+// work-group 0 writes h + delta to the other one).  Shapes the fused launches
+// do not take run the separate kernels with the same results.
+
+namespace {
+
+// device addresses of one model's tensors, resolved once per (base, table)
+struct DecodePlan {
+    const uint8_t* base = nullptr;
+    std::vector<GNCXDecodeLayer> layers;
+    GNCXDecodeTensor embd{}, onorm{};
+    int32_t dims[7] = {};
+    struct Layer {
+        const float *attn_norm, *q_norm, *k_norm, *ffn_norm;
+        const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+    };
+    std::vector<Layer> dev;
+    const uint8_t* embd_dev = nullptr;
+    const float* onorm_dev = nullptr;
+    GNCXDecodeState state{};
+    std::vector<float*> kc, vc;
+    bool state_ok = false;
+} g_plan;
+
+bool plan_model(const GNCXDecodeModel& m, const char* where) {
+    DecodePlan& p = g_plan;
+    const int32_t dims[7] = {m.n_layers, m.embed, m.n_heads, m.n_kv_heads, m.head_dim, m.ffn, m.vocab};
+    const bool same = p.base == m.base && p.dev.size() == static_cast<size_t>(m.n_layers) &&
+                      std::memcmp(p.dims, dims, sizeof(dims)) == 0 &&
+                      std::memcmp(&p.embd, &m.token_embd, sizeof(GNCXDecodeTensor)) == 0 &&
+                      std::memcmp(&p.onorm, &m.output_norm, sizeof(GNCXDecodeTensor)) == 0 &&
+                      std::memcmp(p.layers.data(), m.layers, sizeof(GNCXDecodeLayer) * m.n_layers) == 0;
+    if (same) return true;
+    p.base = nullptr;
+    p.dev.clear();
+    const size_t E = m.embed, Q = static_cast<size_t>(m.n_heads) * m.head_dim,
+                 KV = static_cast<size_t>(m.n_kv_heads) * m.head_dim, F = m.ffn, HD = m.head_dim;
+    auto mat = [&](const GNCXDecodeTensor& t, size_t rows, size_t cols) -> const uint8_t* {
+        if (!type_supported(t.ggml_type)) {
+            set_error(where, "unsupported ggml_type for a layer matrix", -1);
+            return nullptr;
+        }
+        return device_weights(m.base + t.offset, row_bytes(t.ggml_type, static_cast<int32_t>(cols)) * rows, where);
+    };
+    auto vec = [&](const GNCXDecodeTensor& t, size_t n) -> const float* {
+        return reinterpret_cast<const float*>(device_weights(m.base + t.offset, sizeof(float) * n, where));
+    };
+    std::vector<DecodePlan::Layer> dev(m.n_layers);
+    for (int32_t l = 0; l < m.n_layers; ++l) {
+        const GNCXDecodeLayer& L = m.layers[l];
+        DecodePlan::Layer& d = dev[l];
+        d.attn_norm = vec(L.attn_norm, E);
+        d.ffn_norm = vec(L.ffn_norm, E);
+        d.q_norm = m.qk_norm ? vec(L.attn_q_norm, HD) : nullptr;
+        d.k_norm = m.qk_norm ? vec(L.attn_k_norm, HD) : nullptr;
+        d.q = mat(L.attn_q, Q, E);
+        d.k = mat(L.attn_k, KV, E);
+        d.v = mat(L.attn_v, KV, E);
+        d.o = mat(L.attn_output, E, Q);
+        d.gate = mat(L.ffn_gate, F, E);
+        d.up = mat(L.ffn_up, F, E);
+        d.down = mat(L.ffn_down, E, F);
+        if (!d.attn_norm || !d.ffn_norm || (m.qk_norm && (!d.q_norm || !d.k_norm)) || !d.q || !d.k || !d.v || !d.o ||
+            !d.gate || !d.up || !d.down)
+            return false;
+    }
+    const uint8_t* embd = mat(m.token_embd, static_cast<size_t>(m.vocab), E);
+    const float* onorm = vec(m.output_norm, E);
+    if (!embd || !onorm) return false;
+    p.layers.assign(m.layers, m.layers + m.n_layers);
+    p.embd = m.token_embd;
+    p.onorm = m.output_norm;
+    std::memcpy(p.dims, dims, sizeof(dims));
+    p.dev = std::move(dev);
+    p.embd_dev = embd;
+    p.onorm_dev = onorm;
+    p.base = m.base;
+    return true;
+}
+
+// every buffer of the state must be device memory (checked when it changes)
+bool plan_state(const GNCXDecodeModel& m, const GNCXDecodeState& s, const char* where) {
+    DecodePlan& p = g_plan;
+    const bool same = p.state_ok && std::memcmp(&p.state, &s, sizeof(s)) == 0 &&
+                      std::memcmp(p.kc.data(), s.k_cache, sizeof(float*) * m.n_layers) == 0 &&
+                      std::memcmp(p.vc.data(), s.v_cache, sizeof(float*) * m.n_layers) == 0 &&
+                      p.kc.size() == static_cast<size_t>(m.n_layers);
+    if (same) return true;
+    p.state_ok = false;
+    if (!s.k_cache || !s.v_cache || s.max_seq <= 0) {
+        set_error(where, "KV cache tables and max_seq are required", -1);
+        return false;
+    }
+    const void* need[] = {s.hidden[0], s.hidden[1], s.q, s.k, s.v, s.attn, s.proj, s.normed,
+                          s.gate, s.up, s.act, s.logits, s.token};
+    for (const void* b : need)
+        if (!b || !is_device_ptr(b)) {
+            set_error(where, "every state buffer must be device memory", -1);
+            return false;
+        }
+    if (s.token_log && !is_device_ptr(s.token_log)) {
+        set_error(where, "token_log must be device memory", -1);
+        return false;
+    }
+    for (int32_t l = 0; l < m.n_layers; ++l)
+        if (!s.k_cache[l] || !s.v_cache[l] || !is_device_ptr(s.k_cache[l]) || !is_device_ptr(s.v_cache[l])) {
+            set_error(where, "every KV cache must be device memory", -1);
+            return false;
+        }
+    p.state = s;
+    p.kc.assign(s.k_cache, s.k_cache + m.n_layers);
+    p.vc.assign(s.v_cache, s.v_cache + m.n_layers);
+    p.state_ok = true;
+    return true;
+}
+
+}  // namespace
+
+GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id,
+                                  int32_t pos, int32_t greedy) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_decode_step";
+    if (!model || !state || !model->layers || !model->base) {
+        set_error(where, "model (with base and layers) and state are required", -1);
+        return -1;
+    }
+    const GNCXDecodeModel& m = *model;
+    const GNCXDecodeState& s = *state;
+    if (m.n_layers <= 0 || m.embed <= 0 || m.n_heads <= 0 || m.n_kv_heads <= 0 || m.head_dim <= 0 || m.ffn <= 0 ||
+        m.vocab <= 0 || m.n_heads % m.n_kv_heads != 0) {
+        set_error(where, "invalid model shape", -1);
+        return -1;
+    }
+    if (pos < 0 || pos >= s.max_seq) {
+        set_error(where, "position outside the KV cache", -1);
+        return -1;
+    }
+    if (token_id >= m.vocab) {
+        set_error(where, "token id past the vocabulary", -1);
+        return -1;
+    }
+    if (!ensure_runtime(where) || !plan_model(m, where) || !plan_state(m, s, where)) return -1;
+    const DecodePlan& P = g_plan;
+    const hipStream_t st = g_rt.stream;
+    const int32_t E = m.embed, Q = m.n_heads * m.head_dim, KV = m.n_kv_heads * m.head_dim, F = m.ffn;
+
+    RopeTable rope;
+    const RopeTable* rp = nullptr;
+    if (m.rope_base > 0.0f) {
+        if (!rope_table(pos, m.head_dim, m.rope_base, nullptr, rope)) {
+            set_error(where, "head_dim must be even and at most 512", -1);
+            return -1;
+        }
+        rp = &rope;
+    }
+    if (!g_rt.ws.ensure(attention_workspace_bytes(m.n_heads, m.head_dim, pos + 1), where)) return -1;
+
+    // embedding row of the token (cpp:693-760), into hidden[0]
+    int cur = 0;
+    float* H[2] = {s.hidden[0], s.hidden[1]};
+    if (token_id >= 0) {
+        if (!check(launch_fetch_embedding(m.token_embd.ggml_type, P.embd_dev, token_id, E, 1.0f, H[0], st), where))
+            return -1;
+    } else if (!check(launch_fetch_embedding_dev(m.token_embd.ggml_type, P.embd_dev, s.token, m.vocab, E, 1.0f, H[0],
+                                                 st),
+                      where)) {
+        return -1;
+    }
+
+    // x = RMSNorm(H[cur] + delta) * gamma feeding `count` matrices; the new
+    // residual lands in H[cur ^ 1] when delta is given
+    auto norm_matvec = [&](const float* delta, const float* gamma, int32_t count, const uint8_t* const* ws,
+                           const int32_t* ns, int32_t type, float* const* ys, float* act) -> bool {
+        GemvFusion f;
+        f.h = H[cur];
+        f.r = delta;
+        f.gamma = gamma;
+        f.eps = m.eps;
+        f.h_out = delta ? H[cur ^ 1] : nullptr;
+        f.act = act;
+        hipError_t e = launch_gemv_fused(type, count, ws, ns, E, act ? nullptr : ys, f, st);
+        if (e == hipSuccess) {
+            if (delta) cur ^= 1;
+            return true;
+        }
+        if (e != hipErrorNotSupported) return check(e, where);
+        if (delta) {
+            if (!check(launch_add_rmsnorm(H[cur], delta, gamma, E, m.eps, s.normed, st), where)) return false;
+        } else if (!check(launch_rmsnorm(H[cur], gamma, 1, E, m.eps, s.normed, st), where)) {
+            return false;
+        }
+        if (!act) return check(launch_gemv_multi(type, count, ws, ns, s.normed, E, ys, st), where);
+        float* gu[2] = {s.gate, s.up};
+        return check(launch_gemv_multi(type, 2, ws, ns, s.normed, E, gu, st), where) &&
+               check(launch_swiglu(s.gate, s.up, F, act, st), where);
+    };
+
+    const float* delta = nullptr;
+    for (int32_t l = 0; l < m.n_layers; ++l) {
+        const GNCXDecodeLayer& L = m.layers[l];
+        const DecodePlan::Layer& d = P.dev[l];
+        // Q / K / V (one launch when the three share a type)
+        if (L.attn_k.ggml_type == L.attn_q.ggml_type && L.attn_v.ggml_type == L.attn_q.ggml_type) {
+            const uint8_t* ws[3] = {d.q, d.k, d.v};
+            const int32_t ns[3] = {Q, KV, KV};
+            float* ys[3] = {s.q, s.k, s.v};
+            if (!norm_matvec(delta, d.attn_norm, 3, ws, ns, L.attn_q.ggml_type, ys, nullptr)) return -1;
+        } else {
+            const uint8_t* w1[1] = {d.q};
+            const int32_t n1[1] = {Q};
+            float* y1[1] = {s.q};
+            if (!norm_matvec(delta, d.attn_norm, 1, w1, n1, L.attn_q.ggml_type, y1, nullptr)) return -1;
+            // the normalised x again for K and V: from the updated residual, no delta
+            const uint8_t* wk[1] = {d.k};
+            const int32_t nk[1] = {KV};
+            float* yk[1] = {s.k};
+            if (!norm_matvec(nullptr, d.attn_norm, 1, wk, nk, L.attn_k.ggml_type, yk, nullptr)) return -1;
+            const uint8_t* wv[1] = {d.v};
+            float* yv[1] = {s.v};
+            if (!norm_matvec(nullptr, d.attn_norm, 1, wv, nk, L.attn_v.ggml_type, yv, nullptr)) return -1;
+        }
+        // attention step with the Q/K head norm + RoPE prologue
+        AttnArgs a{};
+        a.q = s.q;
+        a.k_new = s.k;
+        a.v_new = s.v;
+        a.k_cache = s.k_cache[l];
+        a.v_cache = s.v_cache[l];
+        a.out = s.attn;
+        a.pos = pos;
+        a.n_heads = m.n_heads;
+        a.n_kv_heads = m.n_kv_heads;
+        a.head_dim = m.head_dim;
+        a.scale = m.attn_scale;
+        a.sliding_window = 0;
+        a.write_kv = 1;
+        a.norm_qk = m.qk_norm ? 1 : 0;
+        a.q_gamma = d.q_norm;
+        a.k_gamma = d.k_norm;
+        a.eps = m.eps;
+        a.rope = rp;
+        if (!check(launch_attention(a, g_rt.ws.p, g_rt.ws.cap, st), where)) return -1;
+        // O projection
+        if (!check(launch_gemv(L.attn_output.ggml_type, d.o, s.attn, Q, E, s.proj, st), where)) return -1;
+        // gate / up with SwiGLU
+        if (L.ffn_up.ggml_type == L.ffn_gate.ggml_type) {
+            const uint8_t* ws[2] = {d.gate, d.up};
+            const int32_t ns[2] = {F, F};
+            float* ys[2] = {s.gate, s.up};
+            if (!norm_matvec(s.proj, d.ffn_norm, 2, ws, ns, L.ffn_gate.ggml_type, ys, s.act)) return -1;
+        } else {
+            const uint8_t* wg[1] = {d.gate};
+            const int32_t nf[1] = {F};
+            float* yg[1] = {s.gate};
+            if (!norm_matvec(s.proj, d.ffn_norm, 1, wg, nf, L.ffn_gate.ggml_type, yg, nullptr)) return -1;
+            const uint8_t* wu[1] = {d.up};
+            float* yu[1] = {s.up};
+            if (!norm_matvec(nullptr, d.ffn_norm, 1, wu, nf, L.ffn_up.ggml_type, yu, nullptr) ||
+                !check(launch_swiglu(s.gate, s.up, F, s.act, st), where))
+                return -1;
+        }
+        // down projection; its output is the next prologue's delta
+        if (!check(launch_gemv(L.ffn_down.ggml_type, d.down, s.act, F, E, s.proj, st), where)) return -1;
+        delta = s.proj;
+    }
+    // final residual add + RMSNorm, then the tied lm_head (cpp:1713-1732)
+    if (!check(launch_add_rmsnorm(H[cur], delta, P.onorm_dev, E, m.eps, s.normed, st), where)) return -1;
+    if (!check(launch_gemv(m.token_embd.ggml_type, P.embd_dev, s.normed, E, m.vocab, s.logits, st), where)) return -1;
+    if (greedy) {
+        if (!g_rt.aux.ensure(argmax_workspace_bytes(m.vocab), where) ||
+            !check(launch_argmax(s.logits, m.vocab, s.token, s.token_log ? s.token_log + pos : nullptr, g_rt.aux.p,
+                                 g_rt.aux.cap, st),
+                   where))
+            return -1;
+    }
+    return 0;
+}
+
+// index of the first largest logit, on the device (the greedy pick of the
+// streamer's sampler without its repetition penalty, lua/gncx_streamer.lua:1229-1272)
+GNCX_API void gncx_hip_argmax(const float* values, int32_t n, int32_t* out_index) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const char* where = "gncx_hip_argmax";
+    if (!values || !out_index || n <= 0 || !ensure_runtime(where)) return;
+    if (!all_device({values, out_index})) {
+        set_error(where, "values and out_index must be device memory", -1);
+        return;
+    }
+    if (!g_rt.aux.ensure(argmax_workspace_bytes(n), where)) return;
+    check(launch_argmax(values, n, out_index, nullptr, g_rt.aux.p, g_rt.aux.cap, g_rt.stream), where);
 }

@@ -19,6 +19,11 @@ differences are where the streamer works on host memory:
   buffers and run on the host for host buffers;
 * the sampler is a greedy device argmax (the streamer's sampler adds a
   repetition penalty on the host, lua/gncx_streamer.lua:1229-1272);
+* `native=True` decodes through gncx_hip_decode_step: the library issues a
+  whole token's launches itself (no per-call Python and pointer checks), with
+  the residual add + RMSNorm in the prologue of the Q/K/V and gate/up
+  launches and SwiGLU in the epilogue of gate/up; decode_greedy() runs steps
+  that feed their own device argmax back, with no host round trip per token;
 * `fused=True` uses the library's launch-saving extensions, with the same
   results: in decode, gncx_hip_attention_step_fused for the four
   prologue+attention calls, gncx_hip_matvec_multi for Q/K/V and for gate/up
@@ -36,7 +41,7 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass, field
 
-from . import Q4_K, Q6_K, row_bytes
+from . import Q4_K, Q6_K, DecodeLayer, DecodeModel, DecodeState, DecodeTensor, row_bytes
 
 _ALIGN = 32  # GGUF default data alignment
 
@@ -238,9 +243,12 @@ class Decoder:
     host-pointer path: inputs staged, outputs written back before return, KV
     caches mirrored by device twins, residual adds on the host."""
 
-    def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda"):
+    def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda",
+                 native: bool = False):
         s = model.shape
-        self.lib, self.torch, self.m, self.s, self.fused = lib, torch, model, s, fused
+        self.lib, self.torch, self.m, self.s, self.fused, self.native = lib, torch, model, s, fused, native
+        if native and device != "cuda":
+            raise ValueError("the native decode step keeps every buffer in device memory")
         f32 = dict(dtype=torch.float32, device=device)
         self.hidden = torch.zeros(s.embed, **f32)
         self.normed = torch.zeros(s.embed, **f32)
@@ -258,6 +266,7 @@ class Decoder:
         self.max_seq = max_seq
         self.scale = 1.0 / (s.head_dim ** 0.5)
         self._qkv = self._gu = None  # gncx_hip_matvec_multi arguments, built on first fused use
+        self._native = None  # gncx_hip_decode_step structs, built on first native use
 
     def _add(self, dst, src):
         """hidden += delta: the streamer's host loop (lua/gncx_streamer.lua:871-873,
@@ -322,11 +331,61 @@ class Decoder:
         fetch = {Q6_K: self.lib.gncx_fetch_token_embedding_q6_k}[s.embd_type]
         fetch(m.base, m.off("token_embd.weight"), int(token), s.embed, 1.0, dst)
 
+    # -- the native decode step ---------------------------------------------------
+    def _native_structs(self):
+        torch, s, m = self.torch, self.s, self.m
+        T = lambda name, kind=None: DecodeTensor(m.off(name), s.layer_type if kind is None else kind)  # noqa: E731
+        layers = (DecodeLayer * s.n_layers)()
+        for l in range(s.n_layers):
+            p = f"blk.{l}"
+            layers[l] = DecodeLayer(T(f"{p}.attn_norm.weight", -1), T(f"{p}.attn_q.weight"), T(f"{p}.attn_k.weight"),
+                                    T(f"{p}.attn_v.weight"), T(f"{p}.attn_q_norm.weight", -1),
+                                    T(f"{p}.attn_k_norm.weight", -1), T(f"{p}.attn_output.weight"),
+                                    T(f"{p}.ffn_norm.weight", -1), T(f"{p}.ffn_gate.weight"),
+                                    T(f"{p}.ffn_up.weight"), T(f"{p}.ffn_down.weight"))
+        model = DecodeModel(m.base, layers, T("token_embd.weight", s.embd_type), T("output_norm.weight", -1),
+                            s.n_layers, s.embed, s.n_heads, s.n_kv, s.head_dim, s.ffn, s.vocab, 1, s.eps,
+                            s.rope_base, self.scale)
+        f32 = dict(dtype=torch.float32, device=self.hidden.device)
+        self.hidden2 = torch.zeros(s.embed, **f32)
+        self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.hidden.device)
+        self.token_log = torch.full((self.max_seq,), -1, dtype=torch.int32, device=self.hidden.device)
+        P = C.c_void_p
+        kc = (P * s.n_layers)(*(t.data_ptr() for t in self.kc))
+        vc = (P * s.n_layers)(*(t.data_ptr() for t in self.vc))
+        state = DecodeState((P * 2)(self.hidden.data_ptr(), self.hidden2.data_ptr()), self.q.data_ptr(),
+                            self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr(), self.proj.data_ptr(),
+                            self.normed.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr(),
+                            self.logits.data_ptr(), C.cast(kc, C.POINTER(P)), C.cast(vc, C.POINTER(P)),
+                            self.max_seq, self.token_dev.data_ptr(), self.token_log.data_ptr())
+        self._native = (layers, model, kc, vc, state)
+
+    def _step(self, token: int, pos: int, greedy: bool):
+        if pos < 0 or pos >= self.max_seq:
+            raise ValueError("position past the KV cache")
+        if self._native is None:
+            self._native_structs()
+        _, model, _, _, state = self._native
+        if self.lib.gncx_hip_decode_step(C.byref(model), C.byref(state), int(token), int(pos), int(greedy)) != 0:
+            raise RuntimeError(self.lib.gncx_hip_last_error().decode())
+
+    def decode_greedy(self, token: int, pos: int, n: int) -> list:
+        """n greedy steps from `token` at `pos` through the native step: each
+        step's device argmax is the next step's input token, and the host waits
+        once, for the n chosen tokens (the streamer's sampler, without its
+        repetition penalty, lua/gncx_streamer.lua:1229-1272)."""
+        for i in range(n):
+            self._step(token if i == 0 else -1, pos + i, True)
+        return self.token_log[pos:pos + n].tolist()
+
     # -- lua/gncx_streamer.lua:759-965 ------------------------------------------
     def forward_token(self, token: int, pos: int):
         s, L = self.s, self.lib
         if pos >= self.max_seq:
             raise ValueError("position past the KV cache")
+        if self.native:
+            self._step(token, pos, False)
+            return self.logits
         h, nrm = self.hidden.data_ptr(), self.normed.data_ptr()
         q, k, v, a = self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr()
         pr, ga, up, ac = self.proj.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr()

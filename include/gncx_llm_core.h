@@ -210,6 +210,81 @@ void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t* mmap_ba
 void gncx_hip_add_rmsnorm(float* hidden, const float* delta, const uint8_t* mmap_base, size_t norm_weight_offset,
                           int32_t dim, float eps, float* out_normed_fp32);
 
+/* The decode chain's neighbours fused into a matvec launch, for callers whose
+ * activations are device memory (weights may be host or device memory, as
+ * mmap_base + offset).
+ *
+ * out_vecs[i] = W_i . x with x = the RMSNorm of gncx_rmsnorm_and_encode_4phase
+ * (no tokens) of hidden + delta (delta may be NULL), formed inside the launch;
+ * hidden_out (NULL, or a buffer other than hidden) receives hidden + delta.
+ * The same values as gncx_hip_add_rmsnorm followed by gncx_hip_matvec_multi
+ * (lua/gncx_streamer.lua:871-880 then :806-809). */
+void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* delta, const uint8_t* mmap_base,
+                                   size_t norm_weight_offset, float eps, float* hidden_out, int32_t count,
+                                   const uint8_t* const* weights, const int32_t* out_dims, int32_t ggml_type,
+                                   int32_t in_dim, float* const* out_vecs);
+/* out_act = SiLU(W_gate . x) * (W_up . x) in one launch: the values of two
+ * gncx_xfold_universal_matvec calls followed by gncx_swiglu_activation
+ * (lua/gncx_streamer.lua:890-894). */
+void gncx_hip_matvec_swiglu(const uint8_t* gate_weights, const uint8_t* up_weights, int32_t ggml_type,
+                            const float* in_vec, int32_t in_dim, int32_t ffn_dim, float* out_act);
+
+/* Native decode step: one token of GNCXStreamer:forward_token
+ * (lua/gncx_streamer.lua:759-965) for a Qwen3/Llama-shaped model, every
+ * launch issued by the library with the chain fused (per layer: Q/K/V with the
+ * residual add + RMSNorm in its prologue; the attention step with the Q/K head
+ * RMSNorm + RoPE prologue; O; gate/up with the add + RMSNorm prologue and the
+ * SwiGLU epilogue; down), then the final RMSNorm and the tied lm_head into
+ * state->logits.  Stream-ordered: nothing synchronises with the host.
+ * token_id >= 0 is the input token; token_id < 0 reads it from
+ * state->token.  greedy != 0 writes the argmax of the logits to
+ * state->token (and to state->token_log[pos] when token_log is given), so a
+ * loop of steps with token_id = -1 decodes greedily without host round trips.
+ * Tensors are addressed like the streamer's (base + offset); every state
+ * buffer is device memory.  Returns 0, or -1 with gncx_hip_last_error set. */
+typedef struct GNCXDecodeTensor {
+    size_t offset;
+    int32_t ggml_type; /* layer matrices and token_embd; ignored for fp32 norms */
+} GNCXDecodeTensor;
+typedef struct GNCXDecodeLayer {
+    GNCXDecodeTensor attn_norm, attn_q, attn_k, attn_v, attn_q_norm, attn_k_norm, attn_output, ffn_norm, ffn_gate,
+        ffn_up, ffn_down;
+} GNCXDecodeLayer;
+typedef struct GNCXDecodeModel {
+    const uint8_t* base;
+    const GNCXDecodeLayer* layers; /* [n_layers] */
+    GNCXDecodeTensor token_embd;   /* embedding table and tied lm_head */
+    GNCXDecodeTensor output_norm;
+    int32_t n_layers, embed, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    int32_t qk_norm; /* 1: per-head RMSNorm of q and k (Qwen3) */
+    float eps, rope_base, attn_scale;
+} GNCXDecodeModel;
+typedef struct GNCXDecodeState {
+    float* hidden[2]; /* [embed] each: the residual stream alternates between them */
+    float* q;         /* [n_heads * head_dim] */
+    float* k;         /* [n_kv_heads * head_dim] */
+    float* v;
+    float* attn;      /* [n_heads * head_dim] */
+    float* proj;      /* [embed] */
+    float* normed;    /* [embed] */
+    float* gate;      /* [ffn] */
+    float* up;
+    float* act;
+    float* logits;    /* [vocab] */
+    float* const* k_cache; /* [n_layers] of [max_seq][n_kv_heads * head_dim] */
+    float* const* v_cache;
+    int32_t max_seq;
+    int32_t* token;     /* [1] */
+    int32_t* token_log; /* NULL or [max_seq] */
+} GNCXDecodeState;
+int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id, int32_t pos,
+                         int32_t greedy);
+/* *out_index = index of the first largest of values[0..n) (NaN never wins):
+ * the greedy pick of the streamer's sampler without its repetition penalty
+ * (lua/gncx_streamer.lua:1229-1272), on the device.  Device pointers; values
+ * 16-byte aligned; n up to 4194304. */
+void gncx_hip_argmax(const float* values, int32_t n, int32_t* out_index);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,14 @@ def lib():
     return lib
 
 
+@pytest.fixture(scope="session")
+def torch_mod():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch
+
+
 def ptr(a) -> int:
     return 0 if a is None else a.ctypes.data
 

@@ -118,3 +118,38 @@ def test_telemetry_matches_reference(built, ref):
     for f, _ in gncx.GNCXTelemetryStats._fields_:
         assert getattr(mine, f) == getattr(theirs, f), f
     assert mine.zero_origin_cancellations > 0
+
+
+def test_decode_structs_match_header(tmp_path):
+    """The ctypes mirrors of the native decode step's structs have the C
+    layout the header declares (sizes and every field offset, from a program
+    compiled against include/gncx_llm_core.h)."""
+    fields = {
+        "GNCXDecodeTensor": ("offset", "ggml_type"),
+        "GNCXDecodeLayer": ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_q_norm", "attn_k_norm", "attn_output",
+                            "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"),
+        "GNCXDecodeModel": ("base", "layers", "token_embd", "output_norm", "n_layers", "embed", "n_heads",
+                            "n_kv_heads", "head_dim", "ffn", "vocab", "qk_norm", "eps", "rope_base", "attn_scale"),
+        "GNCXDecodeState": ("hidden", "q", "k", "v", "attn", "proj", "normed", "gate", "up", "act", "logits",
+                            "k_cache", "v_cache", "max_seq", "token", "token_log"),
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "gncx_llm_core.h"', "int main(void) {"]
+    for s, fs in fields.items():
+        lines.append(f'printf("{s} sizeof %zu\\n", sizeof({s}));')
+        for f in fs:
+            lines.append(f'printf("{s} {f} %zu\\n", offsetof({s}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for ln in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        s, f, v = ln.split()
+        got[(s, f)] = int(v)
+    py = {"GNCXDecodeTensor": gncx.DecodeTensor, "GNCXDecodeLayer": gncx.DecodeLayer,
+          "GNCXDecodeModel": gncx.DecodeModel, "GNCXDecodeState": gncx.DecodeState}
+    for s, fs in fields.items():
+        assert C.sizeof(py[s]) == got[(s, "sizeof")], s
+        for f in fs:
+            assert getattr(py[s], f).offset == got[(s, f)], (s, f)

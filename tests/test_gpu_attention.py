@@ -357,3 +357,33 @@ def test_rmsnorm_rows_equals_per_row_calls(lib, rows, dim):
     lib.gncx_hip_rmsnorm_rows(ptr(x), rows, ptr(g), 0, dim, 1e-6, ptr(got))
     gncx.check(lib)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 4097, 151936])
+def test_argmax_first_of_equal_maxima(lib, n):
+    """gncx_hip_argmax: torch.argmax's pick (the first of equal maxima), NaN
+    never wins, all -inf gives index 0, and a maximum in the last element of
+    a ragged tail is found."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=g)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cases = [x.clone()]
+    if n > 3:
+        y = x.clone()
+        y[n // 3] = 50.0
+        y[n - 1] = 50.0  # equal maximum later: the first one wins
+        y[1] = float("nan")
+        cases.append(y)
+        z = x.clone()
+        z[n - 1] = 99.0  # the last element of a ragged tail
+        cases.append(z)
+    cases.append(torch.full((n,), float("-inf")))
+    for c in cases:
+        d = c.cuda()
+        lib.gncx_hip_argmax(d.data_ptr(), n, out.data_ptr())
+        gncx.check(lib)
+        want = int(torch.argmax(torch.nan_to_num(c, nan=float("-inf"))).item())
+        assert int(out.item()) == want, (n, int(out.item()), want)

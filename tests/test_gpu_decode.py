@@ -71,14 +71,6 @@ class OracleModel:
         return o.lm_head(s.embd_type, table, x, E, s.vocab, 0.0)
 
 
-@pytest.fixture(scope="module")
-def torch_mod():
-    import torch
-    if not torch.cuda.is_available():
-        pytest.skip("no HIP device")
-    return torch
-
-
 @pytest.mark.parametrize("fused", [False, True])
 def test_decode_steps_match_oracle(lib, oracle, torch_mod, fused):
     import gncx_amd.decode as dec
@@ -182,3 +174,83 @@ def test_host_buffers_match_device_buffers(lib, torch_mod, tmp_path, fused):
     finally:
         lib.gncx_hip_weight_forget(None)
         lib.gncx_hip_kv_forget(None)
+
+
+@pytest.mark.parametrize("layer_type", ["q4_k", "q8_0"])
+def test_native_step_equals_fused_calls(lib, torch_mod, layer_type):
+    """gncx_hip_decode_step (the whole token issued by the library, add+RMSNorm
+    fused into the Q/K/V and gate/up launches, SwiGLU into gate/up) gives the
+    logits of the Python-issued fused call sequence bit for bit.  The Q8_0 case
+    has an FFN width (96) whose gate/up rows do not split evenly over the
+    grid, so it also runs the separate-kernel fallback of the SwiGLU epilogue."""
+    import gncx_amd.decode as dec
+    if layer_type == "q4_k":
+        shape = small_shape()
+    else:
+        shape = dec.Qwen3Shape(n_layers=2, embed=256, n_heads=4, n_kv=2, head_dim=64, ffn=96, vocab=600,
+                               layer_type=gncx.Q8_0)
+    model = _build_any(torch_mod, shape, seed=13)
+    a = dec.Decoder(lib, torch_mod, model, max_seq=32, fused=True)
+    b = dec.Decoder(lib, torch_mod, model, max_seq=32, fused=True, native=True)
+    for pos, tok in enumerate([3, 599, 17, 250, 0, 42]):
+        want = a.forward_token(tok, pos).cpu().numpy()
+        gncx.check(lib)
+        got = b.forward_token(tok, pos).cpu().numpy()
+        gncx.check(lib)
+        print(f"native {layer_type} pos={pos} equal={np.array_equal(got, want)}")
+        assert np.array_equal(got, want), (pos, rel_l2(got, want))
+    for l in range(shape.n_layers):
+        assert torch_mod.equal(a.kc[l][:6], b.kc[l][:6]) and torch_mod.equal(a.vc[l][:6], b.vc[l][:6])
+
+
+def _build_any(torch, shape, seed):
+    """build_model for Q4_K layers, or Q8_0 layers (32-int8 blocks, fp16 d)."""
+    import gncx_amd.decode as dec
+    if shape.layer_type != gncx.Q8_0:
+        return dec.build_model(torch, shape, seed=seed)
+    q4 = dec.Qwen3Shape(**{**shape.__dict__, "layer_type": gncx.Q4_K})
+    lay = dec._layout(shape)
+    offsets, total = {}, 0
+    for name, kind, rows, cols in lay:
+        total = (total + 31) // 32 * 32
+        offsets[name] = total
+        total += dec._nbytes(kind, rows, cols)
+    ref = dec.build_model(torch, q4, seed=seed)  # norms and the Q6_K table come from here
+    blob = torch.empty(total, dtype=torch.uint8, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(seed + 100)
+    for name, kind, rows, cols in lay:
+        o, n = offsets[name], dec._nbytes(kind, rows, cols)
+        if kind == gncx.Q8_0:
+            blk = blob[o:o + n].view(-1, 34)
+            blk.copy_(torch.randint(0, 256, blk.shape, generator=g, device="cuda", dtype=torch.uint8))
+            d = (0.02 * torch.randn(blk.shape[0], 1, generator=g, device="cuda")).abs().to(torch.float16)
+            blk[:, 0:2].copy_(d.view(torch.uint8).view(-1, 2))
+        else:
+            ro = ref.offsets[name]
+            blob[o:o + n].copy_(ref.blob[ro:ro + n])
+    return dec.Model(shape, blob, offsets)
+
+
+def test_native_greedy_loop(lib, oracle, torch_mod):
+    """decode_greedy: steps that feed their own device argmax back (token_id
+    -1) pick the tokens a host loop picks from the same logits, and match the
+    oracle-composed model's greedy tokens; the log holds one token per position."""
+    import gncx_amd.decode as dec
+    model = dec.build_model(torch_mod, small_shape(), seed=17)
+    a = dec.Decoder(lib, torch_mod, model, max_seq=32, fused=True, native=True)
+    b = dec.Decoder(lib, torch_mod, model, max_seq=32, fused=True, native=True)
+    got = a.decode_greedy(5, 0, 10)
+    gncx.check(lib)
+    want, tok = [], 5
+    ref = OracleModel(oracle, model)
+    ref_toks, rt = [], 5
+    for pos in range(10):
+        tok = int(torch_mod.argmax(b.forward_token(tok, pos)).item())
+        want.append(tok)
+        lg = ref.step(rt, pos)
+        rt = int(np.argmax(lg))
+        ref_toks.append(rt)
+    print("native greedy", got, "host", want, "oracle", ref_toks)
+    assert got == want
+    assert got == ref_toks
+    assert a.token_log[10:].eq(-1).all()

@@ -278,3 +278,76 @@ def test_matvec_multi_rejects_bad_counts(lib):
                                   (C.c_void_p * 5)(*[ptr(y)] * 5))
         assert lib.gncx_hip_last_status() != 0
     lib.gncx_hip_weight_forget(ptr(w))
+
+
+@pytest.mark.parametrize("t,k,ns,with_delta", [
+    (gncx.Q4_K, 4096, (4096, 1024, 1024), True),
+    (gncx.Q4_K, 4096, (12288, 12288), True),
+    (gncx.Q8_0, 2048, (512, 256, 256), False),
+    (gncx.Q6_K, 1024, (300,), True),
+    (gncx.Q4_0, 4096, (64,), True),
+    (gncx.Q8_0, 4096, (1024,), True),
+])
+def test_matvec_multi_addnorm_equals_separate_calls(lib, torch_mod, t, k, ns, with_delta):
+    """Residual add + RMSNorm formed inside the matvec launch: outputs and the
+    new residual equal gncx_hip_add_rmsnorm followed by gncx_hip_matvec_multi
+    bit for bit.  Q8_0 at k = 4096 needs two K-slices per row, which the fused
+    schedule does not take: the call runs the separate kernels instead."""
+    torch = torch_mod
+    P, I = C.c_void_p, C.c_int32
+    ws = [torch.from_numpy(synth.make_weights(t, n, k, seed=40 + i)).cuda() for i, n in enumerate(ns)]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    h = torch.randn(k, device="cuda", generator=g)
+    r = torch.randn(k, device="cuda", generator=g) if with_delta else None
+    gamma = 1.0 + 0.1 * torch.randn(k, device="cuda", generator=g)
+    h_out = torch.zeros(k, device="cuda")
+    ys = [torch.zeros(n, device="cuda") for n in ns]
+    cnt = len(ns)
+    wa = (P * cnt)(*(w.data_ptr() for w in ws))
+    na = (I * cnt)(*ns)
+    ya = (P * cnt)(*(y.data_ptr() for y in ys))
+    lib.gncx_hip_matvec_multi_addnorm(h.data_ptr(), r.data_ptr() if r is not None else None, gamma.data_ptr(), 0,
+                                      1e-6, h_out.data_ptr(), cnt, wa, na, t, k, ya)
+    gncx.check(lib)
+    # the separate calls
+    h2 = h.clone()
+    normed = torch.zeros(k, device="cuda")
+    if r is not None:
+        lib.gncx_hip_add_rmsnorm(h2.data_ptr(), r.data_ptr(), gamma.data_ptr(), 0, k, 1e-6, normed.data_ptr())
+    else:
+        lib.gncx_rmsnorm_and_encode_4phase(h2.data_ptr(), gamma.data_ptr(), 0, k, 1e-6, 0, normed.data_ptr(), None,
+                                           None)
+    ys2 = [torch.zeros(n, device="cuda") for n in ns]
+    lib.gncx_hip_matvec_multi(cnt, wa, na, t, normed.data_ptr(), k, (P * cnt)(*(y.data_ptr() for y in ys2)))
+    gncx.check(lib)
+    torch.cuda.synchronize()
+    for a, b in zip(ys, ys2):
+        assert torch.equal(a, b), (a - b).abs().max().item()
+    if r is not None:
+        assert torch.equal(h_out, h2)
+    else:
+        assert torch.equal(h_out, h)
+
+
+@pytest.mark.parametrize("t,k,f", [(gncx.Q4_K, 4096, 12288), (gncx.Q4_K, 1024, 512), (gncx.Q8_0, 512, 96),
+                                   (gncx.Q6_K, 4096, 1024)])
+def test_matvec_swiglu_equals_separate_calls(lib, torch_mod, t, k, f):
+    """gate/up matvecs with SiLU(gate) * up in the launch's epilogue equal two
+    matvecs and gncx_swiglu_activation bit for bit (f = 96 with Q8_0 does not
+    split over the grid and takes the separate kernels)."""
+    torch = torch_mod
+    wg = torch.from_numpy(synth.make_weights(t, f, k, seed=51)).cuda()
+    wu = torch.from_numpy(synth.make_weights(t, f, k, seed=52)).cuda()
+    x = torch.from_numpy(synth.make_activations(1, k, seed=53)).cuda()
+    act = torch.zeros(f, device="cuda")
+    lib.gncx_hip_matvec_swiglu(wg.data_ptr(), wu.data_ptr(), t, x.data_ptr(), k, f, act.data_ptr())
+    gncx.check(lib)
+    gate = torch.zeros(f, device="cuda")
+    up = torch.zeros(f, device="cuda")
+    want = torch.zeros(f, device="cuda")
+    lib.gncx_xfold_universal_matvec(wg.data_ptr(), 0, t, x.data_ptr(), None, k, f, gate.data_ptr(), None)
+    lib.gncx_xfold_universal_matvec(wu.data_ptr(), 0, t, x.data_ptr(), None, k, f, up.data_ptr(), None)
+    lib.gncx_swiglu_activation(gate.data_ptr(), up.data_ptr(), f, want.data_ptr())
+    gncx.check(lib)
+    torch.cuda.synchronize()
+    assert torch.equal(act, want), (act - want).abs().max().item()
