@@ -53,6 +53,7 @@ struct AttnParams {
     RopeTable rope;
 };
 
+
 // Per-head RMSNorm then RoPE of one head held in LDS; one wave.
 template <int HD>
 __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope, float eps,
@@ -71,6 +72,61 @@ __device__ void prologue_head(float* v, const float* gamma, bool norm, bool rope
             const float x1 = v[i], x2 = v[i + H];
             v[i] = x1 * rc[i] - x2 * rs[i];
             v[i + H] = x2 * rc[i] + x1 * rs[i];
+        }
+    }
+}
+
+// The prologue's per-lane operands (norm weights of the elements a lane
+// normalises, the RoPE rows of the pairs it rotates), loaded into registers
+// with the other small operands before the K/V rows, so the prologue waits
+// for no memory.
+template <int HD>
+struct ProRegs {
+    static constexpr int NE = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
+    static constexpr int NR = (HD / 2 + 63) / 64;         // rotated pairs per lane
+    float gq[NE], gk[NE], c[NR], s[NR];
+    __device__ __forceinline__ void load(const AttnParams& p, int lane) {
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            const int i = lane + 64 * e < HD ? lane + 64 * e : 0;
+            gq[e] = p.q_gamma ? p.q_gamma[i] : 1.0f;
+            gk[e] = p.k_gamma ? p.k_gamma[i] : 1.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = lane + 64 * r < HD / 2 ? lane + 64 * r : 0;
+            c[r] = p.rope.c[i];
+            s[r] = p.rope.s[i];
+        }
+    }
+};
+
+// prologue_head with the operands in registers; gamma == nullptr means no weight
+template <int HD>
+__device__ __forceinline__ void prologue_head_r(float* v, const float* g, bool has_gamma, bool norm, bool rope,
+                                                float eps, const ProRegs<HD>& pr, int lane) {
+#pragma clang fp contract(off)
+    if (norm) {
+        const float inv = head_inv_rms(v, HD, eps, lane);
+#pragma unroll
+        for (int e = 0; e < ProRegs<HD>::NE; ++e) {
+            const int i = lane + 64 * e;
+            if (i < HD) {
+                const float x = v[i] * inv;
+                v[i] = has_gamma ? x * g[e] : x;
+            }
+        }
+    }
+    if (rope) {
+        constexpr int H = HD / 2;
+#pragma unroll
+        for (int r = 0; r < ProRegs<HD>::NR; ++r) {
+            const int i = lane + 64 * r;
+            if (i < H) {
+                const float x1 = v[i], x2 = v[i + H];
+                v[i] = x1 * pr.c[r] - x2 * pr.s[r];
+                v[i + H] = x2 * pr.c[r] + x1 * pr.s[r];
+            }
         }
     }
 }
@@ -101,6 +157,21 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
     const bool have_new = p.use_new != 0;
 
+    // q rows of this KV head's query heads, k_new and the prologue operands
+    // first: the prologue then runs while the K/V rows are still in flight
+    constexpr int kQRegs = 8;  // q values per thread held across the K/V issue
+    const float* qg = p.q + static_cast<size_t>(hk) * G * HD;
+    float qreg[kQRegs];
+#pragma unroll
+    for (int u = 0; u < kQRegs; ++u) {
+        const int i = tid + u * kThreads;
+        qreg[u] = i < G * HD ? qg[i] : 0.0f;
+    }
+    const float kreg = (have_new && tid < HD) ? p.k_new[static_cast<size_t>(hk) * HD + tid] : 0.0f;
+    const bool pro = p.norm_qk || p.has_rope;
+    ProRegs<HD> pr;
+    if (pro) pr.load(p, lane);
+
     // SHORT: this thread's token is ta + ts; its K / V slices are loaded now
     // (the new token's K comes from LDS after the prologue, its V from v_new)
     float4 kpre[4], vpre[4];
@@ -127,15 +198,18 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     }
 
     // ---- q (and k_new) into LDS, with the optional prologue ----
-    const float* qg = p.q + static_cast<size_t>(hk) * G * HD;
-    for (int i = tid; i < G * HD; i += kThreads) qs[i] = qg[i];
-    if (have_new)
-        for (int i = tid; i < HD; i += kThreads) ks[i] = p.k_new[static_cast<size_t>(hk) * HD + i];
+#pragma unroll
+    for (int u = 0; u < kQRegs; ++u) {
+        const int i = tid + u * kThreads;
+        if (i < G * HD) qs[i] = qreg[u];
+    }
+    for (int i = tid + kQRegs * kThreads; i < G * HD; i += kThreads) qs[i] = qg[i];
+    if (have_new && tid < HD) ks[tid] = kreg;
     __syncthreads();
-    if (p.norm_qk || p.has_rope) {
+    if (pro) {
         for (int h = wv; h < G + (have_new ? 1 : 0); h += kWaves) {
-            if (h < G) prologue_head<HD>(qs + h * HD, p.q_gamma, p.norm_qk, p.has_rope, p.eps, p.rope.c, p.rope.s, lane);
-            else prologue_head<HD>(ks, p.k_gamma, p.norm_qk, p.has_rope, p.eps, p.rope.c, p.rope.s, lane);
+            if (h < G) prologue_head_r<HD>(qs + h * HD, pr.gq, p.q_gamma != nullptr, p.norm_qk, p.has_rope, p.eps, pr, lane);
+            else prologue_head_r<HD>(ks, pr.gk, p.k_gamma != nullptr, p.norm_qk, p.has_rope, p.eps, pr, lane);
         }
         __syncthreads();
         if (split == 0) {
