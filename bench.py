@@ -291,6 +291,32 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
                      "_native_device_greedy: the same steps feeding their own device argmax back"}
 
 
+def decode_only(pkg, lib, torch, mode, prompt_len, n_tokens, seed=1):
+    """The decode of time_decode in one call sequence: a fused prefill of the
+    random prompt, then n_tokens greedy steps (the native mode feeds its
+    device argmax back)."""
+    import gncx_amd.decode as dec
+    s = dec.QWEN3_8B
+    model = dec.build_model(torch, s, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    prompt = torch.randint(0, s.vocab, (prompt_len,), generator=g).tolist()
+    d = dec.Decoder(lib, torch, model, max_seq=prompt_len + n_tokens + 1, fused=True)
+    tok = d.greedy(d.prefill(prompt))
+    d.fused, d.native = mode != "streamer", mode == "native"
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if mode == "native":
+        d.decode_greedy(tok, prompt_len, n_tokens)
+    else:
+        for i in range(n_tokens):
+            tok = d.greedy(d.forward_token(tok, prompt_len + i))
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / n_tokens
+    pkg.check(lib)
+    return {"decode_mode": mode, "decode_tok_s": round(1.0 / dt, 1), "ms_per_token": round(dt * 1e3, 3),
+            "positions": f"{prompt_len}..{prompt_len + n_tokens - 1}"}
+
+
 def cpu_baseline(pkg, t, k, n, w_host, x_host, seconds=10.0):
     """The reference's own matvec (compiled from its source) on this host's
     cores with its default pool size, clamp(hardware threads, 2, 12)
@@ -338,6 +364,9 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-prompt", type=int, default=2048)
     ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--decode-only", choices=["streamer", "fused", "native"], default=None,
+                    help="only the decode measurement: prefill the prompt (fused), then --decode-tokens greedy "
+                         "tokens through one call sequence, and print its rate (for kernel profiles)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -363,6 +392,10 @@ def main() -> int:
     lib = pkg.load()
     assert lib.gncx_hip_init(0) == 0, lib.gncx_hip_last_error()
     lib.gncx_hip_set_stream(C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    if args.decode_only:
+        print(json.dumps(decode_only(pkg, lib, torch, args.decode_only, args.decode_prompt, args.decode_tokens)),
+              flush=True)
+        return 0
 
     t, k, n = pkg.Q4_K, 4096, 14336
     head = time_gemv(pkg, lib, torch, t, k, n, args.steps, args.warmup, args.copies)
