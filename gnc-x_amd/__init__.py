@@ -76,6 +76,39 @@ SIGNATURES = {
     "gncx_fetch_token_embedding_q8_0": (None, [_vp, _sz, _i32, _i32, _f32, _fp]),
     "gncx_fetch_token_embedding_q6_k": (None, [_vp, _sz, _i32, _i32, _f32, _fp]),
     "gncx_fetch_token_embedding_bf16": (None, [_vp, _sz, _i32, _i32, _f32, _fp]),
+    "gncx_geglu_activation": (None, [_fp, _fp, _i32, _fp]),
+    "gncx_gla_map_readonly": (_vp, [C.c_char_p, _vp]),
+    "gncx_gla_get_base_ptr": (_vp, [_vp]),
+    "gncx_gla_unmap": (None, [_vp]),
+    "gncx_gla_prefetch_range": (None, [_vp, _sz, _sz]),
+    "gncx_ram_alloc_colored": (_vp, [_sz, C.c_uint8, C.c_uint8, C.c_uint8]),
+    "gncx_ram_alloc": (_vp, [_sz]),
+    "gncx_ram_get_ptr": (_vp, [_vp]),
+    "gncx_ram_get_ddr3_bank": (C.c_uint8, [_vp]),
+    "gncx_ram_get_l1_set": (C.c_uint8, [_vp]),
+    "gncx_ram_free": (None, [_vp]),
+    "gncx_ram_copy_chunk": (None, [_vp, _sz, _vp, _sz, _sz]),
+    "gncx_genome_get_layer_coordinate": (None, [_i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "gncx_geo_mm_create": (_vp, [C.c_uint32]),
+    "gncx_geo_mm_destroy": (None, [_vp]),
+    "gncx_geo_alloc": (_i32, [_vp, C.c_uint8, _vp, _vp, _vp, _vp]),
+    "gncx_geo_free": (None, [_vp, C.c_uint8, C.c_uint8, C.c_uint8, C.c_uint32]),
+    "gncx_geo_fragmentation": (_f32, [_vp]),
+    "gncx_geo_used": (_sz, [_vp]),
+    "gncx_geo_capacity": (_sz, [_vp]),
+    # exported but not provided (a call records an error, outputs untouched)
+    "gncx_lora_init_adapter": (None, [_fp, _fp, _i32, _i32, _i32, C.c_uint64]),
+    "gncx_lora_forward_add": (None, [_fp, _fp, _fp, _i32, _i32, _i32, _f32, _fp]),
+    "gncx_lora_backward_step": (None, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _f32, _f32, _f32]),
+    "gncx_mezo_perturb_params": (None, [_fp, _i32, C.c_uint64, _f32]),
+    "gncx_mezo_update_params": (None, [_fp, _i32, C.c_uint64, _f32, _f32, _f32]),
+    "gncx_cross_entropy_loss": (_f32, [_fp, _i32, _i32, _fp]),
+    "gncx_project_layer_3d_point": (None, [_i32, _i32, _vp, _fp, _i32, _vp]),
+    "gncx_cosine_similarity": (_f32, [_fp, _fp, _i32]),
+    "gncx_vector_l2_normalize": (None, [_fp, _i32]),
+    "gncx_mean_pooling": (None, [_fp, _i32, _i32, _fp]),
+    "gncx_bidirectional_attention_gqa": (None, [_fp, _fp, _fp, _i32, _i32, _i32, _i32, _f32, _fp]),
+    "gncx_bidirectional_attention": (None, [_fp, _fp, _fp, _i32, _i32, _i32, _f32, _fp]),
     # extensions
     "gncx_hip_init": (C.c_int, [C.c_int]),
     "gncx_hip_set_stream": (None, [_vp]),

@@ -163,6 +163,19 @@ __global__ void swiglu_kernel(const float* __restrict g, const float* __restrict
     }
 }
 
+// tanh-approximated GELU of the gate times up, in the reference's order of
+// operations (cpp:2024-2030) with no contraction into fused multiply-adds.
+__global__ void geglu_kernel(const float* __restrict g, const float* __restrict u, int32_t n,
+                             float* __restrict out) {
+    constexpr float kSqrt2OverPi = 0.7978845608028654f;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float x = g[i];
+        const float cube = __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x);
+        const float t = tanhf(__fmul_rn(kSqrt2OverPi, __fadd_rn(x, cube)));
+        out[i] = __fmul_rn(__fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, t)), u[i]);
+    }
+}
+
 __global__ void vec_add_kernel(float* __restrict y, const float* __restrict x, int32_t n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] += x[i];
 }
@@ -393,6 +406,12 @@ hipError_t launch_vec_add(float* y, const float* x, int32_t n, hipStream_t strea
 hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, gate, up, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_geglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, gate, up, n, out);
     return hipGetLastError();
 }
 

@@ -139,6 +139,8 @@ hipError_t launch_rope(float* q, float* k, const RopeTable& table, int32_t n_hea
 hipError_t launch_vec_add(float* y, const float* x, int32_t n, hipStream_t stream);
 hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* out,
                          hipStream_t stream);
+// GELU(tanh approximation)(gate)*up (reference cpp:2018-2033).
+hipError_t launch_geglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream);
 // tanh softcap in place (reference cpp:1726-1731).
 hipError_t launch_softcap(float* y, int32_t n, float softcap, hipStream_t stream);
 // One embedding row (reference cpp:693-780), scale folded like the reference.

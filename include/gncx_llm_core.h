@@ -122,6 +122,10 @@ void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const uint8_t* mm
 /* SiLU(gate) * up.  Replaces cpp:2038-2052 (called at streamer.lua:894). */
 void gncx_swiglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim, float* out_ffn_vec);
 
+/* GELU (tanh approximation)(gate) * up.  Replaces cpp:2018-2033 (FFI:
+ * streamer.lua:172-177, called at streamer.lua:896). */
+void gncx_geglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim, float* out_ffn_vec);
+
 /* One dequantised embedding row times scale_factor.  Replace cpp:693-715,
  * cpp:720-760 and cpp:765-780 (called at streamer.lua:698-713). */
 void gncx_fetch_token_embedding_q8_0(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
@@ -130,6 +134,78 @@ void gncx_fetch_token_embedding_q6_k(const uint8_t* mmap_base, size_t tensor_abs
                                      int32_t embed_dim, float scale_factor, float* out_hidden);
 void gncx_fetch_token_embedding_bf16(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,
                                      int32_t embed_dim, float scale_factor, float* out_hidden);
+
+/* Weight file and host buffers (FFI: streamer.lua:30-47).  The file is
+ * mapped read-only with read-ahead advice; buffers are page-locked host
+ * memory (hipHostMalloc) when a HIP device is visible, anonymous pages
+ * otherwise, starting at the address bits of the requested bank / L1-set
+ * colour.  Unmapping, freeing or copying into a range drops the device
+ * copies of weights and KV caches that live inside it.
+ * Replace cpp:327-384, 386-389, 391-404, 617-667, 481-551, 553-559,
+ * 561-574, 576-600 and 602-612 in that order. */
+void* gncx_gla_map_readonly(const char* filepath, size_t* out_size);
+const uint8_t* gncx_gla_get_base_ptr(void* opaque_handle);
+void gncx_gla_unmap(void* opaque_handle);
+void gncx_gla_prefetch_range(const uint8_t* mmap_base, size_t offset, size_t num_bytes);
+void* gncx_ram_alloc_colored(size_t total_bytes, uint8_t k, uint8_t d, uint8_t R);
+void* gncx_ram_alloc(size_t total_bytes);
+uint8_t* gncx_ram_get_ptr(void* ram_handle);
+uint8_t gncx_ram_get_ddr3_bank(void* ram_handle);
+uint8_t gncx_ram_get_l1_set(void* ram_handle);
+void gncx_ram_free(void* ram_handle);
+void gncx_ram_copy_chunk(void* ram_handle, size_t dst_offset, const uint8_t* src_base, size_t src_offset,
+                         size_t num_bytes);
+
+/* Centre-relative layer coordinate.  Replaces cpp:672-686 with
+ * gncx_genome_vm.hpp:35-60 (FFI: streamer.lua:49-57, called at
+ * streamer.lua:502-511). */
+void gncx_genome_get_layer_coordinate(int32_t layer_index, int32_t total_layers, int32_t base_k,
+                                      int32_t* out_rel_layer, int32_t* out_dist_centro, int32_t* out_crivo_k,
+                                      int32_t* out_hemisferio);
+
+/* Diagonal slot manager that colours the KV-cache buffers.  Replaces
+ * cpp:2059-2111 with gncx_geometric_mm.hpp (FFI: streamer.lua:188-194,
+ * called at streamer.lua:514-564). */
+void* gncx_geo_mm_create(uint32_t min_frames);
+void gncx_geo_mm_destroy(void* handle);
+int32_t gncx_geo_alloc(void* handle, uint8_t k_hint, uint8_t* out_k, uint8_t* out_d, uint8_t* out_R,
+                       uint32_t* out_linear_idx);
+void gncx_geo_free(void* handle, uint8_t k, uint8_t d, uint8_t R, uint32_t linear_idx);
+float gncx_geo_fragmentation(void* handle);
+size_t gncx_geo_used(void* handle);
+size_t gncx_geo_capacity(void* handle);
+
+/* Exported under the reference's names and signatures so that every binding
+ * resolves, but NOT provided: a call records an error (gncx_hip_last_status),
+ * prints it and leaves all outputs untouched; float results are 0.  They are
+ * the LoRA / MeZO training primitives (cpp:2129-2331), the layer
+ * visualisation point (cpp:2348-2435) and the embedding-model helpers
+ * (cpp:2443-2654), none of which the quantized decode path calls
+ * (FFI: streamer.lua:211-250). */
+typedef struct GNCXLayer3DPoint GNCXLayer3DPoint; /* layout: streamer.lua:196-209 */
+void gncx_lora_init_adapter(float* a_ptr, float* b_ptr, int32_t in_dim, int32_t out_dim, int32_t rank,
+                            uint64_t seed);
+void gncx_lora_forward_add(const float* in_vec, const float* a_ptr, const float* b_ptr, int32_t in_dim,
+                           int32_t out_dim, int32_t rank, float scale, float* io_out_vec);
+void gncx_lora_backward_step(const float* in_vec, const float* grad_out, float* a_ptr, float* b_ptr,
+                             float* grad_in_accum, int32_t in_dim, int32_t out_dim, int32_t rank, float scale,
+                             float lr, float weight_decay);
+void gncx_mezo_perturb_params(float* params, int32_t num_params, uint64_t seed, float epsilon);
+void gncx_mezo_update_params(float* params, int32_t num_params, uint64_t seed, float projected_grad, float lr,
+                             float weight_decay);
+float gncx_cross_entropy_loss(const float* logits, int32_t vocab_size, int32_t target_token_id,
+                              float* out_grad_logits);
+void gncx_project_layer_3d_point(int32_t layer_index, int32_t total_layers, const GNCXCompactToken* in_tokens,
+                                 const float* normed_fp32, int32_t dim, GNCXLayer3DPoint* out_point);
+float gncx_cosine_similarity(const float* u, const float* v, int32_t dim);
+void gncx_vector_l2_normalize(float* vec, int32_t dim);
+void gncx_mean_pooling(const float* hidden_batch, int32_t batch_size, int32_t dim, float* out_pooled);
+void gncx_bidirectional_attention_gqa(const float* q_batch, const float* k_batch, const float* v_batch,
+                                      int32_t batch_size, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                      float attn_scale, float* out_attn_batch);
+void gncx_bidirectional_attention(const float* q_batch, const float* k_batch, const float* v_batch,
+                                  int32_t batch_size, int32_t n_heads, int32_t head_dim, float attn_scale,
+                                  float* out_attn_batch);
 
 /* ---------------- Part 2: build-side extensions ----------------------- */
 /* No counterpart in the reference. */

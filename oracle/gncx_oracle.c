@@ -552,6 +552,17 @@ void orc_swiglu(const float* gate, const float* up, int32_t n, float* out) {
     }
 }
 
+/* cpp:2018-2033: tanh-approximated GELU of gate times up, with the
+ * reference's constants and association. */
+void orc_geglu(const float* gate, const float* up, int32_t n, float* out) {
+    const float c = 0.7978845608028654f;
+    for (int32_t i = 0; i < n; ++i) {
+        const float x = gate[i];
+        const float inner = c * (x + 0.044715f * x * x * x);
+        out[i] = 0.5f * x * (1.0f + tanhf(inner)) * up[i];
+    }
+}
+
 /* cpp:693-780: one embedding row, times scale_factor folded into d. */
 void orc_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim,
                          float scale, float* out) {

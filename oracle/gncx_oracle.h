@@ -65,6 +65,7 @@ void     orc_attention_step(const float* q, const float* k_new, const float* v_n
                             int32_t head_dim, float scale, int32_t sliding_window,
                             int32_t write_kv, float* out);
 void     orc_swiglu(const float* gate, const float* up, int32_t n, float* out);
+void     orc_geglu(const float* gate, const float* up, int32_t n, float* out);
 void     orc_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim,
                              float scale, float* out);
 

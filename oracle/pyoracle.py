@@ -58,6 +58,7 @@ class Oracle:
             "orc_rope": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32]),
             "orc_attention_step": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
             "orc_swiglu": (None, [_vp, _vp, _i32, _vp]),
+            "orc_geglu": (None, [_vp, _vp, _i32, _vp]),
             "orc_fetch_embedding": (None, [_i32, _vp, _i32, _i32, _f32, _vp]),
         }
         for name, (res, args) in sig.items():
@@ -145,6 +146,12 @@ class Oracle:
         self.lib.orc_swiglu(_ptr(g), _ptr(np.ascontiguousarray(u, dtype=np.float32)), g.size, _ptr(out))
         return out
 
+    def geglu(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.orc_geglu(_ptr(g), _ptr(np.ascontiguousarray(u, dtype=np.float32)), g.size, _ptr(out))
+        return out
+
     def fetch_embedding(self, ggml_type, table, token, dim, scale):
         out = np.empty(dim, dtype=np.float32)
         self.lib.orc_fetch_embedding(ggml_type, _ptr(table), token, dim, scale, _ptr(out))
@@ -173,6 +180,15 @@ class Reference:
             "gncx_apply_rope_xor11_ext": (None, [_vp, _vp, _vp, _vp, _sz, _i32, _i32, _i32, _i32, _i32, _f32]),
             "gncx_rmsnorm_and_encode_4phase": (None, [_vp, _vp, _sz, _i32, _f32, _i32, _vp, _vp, _vp]),
             "gncx_swiglu_activation": (None, [_vp, _vp, _i32, _vp]),
+            "gncx_geglu_activation": (None, [_vp, _vp, _i32, _vp]),
+            "gncx_genome_get_layer_coordinate": (None, [_i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+            "gncx_geo_mm_create": (_vp, [C.c_uint32]),
+            "gncx_geo_mm_destroy": (None, [_vp]),
+            "gncx_geo_alloc": (_i32, [_vp, C.c_uint8, _vp, _vp, _vp, _vp]),
+            "gncx_geo_free": (None, [_vp, C.c_uint8, C.c_uint8, C.c_uint8, C.c_uint32]),
+            "gncx_geo_fragmentation": (_f32, [_vp]),
+            "gncx_geo_used": (_sz, [_vp]),
+            "gncx_geo_capacity": (_sz, [_vp]),
             "gncx_fetch_token_embedding_q8_0": (None, [_vp, _sz, _i32, _i32, _f32, _vp]),
             "gncx_fetch_token_embedding_q6_k": (None, [_vp, _sz, _i32, _i32, _f32, _vp]),
             "gncx_fetch_token_embedding_bf16": (None, [_vp, _sz, _i32, _i32, _f32, _vp]),
@@ -250,6 +266,12 @@ class Reference:
         g = np.ascontiguousarray(g, dtype=np.float32)
         out = np.empty_like(g)
         self.lib.gncx_swiglu_activation(_ptr(g), _ptr(np.ascontiguousarray(u, dtype=np.float32)), g.size, _ptr(out))
+        return out
+
+    def geglu(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.gncx_geglu_activation(_ptr(g), _ptr(np.ascontiguousarray(u, dtype=np.float32)), g.size, _ptr(out))
         return out
 
     def fetch_embedding(self, ggml_type, table, token, dim, scale):

@@ -23,6 +23,9 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "gnc-x_amd"))
 import synth  # noqa: E402
 
+sys.path.insert(0, str(pathlib.Path(__file__).resolve().parent))
+import host_scripts  # noqa: E402
+
 OUT = pathlib.Path(__file__).resolve().parent / "ref_vectors.npz"
 TYPES = {"q4_0": 2, "q8_0": 8, "q4_k": 12, "q6_k": 14, "bf16": 30}
 
@@ -113,6 +116,18 @@ def main() -> None:
     gx = (rng.standard_normal(2048) * 4).astype(np.float32)
     ux = rng.standard_normal(2048).astype(np.float32)
     data["swi_g"], data["swi_u"], data["swi_y"] = gx, ux, ref.swiglu(gx, ux)
+
+    # GeGLU over the tanh range and its saturation, with an odd tail
+    gg = np.concatenate([np.linspace(-12, 12, 2001), rng.standard_normal(50) * 3]).astype(np.float32)
+    gg[7] = 0.0
+    ug = rng.standard_normal(gg.size).astype(np.float32)
+    data["geg_g"], data["geg_u"], data["geg_y"] = gg, ug, ref.geglu(gg, ug)
+
+    # loader host bookkeeping: layer coordinates and slot-manager call sequences
+    data["genome_table"] = host_scripts.genome_table(ref.lib)
+    for mf, n_ops, seed in host_scripts.GEO_CASES:
+        ops, res = host_scripts.geo_generate(ref.lib, mf, n_ops, 7000 + seed)
+        data[f"geo_{mf}_ops"], data[f"geo_{mf}_res"] = ops, res
 
     # embedding rows (the reference's explicit block decoders)
     for name, t in (("q8_0", 8), ("q6_k", 14), ("bf16", 30)):

@@ -16,13 +16,20 @@ import synth
 from conftest import ROOT, gncx, ptr
 
 HEADER = ROOT / "include" / "gncx_llm_core.h"
-REF_CPP_EXPORTS = [  # the hot path and its companions, named as cpp exports them
-    "gncx_xfold_universal_matvec", "gncx_xfold_q4_0_matvec", "gncx_xfold_universal_matbatch",
-    "gncx_xfold_q4_0_matbatch", "gncx_universal_lm_head_logits", "gncx_q8_0_lm_head_logits",
-    "gncx_mqa_attention_step_ext", "gncx_mqa_attention_step", "gncx_rmsnorm_inplace_heads",
-    "gncx_apply_rope_xor11_ext", "gncx_apply_rope_xor11", "gncx_rmsnorm_and_encode_4phase",
-    "gncx_swiglu_activation", "gncx_fetch_token_embedding_q8_0", "gncx_fetch_token_embedding_q6_k",
-    "gncx_fetch_token_embedding_bf16",
+REF_CPP_EXPORTS = [  # the 48 names csrc/gncx_llm_kernels.cpp exports, in its order
+    "gncx_gla_map_readonly", "gncx_gla_get_base_ptr", "gncx_gla_unmap", "gncx_ram_alloc_colored", "gncx_ram_alloc",
+    "gncx_ram_get_ptr", "gncx_ram_get_ddr3_bank", "gncx_ram_get_l1_set", "gncx_ram_free", "gncx_ram_copy_chunk",
+    "gncx_gla_prefetch_range", "gncx_genome_get_layer_coordinate", "gncx_fetch_token_embedding_q8_0",
+    "gncx_fetch_token_embedding_q6_k", "gncx_fetch_token_embedding_bf16", "gncx_rmsnorm_and_encode_4phase",
+    "gncx_rmsnorm_inplace_heads", "gncx_xfold_universal_matvec", "gncx_xfold_q4_0_matvec",
+    "gncx_xfold_universal_matbatch", "gncx_xfold_q4_0_matbatch", "gncx_universal_lm_head_logits",
+    "gncx_q8_0_lm_head_logits", "gncx_apply_rope_xor11_ext", "gncx_apply_rope_xor11", "gncx_mqa_attention_step_ext",
+    "gncx_mqa_attention_step", "gncx_geglu_activation", "gncx_swiglu_activation", "gncx_geo_mm_create",
+    "gncx_geo_mm_destroy", "gncx_geo_alloc", "gncx_geo_free", "gncx_geo_fragmentation", "gncx_geo_used",
+    "gncx_geo_capacity", "gncx_lora_init_adapter", "gncx_lora_forward_add", "gncx_lora_backward_step",
+    "gncx_mezo_perturb_params", "gncx_mezo_update_params", "gncx_cross_entropy_loss", "gncx_project_layer_3d_point",
+    "gncx_cosine_similarity", "gncx_vector_l2_normalize", "gncx_mean_pooling", "gncx_bidirectional_attention_gqa",
+    "gncx_bidirectional_attention",
 ]
 
 
@@ -67,10 +74,11 @@ def test_ctypes_signatures_cover_header(built):
 
 
 def test_exports_match_reference_signatures(built, ref):
-    """Every reference name we export is exported by the reference build too."""
+    """The reference build exports exactly these 48 names, and so does ours."""
     ref_syms = exported(pathlib.Path(ref.lib._name))
-    for name in REF_CPP_EXPORTS:
-        assert name in ref_syms, name
+    assert len(REF_CPP_EXPORTS) == 48
+    assert ref_syms == set(REF_CPP_EXPORTS), sorted(ref_syms ^ set(REF_CPP_EXPORTS))
+    assert set(REF_CPP_EXPORTS) <= exported(built)
 
 
 def _has_gpu(lib) -> bool:

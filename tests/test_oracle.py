@@ -351,6 +351,23 @@ def test_swiglu(oracle, golden):
     assert z[0] == 0.0 and abs(z[1]) < 1e-30
 
 
+def test_geglu(oracle, golden):
+    """The reference library may contract x + 0.044715 x^3 into an FMA; the
+    oracle does not, so the bar is 1e-6 relative L2 plus the closed forms:
+    GELU(0) = 0, x * u where tanh saturates to 1, 0 where it saturates to -1."""
+    g, u = golden["geg_g"], golden["geg_u"]
+    y = oracle.geglu(g, u)
+    assert rel_l2(y, golden["geg_y"]) < 1e-6
+    assert y[7] == 0.0
+    hi, lo = g >= 10.0, g <= -10.0
+    assert np.array_equal(y[hi], (0.5 * g[hi] * 2.0 * u[hi]).astype(np.float32))
+    assert np.all(np.abs(y[lo]) < 1e-6)
+    # float64 evaluation of the same formula
+    x = g.astype(np.float64)
+    want = 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3))) * u
+    assert rel_l2(y, want) < 1e-6
+
+
 def test_oracle_against_live_reference(oracle, ref):
     """Where the reference library is built (this container), compare on a
     fresh seed as well."""
