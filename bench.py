@@ -245,21 +245,35 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     pos += n_tokens
     assert len(toks) == n_tokens and all(0 <= t < s.vocab for t in toks)
     # the unchanged streamer's contract: every buffer and KV cache in host
-    # memory, so each call stages its inputs and writes its outputs back
-    # before returning (short prompt: its per-token prefill alone syncs
-    # ~10 times per token and layer)
+    # memory from gncx_ram_alloc_colored, the 4-phase token array passed as
+    # the streamer passes it (short prompt: its per-token prefill alone syncs
+    # ~10 times per token and layer).  Synchronous: each call stages its
+    # inputs and writes its outputs back before returning.  Lazy: the buffers
+    # keep device copies and only the host's own accesses bring data back.
     host_prompt, host_tokens = 128, 32
     del d
     torch.cuda.empty_cache()
-    dh = dec.Decoder(lib, torch, model, max_seq=host_prompt + host_tokens + 1, device="cpu")
-    tok_h = dh.greedy(dh.prefill(prompt[:host_prompt]))
-    t0 = time.perf_counter()
-    for i in range(host_tokens):
-        tok_h = dh.greedy(dh.forward_token(tok_h, host_prompt + i))
-    host_s = (time.perf_counter() - t0) / host_tokens
-    pkg.check(lib)
-    del dh
-    lib.gncx_hip_kv_forget(None)
+    host_runs = {}
+    for lazy in (0, 1):
+        lib.gncx_hip_set_host_coherence(lazy)
+        dh = dec.Decoder(lib, torch, model, max_seq=host_prompt + host_tokens + 1, device="cpu", host="ram",
+                         tokens=True)
+        try:
+            tok_h = dh.greedy(dh.prefill(prompt[:host_prompt]))
+            seq = []
+            t0 = time.perf_counter()
+            for i in range(host_tokens):
+                tok_h = dh.greedy(dh.forward_token(tok_h, host_prompt + i))
+                seq.append(tok_h)
+            host_runs[lazy] = ((time.perf_counter() - t0) / host_tokens, seq)
+            pkg.check(lib)
+        finally:
+            lib.gncx_hip_set_host_coherence(0)
+            dh.close()
+            del dh
+            lib.gncx_hip_kv_forget(None)
+    host_s, host_lazy_s = host_runs[0][0], host_runs[1][0]
+    assert host_runs[0][1] == host_runs[1][1], "lazy host buffers changed the greedy tokens"
     weight_bytes = model.blob.numel()
     kv_bytes = 2 * s.n_layers * s.kv_dim * 4 * (prompt_len + n_tokens)  # K and V rows read at the mid position
     del model
@@ -279,8 +293,11 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             "prefill_s_fused": round(prefill_fused_s, 3), "prefill_tok_s_fused": round(prompt_len / prefill_fused_s, 1),
             "prefill_fused_vs_unfused_logits_rel_l2": round(prefill_rel, 7), "decode_tokens_each": n_tokens,
             "decode_tok_s_host_buffers": round(1.0 / host_s, 1),
+            "decode_tok_s_host_buffers_lazy": round(1.0 / host_lazy_s, 1),
             "host_buffers_positions": f"{host_prompt}..{host_prompt + host_tokens - 1} (every call's inputs and "
-                                      "outputs in host memory, as the unchanged streamer passes them)",
+                                      "outputs in host buffers from gncx_ram_alloc_colored and the 4-phase token "
+                                      "array, as the unchanged streamer passes them; _lazy: the same with "
+                                      "gncx_hip_set_host_coherence(1), same greedy tokens)",
             "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
             "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
                      "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",

@@ -26,8 +26,10 @@
 // is no CPU fallback.  GNCX_ABORT_ON_ERROR=1 turns failures into abort().
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <signal.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
+#include <ucontext.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -36,6 +38,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -52,7 +55,21 @@ namespace {
 
 using namespace gncx;
 
-std::mutex g_mu;
+// The one lock of the library; t_in_call marks the thread that holds it (the
+// page-fault handler of the lazy host buffers must not take it twice).
+thread_local bool t_in_call = false;
+struct CallLock {
+    std::mutex m;
+    void lock() {
+        m.lock();
+        t_in_call = true;
+    }
+    void unlock() {
+        t_in_call = false;
+        m.unlock();
+    }
+};
+CallLock g_mu;
 std::string g_last_error;
 int g_last_code = 0;
 
@@ -82,6 +99,7 @@ bool check(hipError_t e, const char* where) {
 }
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+size_t dim_count(int32_t v) { return v > 0 ? static_cast<size_t>(v) : 0; }
 
 // ---- runtime state ----------------------------------------------------
 
@@ -451,6 +469,217 @@ void kv_mark_written(float* host, int32_t row) {
     std::memcpy(it->second.row0.data(), host, sizeof(float) * std::min<int32_t>(8, it->second.kv_dim));
 }
 
+// ---- lazily coherent host buffers ---------------------------------------
+// Buffers from gncx_ram_alloc_colored / gncx_ram_alloc are host memory the
+// caller reads and writes with plain loads and stores.  By default they are
+// page-locked and every call that uses one copies in and out and returns
+// complete, as for any host pointer.  In lazy mode (GNCX_HOST_LAZY=1 in the
+// environment, or gncx_hip_set_host_coherence(1), before the buffers are
+// allocated) they are ordinary pages instead, each buffer used by a call gets
+// a device copy, and which copy is current follows the accesses, tracked by
+// page protection:
+//   kHost    the host pages are current and read-write (device copy stale);
+//   kShared  both are current, the pages read-only (a host write is caught);
+//   kDevice  the device copy is current, the pages inaccessible (any host
+//            access is caught).
+// A call that reads a buffer makes the device copy current (one upload when
+// the host pages hold it) and uses it in place; a call that writes one writes
+// the device copy and leaves it kDevice: no download and no wait, so a call
+// whose outputs are all such buffers returns once its work is queued.  A host
+// access to an inaccessible page raises SIGSEGV; the handler waits for the
+// device, downloads the buffer and leaves it read-only (kShared); a host write
+// to a read-only page makes it read-write (kHost).  Each buffer is a mapping
+// of its own, so the protection catches nothing else.  A system call handed
+// an inaccessible buffer fails with EFAULT instead of faulting:
+// gncx_hip_host_flush makes buffers host-resident before such use.
+enum class Home : uint8_t { kHost, kShared, kDevice };
+
+struct HostBuffer {
+    void* block = nullptr;  // what was allocated (whole pages)
+    size_t block_bytes = 0;
+    bool pinned = false;    // hipHostMalloc: page-locked, never protected
+    uint8_t* ptr = nullptr;  // coloured start handed to the caller
+    size_t bytes = 0;
+    uint8_t bank = 0;
+    uint8_t l1_set = 0;
+    uint8_t* twin = nullptr;  // device copy (lazy buffers)
+    Home home = Home::kHost;
+};
+std::map<uintptr_t, HostBuffer*> g_bufs;  // by block address
+int g_lazy = -1;                           // -1: not read from the environment yet
+struct sigaction g_prev_segv;
+
+bool lazy_mode() {
+    if (g_lazy < 0) {
+        const char* e = std::getenv("GNCX_HOST_LAZY");
+        g_lazy = e && e[0] == '1' ? 1 : 0;
+    }
+    return g_lazy == 1;
+}
+
+// The buffer whose block holds address a (page-locked ones included).
+HostBuffer* buffer_at(uintptr_t a) {
+    auto it = g_bufs.upper_bound(a);
+    if (it == g_bufs.begin()) return nullptr;
+    --it;
+    HostBuffer* b = it->second;
+    return a < it->first + b->block_bytes ? b : nullptr;
+}
+
+size_t page_bytes() {
+    static const size_t pg = static_cast<size_t>(sysconf(_SC_PAGESIZE));
+    return pg;
+}
+
+bool protect(HostBuffer& b, int prot) {
+    const uintptr_t pg = page_bytes();
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(b.ptr) & ~(pg - 1);
+    const uintptr_t hi = (reinterpret_cast<uintptr_t>(b.ptr) + b.bytes + pg - 1) & ~(pg - 1);
+    return mprotect(reinterpret_cast<void*>(lo), hi - lo, prot) == 0;
+}
+
+// device copy -> host pages (made read-write first); waits for queued work
+bool download(HostBuffer& b, const char* where) {
+    if (!protect(b, PROT_READ | PROT_WRITE)) {
+        set_error(where, "mprotect failed on a lazy host buffer", -1);
+        return false;
+    }
+    if (!check(hipStreamSynchronize(g_rt.stream), where)) return false;
+    return check(hipMemcpy(b.ptr, b.twin, b.bytes, hipMemcpyDeviceToHost), where);
+}
+
+// host pages -> device copy, ordered after the work already queued
+bool upload(HostBuffer& b, const char* where) {
+    if (b.bytes <= kPinnedMax) return h2d(b.twin, b.ptr, b.bytes, where);
+    if (!check(hipStreamSynchronize(g_rt.stream), where)) return false;
+    return check(hipMemcpy(b.twin, b.ptr, b.bytes, hipMemcpyHostToDevice), where);
+}
+
+// Bring a lazy buffer back to the host: current and read-write.
+bool make_host(HostBuffer& b, const char* where) {
+    if (b.home == Home::kHost) return true;
+    if (b.home == Home::kDevice ? !download(b, where) : !protect(b, PROT_READ | PROT_WRITE)) return false;
+    b.home = Home::kHost;
+    return true;
+}
+
+void on_segv(int sig, siginfo_t* si, void* uc);
+
+void ensure_segv_handler() {
+    struct sigaction cur;
+    sigaction(SIGSEGV, nullptr, &cur);
+    if ((cur.sa_flags & SA_SIGINFO) && cur.sa_sigaction == on_segv) return;
+    struct sigaction sa;
+    std::memset(&sa, 0, sizeof(sa));
+    sa.sa_sigaction = on_segv;
+    sa.sa_flags = SA_SIGINFO | SA_RESTART;
+    sigemptyset(&sa.sa_mask);
+    sigaction(SIGSEGV, &sa, &g_prev_segv);
+}
+
+// A host access to a lazy buffer's protected page: make the host copy
+// current (read-only), or read-write for a write to a read-only page; any
+// other fault goes to the handler that was installed before.
+void on_segv(int sig, siginfo_t* si, void* uc) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(si->si_addr);
+    // x86-64 page-fault error code: bit 1 set for a write
+    const bool write = (static_cast<ucontext_t*>(uc)->uc_mcontext.gregs[REG_ERR] & 2) != 0;
+    bool handled = false;
+    auto handle = [&]() {
+        HostBuffer* b = buffer_at(a);
+        if (!b || b->pinned || !b->twin || b->home == Home::kHost) return;
+        const uintptr_t pg = page_bytes();
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(b->ptr) & ~(pg - 1);
+        const uintptr_t hi = (reinterpret_cast<uintptr_t>(b->ptr) + b->bytes + pg - 1) & ~(pg - 1);
+        if (a < lo || a >= hi) return;
+        const char* where = "lazy host buffer access";
+        if (b->home == Home::kDevice) {
+            if (!download(*b, where)) {
+                (void)protect(*b, PROT_READ | PROT_WRITE);  // the data is lost; keep the program running
+                b->home = Home::kHost;
+            } else if (protect(*b, PROT_READ)) {
+                b->home = Home::kShared;
+            } else {
+                b->home = Home::kHost;
+            }
+        } else if (!write) {
+            // a read that faulted before another thread made the pages readable
+        } else if (protect(*b, PROT_READ | PROT_WRITE)) {
+            b->home = Home::kHost;
+        } else {
+            return;
+        }
+        handled = true;
+    };
+    if (t_in_call) {
+        handle();  // the library itself touched the buffer: it holds the lock
+    } else {
+        std::lock_guard<CallLock> lk(g_mu);
+        handle();
+    }
+    if (handled) return;
+    if (g_prev_segv.sa_flags & SA_SIGINFO) {
+        if (g_prev_segv.sa_sigaction) g_prev_segv.sa_sigaction(sig, si, uc);
+        return;
+    }
+    if (g_prev_segv.sa_handler == SIG_DFL || g_prev_segv.sa_handler == SIG_IGN) {
+        signal(SIGSEGV, SIG_DFL);  // the access runs again and takes the default action
+        return;
+    }
+    g_prev_segv.sa_handler(sig);
+}
+
+// [p, p + bytes) inside a lazy buffer: its address in the device copy, after
+// making that copy current (read) and taking ownership for the device
+// (write).  Any other pointer comes back unchanged.  A range that leaves its
+// buffer makes the buffer host-resident and is used as host memory.
+constexpr int kRd = 1, kWr = 2;
+template <class T>
+T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
+    if (!p || !ok || g_lazy != 1) return p;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    HostBuffer* b = buffer_at(a);
+    if (!b || b->pinned) return p;
+    const size_t bytes = count * sizeof(T);
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(b->ptr);
+    if (a < lo || a + bytes > lo + b->bytes) {
+        ok = make_host(*b, where);
+        return p;
+    }
+    if (!b->twin) {
+        void* d = nullptr;
+        if (!ensure_runtime(where) || !check(hipMalloc(&d, round_up(b->bytes, 256) + 256), where)) {
+            ok = false;
+            return nullptr;
+        }
+        b->twin = static_cast<uint8_t*>(d);
+        b->home = Home::kHost;  // the pages hold the data
+    }
+    ensure_segv_handler();
+    if (b->home == Home::kHost) {
+        // uploaded for writes too: a call that writes nothing keeps the data
+        if (!upload(*b, where)) {
+            ok = false;
+            return nullptr;
+        }
+        if (!protect(*b, PROT_READ)) {
+            set_error(where, "mprotect failed on a lazy host buffer", -1);
+            ok = false;
+            return nullptr;
+        }
+        b->home = Home::kShared;
+    }
+    if ((access & kWr) && b->home != Home::kDevice) {
+        if (!protect(*b, PROT_NONE)) {
+            set_error(where, "mprotect failed on a lazy host buffer", -1);
+            ok = false;
+            return nullptr;
+        }
+        b->home = Home::kDevice;
+    }
+    return reinterpret_cast<T*>(b->twin + (a - lo));
+}
+
 struct AttnCall {
     const float* q;
     const float* k;
@@ -575,7 +804,11 @@ bool attention_impl(const AttnCall& c, const char* where) {
 GNCX_API void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
                                           const float* in_vec, const GNCXCompactToken* in_tokens, int32_t in_dim,
                                           int32_t out_dim, float* out_vec, GNCXTelemetryStats* telemetry) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
+    bool ok = true;
+    in_vec = lazy_ptr(in_vec, dim_count(in_dim), kRd, ok, "gncx_xfold_universal_matvec");
+    out_vec = lazy_ptr(out_vec, dim_count(out_dim), kWr, ok, "gncx_xfold_universal_matvec");
+    if (!ok) return;
     uint64_t canceled = 0;
     bool reuse = false;
     if (in_tokens != nullptr && in_vec == g_act.last_in && in_dim == g_act.last_dim &&
@@ -612,8 +845,12 @@ GNCX_API void gncx_xfold_q4_0_matvec(const uint8_t* mmap_base, size_t weight_abs
 GNCX_API void gncx_xfold_universal_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
                                             const float* in_batch, int32_t batch_size, int32_t in_dim,
                                             int32_t out_dim, float* out_batch, GNCXTelemetryStats* telemetry) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_xfold_universal_matbatch";
+    bool ok = true;
+    in_batch = lazy_ptr(in_batch, dim_count(batch_size) * dim_count(in_dim), kRd, ok, where);
+    out_batch = lazy_ptr(out_batch, dim_count(batch_size) * dim_count(out_dim), kWr, ok, where);
+    if (!ok) return;
     if (type_supported(ggml_type) && batch_size > 0 && out_dim > 0 && in_dim > 0 && ensure_runtime(where)) {
         do {
             const size_t wbytes = row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dim);
@@ -657,7 +894,11 @@ GNCX_API void gncx_xfold_q4_0_matbatch(const uint8_t* mmap_base, size_t weight_a
 GNCX_API void gncx_universal_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, int32_t ggml_type,
                                             const float* final_hidden, int32_t embed_dim, int32_t vocab_size,
                                             float softcap, float* out_logits) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
+    bool ok = true;
+    final_hidden = lazy_ptr(final_hidden, dim_count(embed_dim), kRd, ok, "gncx_universal_lm_head_logits");
+    out_logits = lazy_ptr(out_logits, dim_count(vocab_size), kWr, ok, "gncx_universal_lm_head_logits");
+    if (!ok) return;
     g_act.last_in = nullptr;  // the inner matvec is called with in_tokens == NULL
     if (type_supported(ggml_type) && vocab_size > 0 && embed_dim > 0)
         matvec_impl(mmap_base, embd_abs_offset, ggml_type, final_hidden, embed_dim, vocab_size, out_logits,
@@ -676,10 +917,21 @@ GNCX_API void gncx_mqa_attention_step_ext(const float* q_vec, const float* k_vec
                                           float* k_cache_layer, float* v_cache_layer, int32_t pos, int32_t n_heads,
                                           int32_t n_kv_heads, int32_t head_dim, float attn_scale,
                                           int32_t sliding_window, int32_t write_kv, float* out_attn_vec) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_mqa_attention_step_ext";
+    bool ok = true;
+    const size_t qn = dim_count(n_heads) * dim_count(head_dim), kvn = dim_count(n_kv_heads) * dim_count(head_dim);
+    const int cache_access = write_kv && k_vec && v_vec ? kRd | kWr : kRd;
+    q_vec = lazy_ptr(q_vec, qn, kRd, ok, where);
+    k_vec = lazy_ptr(k_vec, kvn, kRd, ok, where);
+    v_vec = lazy_ptr(v_vec, kvn, kRd, ok, where);
+    k_cache_layer = lazy_ptr(k_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
+    v_cache_layer = lazy_ptr(v_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
+    out_attn_vec = lazy_ptr(out_attn_vec, qn, kWr, ok, where);
+    if (!ok) return;
     AttnCall c{q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim, attn_scale,
                sliding_window, write_kv, out_attn_vec};
-    attention_impl(c, "gncx_mqa_attention_step_ext");
+    attention_impl(c, where);
 }
 
 // cpp:1996-2013
@@ -694,7 +946,7 @@ GNCX_API void gncx_mqa_attention_step(const float* q_vec, const float* k_vec, co
 // cpp:895-953
 GNCX_API void gncx_rmsnorm_inplace_heads(float* vec, const uint8_t* mmap_base, size_t norm_weight_offset,
                                          int32_t has_weight, int32_t n_heads, int32_t head_dim, float eps) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_rmsnorm_inplace_heads";
     if (n_heads <= 0 || head_dim <= 0 || !ensure_runtime(where)) return;
     const float* g = nullptr;
@@ -704,6 +956,9 @@ GNCX_API void gncx_rmsnorm_inplace_heads(float* vec, const uint8_t* mmap_base, s
         if (!g) return;
     }
     const size_t n = static_cast<size_t>(n_heads) * head_dim;
+    bool ok = true;
+    vec = lazy_ptr(vec, n, kRd | kWr, ok, where);
+    if (!ok) return;
     const bool host = !is_device_ptr(vec);
     float* d = host ? const_cast<float*>(stage_in(vec, n, g_rt.q, where)) : vec;
     if (!d) return;
@@ -716,7 +971,7 @@ GNCX_API void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactT
                                         const uint8_t* mmap_base, size_t rope_freqs_offset, int32_t has_rope_freqs,
                                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t pos,
                                         float freq_base) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_apply_rope_xor11_ext";
     if (!ensure_runtime(where)) return;
     const int32_t half = head_dim / 2;
@@ -733,6 +988,10 @@ GNCX_API void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactT
     }
     const size_t qn = q_vec ? static_cast<size_t>(n_heads) * head_dim : 0;
     const size_t kn = k_vec ? static_cast<size_t>(n_kv_heads) * head_dim : 0;
+    bool ok = true;
+    q_vec = lazy_ptr(q_vec, qn, kRd | kWr, ok, where);
+    k_vec = lazy_ptr(k_vec, kn, kRd | kWr, ok, where);
+    if (!ok) return;
     const bool hq = q_vec && !is_device_ptr(q_vec), hk = k_vec && !is_device_ptr(k_vec);
     float* dq = q_vec ? (hq ? const_cast<float*>(stage_in(q_vec, qn, g_rt.q, where)) : q_vec) : nullptr;
     float* dk = k_vec ? (hk ? const_cast<float*>(stage_in(k_vec, kn, g_rt.k, where)) : k_vec) : nullptr;
@@ -757,9 +1016,14 @@ GNCX_API void gncx_apply_rope_xor11(float* q_vec, float* k_vec, GNCXCompactToken
 // cpp:2038-2052
 GNCX_API void gncx_swiglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim,
                                      float* out_ffn_vec) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_swiglu_activation";
     if (ffn_dim <= 0 || !ensure_runtime(where)) return;
+    bool ok = true;
+    gate_vec = lazy_ptr(gate_vec, dim_count(ffn_dim), kRd, ok, where);
+    up_vec = lazy_ptr(up_vec, dim_count(ffn_dim), kRd, ok, where);
+    out_ffn_vec = lazy_ptr(out_ffn_vec, dim_count(ffn_dim), kWr, ok, where);
+    if (!ok) return;
     const float* g = stage_in(gate_vec, ffn_dim, g_rt.q, where);
     const float* u = stage_in(up_vec, ffn_dim, g_rt.k, where);
     if (!g || !u) return;
@@ -773,9 +1037,14 @@ GNCX_API void gncx_swiglu_activation(const float* gate_vec, const float* up_vec,
 // cpp:2018-2033
 GNCX_API void gncx_geglu_activation(const float* gate_vec, const float* up_vec, int32_t ffn_dim,
                                     float* out_ffn_vec) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_geglu_activation";
     if (ffn_dim <= 0 || !ensure_runtime(where)) return;
+    bool ok = true;
+    gate_vec = lazy_ptr(gate_vec, dim_count(ffn_dim), kRd, ok, where);
+    up_vec = lazy_ptr(up_vec, dim_count(ffn_dim), kRd, ok, where);
+    out_ffn_vec = lazy_ptr(out_ffn_vec, dim_count(ffn_dim), kWr, ok, where);
+    if (!ok) return;
     const float* g = stage_in(gate_vec, ffn_dim, g_rt.q, where);
     const float* u = stage_in(up_vec, ffn_dim, g_rt.k, where);
     if (!g || !u) return;
@@ -789,9 +1058,13 @@ GNCX_API void gncx_geglu_activation(const float* gate_vec, const float* up_vec, 
 // y[i] += x[i]: the residual adds the streamer does on the host
 // (lua/gncx_streamer.lua:871-873, 906-908), on the device.
 GNCX_API void gncx_hip_vec_add(float* y, const float* x, int32_t n) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_vec_add";
     if (n <= 0 || !y || !x || !ensure_runtime(where)) return;
+    bool ok = true;
+    x = lazy_ptr(x, dim_count(n), kRd, ok, where);
+    y = lazy_ptr(y, dim_count(n), kRd | kWr, ok, where);
+    if (!ok) return;
     const float* xd = stage_in(x, n, g_rt.k, where);
     if (!xd) return;
     const bool host_y = !is_device_ptr(y);
@@ -806,14 +1079,19 @@ GNCX_API void gncx_hip_vec_add(float* y, const float* x, int32_t n) {
 
 // Several matrices of one type and in_dim applied to the same x in one launch.
 GNCX_API void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
-                                    int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_vecs) {
-    std::lock_guard<std::mutex> lk(g_mu);
+                                    int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_arg) {
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_matvec_multi";
-    if (count <= 0 || count > kMaxGemvMats || !weights || !out_dims || !out_vecs || !in_vec || in_dim <= 0) {
+    if (count <= 0 || count > kMaxGemvMats || !weights || !out_dims || !out_arg || !in_vec || in_dim <= 0) {
         set_error(where, "count must be 1..4, with weights, out_dims, in_vec and out_vecs given", -1);
         return;
     }
     if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    bool ok = true;
+    float* out_vecs[kMaxGemvMats];
+    in_vec = lazy_ptr(in_vec, dim_count(in_dim), kRd, ok, where);
+    for (int32_t i = 0; i < count; ++i) out_vecs[i] = lazy_ptr(out_arg[i], dim_count(out_dims[i]), kWr, ok, where);
+    if (!ok) return;
     // x staged here is not the vector the matvec act-quant cache rule refers to
     g_act.last_in = nullptr;
     g_act.staged_on_device = false;
@@ -849,10 +1127,15 @@ GNCX_API void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights
 // of the new hidden into out_normed_fp32, in one kernel.
 GNCX_API void gncx_hip_add_rmsnorm(float* hidden, const float* delta, const uint8_t* mmap_base,
                                    size_t norm_weight_offset, int32_t dim, float eps, float* out_normed_fp32) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_add_rmsnorm";
     g_norm_epoch++;
     if (dim <= 0 || !hidden || !delta || !out_normed_fp32 || !ensure_runtime(where)) return;
+    bool ok = true;
+    hidden = lazy_ptr(hidden, dim_count(dim), kRd | kWr, ok, where);
+    delta = lazy_ptr(delta, dim_count(dim), kRd, ok, where);
+    out_normed_fp32 = lazy_ptr(out_normed_fp32, dim_count(dim), kWr, ok, where);
+    if (!ok) return;
     const float* g = reinterpret_cast<const float*>(
         device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
     if (!g) return;
@@ -876,8 +1159,11 @@ namespace {
 // cpp:693-780: one row of the embedding table, decoded on the device.
 void fetch_embedding(int32_t type, const uint8_t* base, size_t off, int32_t token, int32_t dim, float scale,
                      float* out, const char* where) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     if (dim <= 0 || token < 0 || !ensure_runtime(where)) return;
+    bool ok = true;
+    out = lazy_ptr(out, dim_count(dim), kWr, ok, where);
+    if (!ok) return;
     const size_t rb = row_bytes(type, dim);
     const uint8_t* row = base + off + static_cast<size_t>(token) * rb;
     const uint8_t* drow;
@@ -926,10 +1212,14 @@ GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const ui
                                              size_t norm_weight_offset, int32_t dim, float eps, int32_t layer_k,
                                              float* out_normed_fp32, GNCXCompactToken* out_tokens,
                                              float* out_quant_scale) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_rmsnorm_and_encode_4phase";
     g_norm_epoch++;
     if (dim <= 0 || !ensure_runtime(where)) return;
+    bool ok = true;
+    input_hidden = lazy_ptr(input_hidden, dim_count(dim), kRd, ok, where);
+    out_normed_fp32 = lazy_ptr(out_normed_fp32, dim_count(dim), kWr, ok, where);
+    if (!ok) return;
     const float* g = reinterpret_cast<const float*>(
         device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
     if (!g) return;
@@ -990,7 +1280,7 @@ GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const ui
 
 // Select the device (default 0 or $GNCX_DEVICE).  Returns 0 or a HIP error.
 GNCX_API int gncx_hip_init(int device) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n <= 0) {
@@ -1007,20 +1297,20 @@ GNCX_API int gncx_hip_init(int device) {
 
 // Stream the library enqueues on (default: the null stream).
 GNCX_API void gncx_hip_set_stream(void* stream) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     g_rt.stream = static_cast<hipStream_t>(stream);
 }
 GNCX_API void* gncx_hip_get_stream(void) { return g_rt.stream; }
 
 GNCX_API int gncx_hip_synchronize(void) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     return static_cast<int>(hipStreamSynchronize(g_rt.stream));
 }
 
 // Last failure ("" when none) and its code (0 when none); reading clears.
 GNCX_API const char* gncx_hip_last_error(void) { return g_last_error.c_str(); }
 GNCX_API int gncx_hip_last_status(void) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const int c = g_last_code;
     g_last_code = 0;
     if (c == 0) g_last_error.clear();
@@ -1029,7 +1319,7 @@ GNCX_API int gncx_hip_last_status(void) {
 
 // Drop the device copy of host weights at p (all copies when p is null).
 GNCX_API void gncx_hip_weight_forget(const void* p) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     if (p) {
         forget_weight(reinterpret_cast<uintptr_t>(p));
         return;
@@ -1041,7 +1331,7 @@ GNCX_API void gncx_hip_weight_forget(const void* p) {
 // Drop the device twin of a host KV cache (all twins when p is null); call
 // after rewriting a host cache outside this library.
 GNCX_API void gncx_hip_kv_forget(const float* p) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     if (p) {
         forget_kv(reinterpret_cast<uintptr_t>(p));
         return;
@@ -1052,7 +1342,7 @@ GNCX_API void gncx_hip_kv_forget(const float* p) {
 
 // Bytes of device memory held by uploaded weights.
 GNCX_API size_t gncx_hip_weight_bytes(void) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     size_t s = 0;
     for (auto& kv : g_rt.weights) s += kv.second.bytes;
     return s;
@@ -1062,7 +1352,7 @@ GNCX_API size_t gncx_hip_weight_bytes(void) {
 // the dots use (bit-exact with the reference's decoders).
 GNCX_API void gncx_hip_dequantize(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
                                   int32_t in_dim, int32_t out_dim, float* out) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_dequantize";
     if (!type_supported(ggml_type) || in_dim <= 0 || out_dim <= 0 || !ensure_runtime(where)) return;
     const size_t wbytes = row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dim);
@@ -1080,7 +1370,7 @@ GNCX_API void gncx_hip_dequantize(const uint8_t* mmap_base, size_t weight_abs_of
 // q[rows*in_dim] int8 and meta[rows*in_dim/32][4] = {d (float bits), sum of
 // q[0:16], sum of q[16:32], sum of q[0:32]}.
 GNCX_API void gncx_hip_quantize_act(const float* in, int32_t rows, int32_t in_dim, int8_t* q, int32_t* meta) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_quantize_act";
     if (rows <= 0 || in_dim <= 0 || !ensure_runtime(where)) return;
     const size_t n = static_cast<size_t>(rows) * in_dim;
@@ -1208,11 +1498,22 @@ GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const fl
                                             size_t q_norm_offset, size_t k_norm_offset, int32_t has_norm_weight,
                                             float norm_eps, size_t rope_freqs_offset, int32_t has_rope_freqs,
                                             float rope_base, float* out_attn_vec) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_attention_step_fused";
+    bool ok = true;
+    const size_t qn = dim_count(n_heads) * dim_count(head_dim), kvn = dim_count(n_kv_heads) * dim_count(head_dim);
+    const int cache_access = write_kv && k_vec && v_vec ? kRd | kWr : kRd;
+    q_vec = lazy_ptr(q_vec, qn, kRd | kWr, ok, where);
+    k_vec = lazy_ptr(k_vec, kvn, kRd | kWr, ok, where);
+    v_vec = lazy_ptr(v_vec, kvn, kRd, ok, where);
+    k_cache_layer = lazy_ptr(k_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
+    v_cache_layer = lazy_ptr(v_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
+    out_attn_vec = lazy_ptr(out_attn_vec, qn, kWr, ok, where);
+    if (!ok) return;
     attention_step_fused_impl(q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim,
                               attn_scale, sliding_window, write_kv, mmap_base, q_norm_offset, k_norm_offset,
                               has_norm_weight, norm_eps, rope_freqs_offset, has_rope_freqs, rope_base, out_attn_vec,
-                              "gncx_hip_attention_step_fused");
+                              where);
 }
 
 // gncx_hip_attention_step_fused for tokens pos0 .. pos0 + batch - 1 in turn
@@ -1224,7 +1525,7 @@ GNCX_API void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const f
                                          size_t k_norm_offset, int32_t has_norm_weight, float norm_eps,
                                          size_t rope_freqs_offset, int32_t has_rope_freqs, float rope_base,
                                          float* out_batch) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_attention_prefill";
     if (!ensure_runtime(where) || batch <= 0) return;
     if (pos0 < 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_heads % n_kv_heads != 0 || !q_batch ||
@@ -1233,6 +1534,15 @@ GNCX_API void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const f
         return;
     }
     const size_t qn = static_cast<size_t>(n_heads) * head_dim, kn = static_cast<size_t>(n_kv_heads) * head_dim;
+    bool ok = true;
+    const size_t bt = dim_count(batch), rows = dim_count(pos0) + bt;
+    q_batch = lazy_ptr(q_batch, bt * qn, kRd | kWr, ok, where);
+    k_batch = lazy_ptr(k_batch, bt * kn, kRd | kWr, ok, where);
+    v_batch = lazy_ptr(v_batch, bt * kn, kRd, ok, where);
+    k_cache_layer = lazy_ptr(k_cache_layer, rows * kn, kRd | kWr, ok, where);
+    v_cache_layer = lazy_ptr(v_cache_layer, rows * kn, kRd | kWr, ok, where);
+    out_batch = lazy_ptr(out_batch, bt * qn, kWr, ok, where);
+    if (!ok) return;
     if (!attention_prefill_supported(n_heads, n_kv_heads, head_dim)) {
         for (int32_t t = 0; t < batch; ++t)
             attention_step_fused_impl(q_batch + t * qn, k_batch + t * kn, v_batch + t * kn, k_cache_layer,
@@ -1315,7 +1625,7 @@ GNCX_API void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const f
 // RMSNorm of `rows` contiguous vectors of dim with one gamma
 GNCX_API void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t* mmap_base,
                                     size_t norm_weight_offset, int32_t dim, float eps, float* out) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_rmsnorm_rows";
     g_norm_epoch++;
     if (rows <= 0 || dim <= 0 || !in || !out || !ensure_runtime(where)) return;
@@ -1348,7 +1658,7 @@ GNCX_API void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* de
                                             size_t norm_weight_offset, float eps, float* hidden_out, int32_t count,
                                             const uint8_t* const* weights, const int32_t* out_dims,
                                             int32_t ggml_type, int32_t in_dim, float* const* out_vecs) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_matvec_multi_addnorm";
     g_norm_epoch++;
     if (count <= 0 || count > kMaxGemvMats || !weights || !out_dims || !out_vecs || !hidden || in_dim <= 0 ||
@@ -1408,7 +1718,7 @@ GNCX_API void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* de
 
 GNCX_API void gncx_hip_matvec_swiglu(const uint8_t* gate_weights, const uint8_t* up_weights, int32_t ggml_type,
                                      const float* in_vec, int32_t in_dim, int32_t ffn_dim, float* out_act) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_matvec_swiglu";
     if (!gate_weights || !up_weights || !in_vec || !out_act || in_dim <= 0 || ffn_dim <= 0) {
         set_error(where, "weights, in_vec, out_act and positive dims are required", -1);
@@ -1572,7 +1882,7 @@ bool plan_state(const GNCXDecodeModel& m, const GNCXDecodeState& s, const char* 
 
 GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id,
                                   int32_t pos, int32_t greedy) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_decode_step";
     if (!model || !state || !model->layers || !model->base) {
         set_error(where, "model (with base and layers) and state are required", -1);
@@ -1733,7 +2043,7 @@ GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecode
 // index of the first largest logit, on the device (the greedy pick of the
 // streamer's sampler without its repetition penalty, lua/gncx_streamer.lua:1229-1272)
 GNCX_API void gncx_hip_argmax(const float* values, int32_t n, int32_t* out_index) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const char* where = "gncx_hip_argmax";
     if (!values || !out_index || n <= 0 || !ensure_runtime(where)) return;
     if (!all_device({values, out_index})) {
@@ -1762,16 +2072,6 @@ struct MappedFile {
     int fd = -1;
     const uint8_t* base = nullptr;
     size_t bytes = 0;
-};
-
-struct HostBuffer {
-    void* block = nullptr;  // what was allocated
-    size_t block_bytes = 0;
-    bool pinned = false;    // hipHostMalloc (else mmap)
-    uint8_t* ptr = nullptr;  // coloured start handed to the caller
-    size_t bytes = 0;
-    uint8_t bank = 0;
-    uint8_t l1_set = 0;
 };
 
 uint32_t g_alloc_seq = 0;  // gncx_ram_alloc's rotating colour (cpp:553-559)
@@ -1845,7 +2145,7 @@ GNCX_API void gncx_gla_unmap(void* opaque_handle) {
     if (!opaque_handle) return;
     auto* h = static_cast<MappedFile*>(opaque_handle);
     {
-        std::lock_guard<std::mutex> lk(g_mu);
+        std::lock_guard<CallLock> lk(g_mu);
         forget_range(reinterpret_cast<uintptr_t>(h->base), reinterpret_cast<uintptr_t>(h->base) + h->bytes);
     }
     munmap(const_cast<uint8_t*>(h->base), h->bytes);
@@ -1873,8 +2173,8 @@ GNCX_API void* gncx_ram_alloc_colored(size_t total_bytes, uint8_t k, uint8_t d, 
     const uintptr_t want = (full ? static_cast<uintptr_t>(bank) << 14 : 0) | (static_cast<uintptr_t>(set) << 6);
     const size_t block_bytes = total_bytes + (size_t{128} << 10) + 64;
     auto* h = new HostBuffer();
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (device_visible() && ensure_runtime("gncx_ram_alloc_colored")) {
+    std::lock_guard<CallLock> lk(g_mu);
+    if (!lazy_mode() && device_visible() && ensure_runtime("gncx_ram_alloc_colored")) {
         void* p = nullptr;
         if (hipHostMalloc(&p, block_bytes, hipHostMallocDefault) == hipSuccess && p) {
             h->block = p;
@@ -1897,6 +2197,7 @@ GNCX_API void* gncx_ram_alloc_colored(size_t total_bytes, uint8_t k, uint8_t d, 
     h->bytes = total_bytes;
     h->bank = static_cast<uint8_t>((a >> 14) & 7u);
     h->l1_set = static_cast<uint8_t>((a >> 6) & 63u);
+    g_bufs[reinterpret_cast<uintptr_t>(h->block)] = h;
     return h;
 }
 
@@ -1906,7 +2207,7 @@ GNCX_API void* gncx_ram_alloc(size_t total_bytes) {
     static constexpr uint8_t kRot[4] = {1, 3, 5, 7};
     uint32_t seq;
     {
-        std::lock_guard<std::mutex> lk(g_mu);
+        std::lock_guard<CallLock> lk(g_mu);
         seq = g_alloc_seq++;
     }
     return gncx_ram_alloc_colored(total_bytes, static_cast<uint8_t>(seq & 3u), static_cast<uint8_t>(seq & 63u),
@@ -1928,8 +2229,14 @@ GNCX_API uint8_t gncx_ram_get_l1_set(void* ram_handle) {
 GNCX_API void gncx_ram_free(void* ram_handle) {
     if (!ram_handle) return;
     auto* h = static_cast<HostBuffer*>(ram_handle);
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     forget_range(reinterpret_cast<uintptr_t>(h->ptr), reinterpret_cast<uintptr_t>(h->ptr) + h->bytes);
+    g_bufs.erase(reinterpret_cast<uintptr_t>(h->block));
+    if (h->twin) {
+        // queued work may still use the device copy
+        (void)hipStreamSynchronize(g_rt.stream);
+        (void)hipFree(h->twin);
+    }
     if (h->pinned) {
         // pending deferred write-backs never target freed memory: they are
         // flushed before the call that queued them returns
@@ -1945,10 +2252,38 @@ GNCX_API void gncx_ram_copy_chunk(void* ram_handle, size_t dst_offset, const uin
                                   size_t num_bytes) {
     if (!ram_handle || !src_base || num_bytes == 0) return;
     auto* h = static_cast<HostBuffer*>(ram_handle);
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     const uintptr_t dst = reinterpret_cast<uintptr_t>(h->ptr) + dst_offset;
     forget_range(dst, dst + num_bytes);
+    if (h->twin && !make_host(*h, "gncx_ram_copy_chunk")) return;
     std::memcpy(h->ptr + dst_offset, src_base + src_offset, num_bytes);
+}
+
+// Lazy coherence of the library's host buffers on (1) or off (0); any other
+// value only reports.  Returns the mode before the call.  It applies to
+// buffers allocated while it is on; turning it off brings every buffer back
+// to the host (current and read-write).
+GNCX_API int gncx_hip_set_host_coherence(int lazy) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const int before = lazy_mode() ? 1 : 0;
+    if (lazy == 0 && before == 1)
+        for (auto& kv : g_bufs)
+            if (kv.second->twin) (void)make_host(*kv.second, "gncx_hip_set_host_coherence");
+    if (lazy == 0 || lazy == 1) g_lazy = lazy;
+    return before;
+}
+
+// Make the host buffer holding p (every buffer when p is null) current and
+// read-write on the host, e.g. before handing it to a system call.
+GNCX_API void gncx_hip_host_flush(const void* p) {
+    std::lock_guard<CallLock> lk(g_mu);
+    if (!p) {
+        for (auto& kv : g_bufs)
+            if (kv.second->twin) (void)make_host(*kv.second, "gncx_hip_host_flush");
+        return;
+    }
+    HostBuffer* b = buffer_at(reinterpret_cast<uintptr_t>(p));
+    if (b && b->twin) (void)make_host(*b, "gncx_hip_host_flush");
 }
 
 // ---- exports outside the decode path ----------------------------------
@@ -1959,7 +2294,7 @@ GNCX_API void gncx_ram_copy_chunk(void* ram_handle, size_t dst_offset, const uin
 // and leaves every output untouched (float results are 0).
 namespace {
 void not_provided(const char* where) {
-    std::lock_guard<std::mutex> lk(g_mu);
+    std::lock_guard<CallLock> lk(g_mu);
     set_error(where, "not provided by this library (outside the quantized decode path); outputs untouched", -1);
 }
 }  // namespace

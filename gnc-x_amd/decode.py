@@ -10,7 +10,12 @@ differences are where the streamer works on host memory:
 * by default every buffer is device memory (torch tensors whose data_ptr()
   goes through the C-ABI, which the library uses in place); with
   Decoder(device="cpu") they are host memory, as in the streamer, and every
-  call takes the library's host-pointer path;
+  call takes the library's host-pointer path.  host="ram" allocates them as
+  the streamer does (lua/gncx_streamer.lua:461-477, 514-564): scratch and
+  KV caches from gncx_ram_alloc_colored, the caches coloured by the
+  gncx_geo_* slot manager at each layer's gncx_genome_* sieve order; with
+  tokens=True the norms and Q/K/V, gate/up and RoPE calls carry the 4-phase
+  token array as the streamer's do (lua/gncx_streamer.lua:793-843, 877-891);
 * the weights are one device blob laid out like a GGUF data section (tensors
   at 32-byte aligned offsets), addressed as (base, offset) exactly as the
   streamer addresses its mapped file;
@@ -244,25 +249,69 @@ class Decoder:
     caches mirrored by device twins, residual adds on the host."""
 
     def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda",
-                 native: bool = False):
+                 native: bool = False, host: str = "torch", tokens: bool = False, layer_k: int = 3):
         s = model.shape
         self.lib, self.torch, self.m, self.s, self.fused, self.native = lib, torch, model, s, fused, native
         if native and device != "cuda":
             raise ValueError("the native decode step keeps every buffer in device memory")
+        if host == "ram" and device != "cpu":
+            raise ValueError("host='ram' places the buffers in host memory: device must be 'cpu'")
         f32 = dict(dtype=torch.float32, device=device)
-        self.hidden = torch.zeros(s.embed, **f32)
-        self.normed = torch.zeros(s.embed, **f32)
-        self.q = torch.zeros(s.q_dim, **f32)
-        self.k = torch.zeros(s.kv_dim, **f32)
-        self.v = torch.zeros(s.kv_dim, **f32)
-        self.attn = torch.zeros(s.q_dim, **f32)
-        self.proj = torch.zeros(s.embed, **f32)
-        self.gate = torch.zeros(s.ffn, **f32)
-        self.up = torch.zeros(s.ffn, **f32)
-        self.act = torch.zeros(s.ffn, **f32)
-        self.logits = torch.zeros(s.vocab, **f32)
-        self.kc = [torch.zeros(max_seq, s.kv_dim, **f32) for _ in range(s.n_layers)]
-        self.vc = [torch.zeros(max_seq, s.kv_dim, **f32) for _ in range(s.n_layers)]
+        self._ram = []  # gncx_ram_* handles, freed by close()
+        if host == "ram":
+            import numpy as np
+
+            def buf(n, slot_d, k=1, r=3, rows=None):
+                count = n * (rows or 1)
+                h = lib.gncx_ram_alloc_colored(max(count * 4, 4096), k, slot_d, r)
+                if not h:
+                    raise MemoryError("gncx_ram_alloc_colored failed")
+                self._ram.append(h)
+                a = np.ctypeslib.as_array((C.c_float * count).from_address(lib.gncx_ram_get_ptr(h)))
+                t = torch.from_numpy(a)
+                return t.view(rows, n) if rows else t
+        else:
+            def buf(n, slot_d, k=1, r=3, rows=None):
+                return torch.zeros(*((rows, n) if rows else (n,)), **f32)
+        # the streamer's scratch colours (lua/gncx_streamer.lua:461-477)
+        self.hidden = buf(s.embed, 0)
+        self.normed = buf(s.embed, 1)
+        self.q = buf(s.q_dim, 2)
+        self.k = buf(s.kv_dim, 3)
+        self.v = buf(s.kv_dim, 4)
+        self.attn = buf(s.q_dim, 5)
+        self.proj = buf(s.embed, 6)
+        self.gate = buf(s.ffn, 7)
+        self.up = buf(s.ffn, 8)
+        self.act = buf(s.ffn, 9)
+        self.logits = buf(s.vocab, 10)
+        # per-layer sieve order (lua/gncx_streamer.lua:502-511)
+        self.crivo = []
+        out = [C.c_int32() for _ in range(4)]
+        for l in range(s.n_layers):
+            lib.gncx_genome_get_layer_coordinate(l, s.n_layers, layer_k, *[C.addressof(o) for o in out])
+            self.crivo.append(out[2].value)
+        self.layer_k = layer_k
+        self.kc, self.vc = [], []
+        if host == "ram":
+            # KV caches coloured by the slot manager (lua/gncx_streamer.lua:514-564)
+            gmm = lib.gncx_geo_mm_create(s.n_layers * 2)
+            kk, dd, rr, idx = C.c_uint8(), C.c_uint8(), C.c_uint8(), C.c_uint32()
+            try:
+                for l in range(s.n_layers):
+                    for lst in (self.kc, self.vc):
+                        lib.gncx_geo_alloc(gmm, self.crivo[l], C.addressof(kk), C.addressof(dd), C.addressof(rr),
+                                           C.addressof(idx))
+                        lst.append(buf(s.kv_dim, dd.value, kk.value, rr.value, rows=max_seq))
+            finally:
+                lib.gncx_geo_mm_destroy(gmm)
+        else:
+            self.kc = [buf(s.kv_dim, 0, rows=max_seq) for _ in range(s.n_layers)]
+            self.vc = [buf(s.kv_dim, 0, rows=max_seq) for _ in range(s.n_layers)]
+        # the 4-phase token array and quant scale (lua/gncx_streamer.lua:486-487)
+        from . import GNCXCompactToken
+        self.tokens = (GNCXCompactToken * max(s.embed, s.q_dim, s.ffn))() if tokens else None
+        self.qscale = (C.c_float * 1)()
         self.max_seq = max_seq
         self.scale = 1.0 / (s.head_dim ** 0.5)
         self._qkv = self._gu = None  # gncx_hip_matvec_multi arguments, built on first fused use
@@ -291,17 +340,28 @@ class Decoder:
             self._gu.append((w, (I * 2)(s.ffn, s.ffn), y))
 
     # -- the pieces shared by forward_token and prefill ----------------------
-    def _matvec(self, name, x, in_dim, out_dim, y):
-        self.lib.gncx_xfold_universal_matvec(self.m.base, self.m.off(name), self.s.layer_type, x, None, in_dim,
+    def close(self):
+        """Free the gncx_ram_* buffers (host="ram"); the buffers' tensors must
+        not be used afterwards."""
+        for h in self._ram:
+            self.lib.gncx_ram_free(h)
+        self._ram = []
+
+    def _tok(self):
+        return C.addressof(self.tokens) if self.tokens is not None else None
+
+    def _matvec(self, name, x, in_dim, out_dim, y, tokens=None):
+        self.lib.gncx_xfold_universal_matvec(self.m.base, self.m.off(name), self.s.layer_type, x, tokens, in_dim,
                                              out_dim, y, None)
 
     def _matbatch(self, name, x, b, in_dim, out_dim, y):
         self.lib.gncx_xfold_universal_matbatch(self.m.base, self.m.off(name), self.s.layer_type, x, b, in_dim,
                                                out_dim, y, None)
 
-    def _norm(self, name, x, out):
-        self.lib.gncx_rmsnorm_and_encode_4phase(x, self.m.base, self.m.off(name), self.s.embed, self.s.eps, 0, out,
-                                                None, None)
+    def _norm(self, name, x, out, layer_k=0):
+        tk = self._tok()
+        self.lib.gncx_rmsnorm_and_encode_4phase(x, self.m.base, self.m.off(name), self.s.embed, self.s.eps, layer_k,
+                                                out, tk, C.addressof(self.qscale) if tk else None)
 
     def _attention(self, l, q, k, v, pos, out):
         s, L, m = self.s, self.lib, self.m
@@ -314,13 +374,13 @@ class Decoder:
             return
         L.gncx_rmsnorm_inplace_heads(q, m.base, m.off(f"{p}.attn_q_norm.weight"), 1, s.n_heads, s.head_dim, s.eps)
         L.gncx_rmsnorm_inplace_heads(k, m.base, m.off(f"{p}.attn_k_norm.weight"), 1, s.n_kv, s.head_dim, s.eps)
-        L.gncx_apply_rope_xor11_ext(q, k, None, None, 0, 0, s.n_heads, s.n_kv, s.head_dim, pos, s.rope_base)
+        L.gncx_apply_rope_xor11_ext(q, k, self._tok(), None, 0, 0, s.n_heads, s.n_kv, s.head_dim, pos, s.rope_base)
         L.gncx_mqa_attention_step_ext(q, k, v, kc, vc, pos, s.n_heads, s.n_kv, s.head_dim, self.scale, 0, 1, out)
 
     def _lm_head(self, normed_ready: bool = False):
         s, m = self.s, self.m
         if not normed_ready:
-            self._norm("output_norm.weight", self.hidden.data_ptr(), self.normed.data_ptr())
+            self._norm("output_norm.weight", self.hidden.data_ptr(), self.normed.data_ptr(), self.layer_k)
         self.lib.gncx_universal_lm_head_logits(m.base, m.off("token_embd.weight"), s.embd_type,
                                                self.normed.data_ptr(), s.embed, s.vocab, 0.0,
                                                self.logits.data_ptr())
@@ -392,18 +452,19 @@ class Decoder:
         self._embed(token, h)
         if self.fused:
             return self._forward_fused(pos)
+        tk = self._tok()
         for l in range(s.n_layers):
             p = f"blk.{l}"
-            self._norm(f"{p}.attn_norm.weight", h, nrm)
-            self._matvec(f"{p}.attn_q.weight", nrm, s.embed, s.q_dim, q)
-            self._matvec(f"{p}.attn_k.weight", nrm, s.embed, s.kv_dim, k)
-            self._matvec(f"{p}.attn_v.weight", nrm, s.embed, s.kv_dim, v)
+            self._norm(f"{p}.attn_norm.weight", h, nrm, self.crivo[l])
+            self._matvec(f"{p}.attn_q.weight", nrm, s.embed, s.q_dim, q, tk)
+            self._matvec(f"{p}.attn_k.weight", nrm, s.embed, s.kv_dim, k, tk)
+            self._matvec(f"{p}.attn_v.weight", nrm, s.embed, s.kv_dim, v, tk)
             self._attention(l, q, k, v, pos, a)
             self._matvec(f"{p}.attn_output.weight", a, s.q_dim, s.embed, pr)
             self._add(self.hidden, self.proj)
-            self._norm(f"{p}.ffn_norm.weight", h, nrm)
-            self._matvec(f"{p}.ffn_gate.weight", nrm, s.embed, s.ffn, ga)
-            self._matvec(f"{p}.ffn_up.weight", nrm, s.embed, s.ffn, up)
+            self._norm(f"{p}.ffn_norm.weight", h, nrm, self.crivo[l])
+            self._matvec(f"{p}.ffn_gate.weight", nrm, s.embed, s.ffn, ga, tk)
+            self._matvec(f"{p}.ffn_up.weight", nrm, s.embed, s.ffn, up, tk)
             L.gncx_swiglu_activation(ga, up, s.ffn, ac)
             self._matvec(f"{p}.ffn_down.weight", ac, s.ffn, s.embed, pr)
             self._add(self.hidden, self.proj)

@@ -226,6 +226,23 @@ void gncx_hip_weight_forget(const void* p);
 /* Drop the device twin of a host KV cache (every twin when p is NULL); call
  * after rewriting a host cache outside this library. */
 void gncx_hip_kv_forget(const float* p);
+/* Lazy coherence of the buffers from gncx_ram_alloc(_colored): 1 on, 0 off,
+ * anything else only reports; returns the mode before the call (the initial
+ * mode is 1 when the environment has GNCX_HOST_LAZY=1).  Buffers allocated
+ * while it is on are ordinary pages with a device copy each: a call that
+ * reads one uses the device copy in place (uploaded once when the host wrote
+ * it), a call that writes one writes only the device copy and, when all its
+ * outputs are such buffers or device memory, returns without waiting for
+ * the device.  The host copy is brought back on the host's first access
+ * (caught by page protection; a SIGSEGV handler is installed and chains to
+ * the previous one).  A system call given a buffer the device holds fails
+ * with EFAULT: call gncx_hip_host_flush first.  Turning the mode off brings
+ * every buffer back to the host.  Off (the default), buffers are page-locked
+ * and every call copies in and out and returns complete. */
+int gncx_hip_set_host_coherence(int lazy);
+/* Bring the buffer holding p (all buffers when p is NULL) back to the host:
+ * current and read-write. */
+void gncx_hip_host_flush(const void* p);
 /* Device bytes held by uploaded weights. */
 size_t gncx_hip_weight_bytes(void);
 /* out[out_dim x in_dim] = fp32 decode of the weights with the block decoders

@@ -1,0 +1,174 @@
+"""GPU: lazily coherent host buffers (gncx_hip_set_host_coherence(1)).
+
+Buffers from gncx_ram_alloc_colored keep a device copy; calls use it in
+place and outputs stay on the device until the host touches them (a page
+fault brings them back).  Every result must equal the synchronous host-buffer
+path bit for bit, through plain numpy / torch reads and writes of the
+buffers between calls, partial writes, in-place calls, KV caches, the
+4-phase token arrays of the streamer, copies into and frees of buffers the
+device holds, and a flush before a system call."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import synth
+from conftest import gncx, ptr, rel_l2
+
+pytestmark = pytest.mark.gpu
+Q4_K = 12
+
+
+@pytest.fixture
+def lazy(lib):
+    before = lib.gncx_hip_set_host_coherence(1)
+    assert before == 0
+    handles = []
+
+    def alloc(n, slot=0):
+        h = lib.gncx_ram_alloc_colored(max(4 * n, 4096), 1, slot, 3)
+        assert h
+        handles.append(h)
+        return h, np.ctypeslib.as_array((C.c_float * n).from_address(lib.gncx_ram_get_ptr(h)))
+
+    yield alloc
+    for h in handles:
+        lib.gncx_ram_free(h)
+    lib.gncx_hip_set_host_coherence(0)
+    lib.gncx_hip_last_status()
+
+
+def test_lazy_matvec_follows_host_reads_and_writes(lib, oracle, lazy):
+    k, n = 1024, 300
+    w = synth.make_weights(Q4_K, n, k, seed=61)
+    _, x = lazy(k, 1)
+    _, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=62)
+    y[:] = 5.0
+    for rnd in range(3):
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+        gncx.check(lib)
+        want = oracle.matvec(Q4_K, w, x.copy(), k, n)
+        assert rel_l2(y, want) < 1e-3, rnd          # a host read brings y back
+        assert rel_l2(y.copy(), want) < 1e-3        # and reads again without a round trip
+        x[::7] *= -1.5                              # a host write to x: the next call uploads it
+    # in place on a buffer the device holds, then a partial host write
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    lib.gncx_hip_vec_add(y.ctypes.data, y.ctypes.data, n)
+    gncx.check(lib)
+    want = 2 * oracle.matvec(Q4_K, w, x.copy(), k, n)
+    assert rel_l2(y, want) < 1e-3
+    y[10] = 123.0
+    lib.gncx_hip_vec_add(y.ctypes.data, y.ctypes.data, n)
+    want[10] = 123.0
+    assert rel_l2(y, 2 * want) < 1e-3 and y[10] == 246.0
+
+
+def test_lazy_elementwise_outputs_stay_on_device(lib, golden, lazy):
+    """SwiGLU and GeGLU chained through lazy buffers, one in place; the
+    outputs are read on the host only at the end."""
+    gg, uu = golden["swi_g"], golden["swi_u"]
+    nf = gg.size
+    _, g = lazy(nf, 1)
+    _, u = lazy(nf, 2)
+    _, a = lazy(nf, 3)
+    _, b = lazy(nf, 4)
+    g[:], u[:] = gg, uu
+    lib.gncx_swiglu_activation(g.ctypes.data, u.ctypes.data, nf, a.ctypes.data)
+    lib.gncx_geglu_activation(a.ctypes.data, u.ctypes.data, nf, b.ctypes.data)
+    lib.gncx_swiglu_activation(g.ctypes.data, u.ctypes.data, nf, g.ctypes.data)  # in place
+    gncx.check(lib)
+    lib.gncx_hip_set_host_coherence(0)
+    try:
+        hg, hu = gg.copy(), uu.copy()  # named: the library reads them during the calls
+        ref_a = np.zeros(nf, np.float32)
+        ref_b = np.zeros(nf, np.float32)
+        lib.gncx_swiglu_activation(ptr(hg), ptr(hu), nf, ptr(ref_a))
+        lib.gncx_geglu_activation(ptr(ref_a), ptr(hu), nf, ptr(ref_b))
+    finally:
+        lib.gncx_hip_set_host_coherence(1)
+    assert np.array_equal(b, ref_b)
+    assert np.array_equal(a, ref_a)
+    assert np.array_equal(g, ref_a)
+
+
+def test_lazy_flush_before_system_call(lib, oracle, lazy, tmp_path):
+    k, n = 512, 1024
+    w = synth.make_weights(Q4_K, n, k, seed=63)
+    _, x = lazy(k, 1)
+    _, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=64)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    gncx.check(lib)
+    lib.gncx_hip_host_flush(y.ctypes.data)
+    f = tmp_path / "y.bin"
+    fd = os.open(f, os.O_WRONLY | os.O_CREAT)
+    try:
+        assert os.write(fd, memoryview(y).cast("B")) == 4 * n
+    finally:
+        os.close(fd)
+    assert rel_l2(np.fromfile(f, np.float32), oracle.matvec(Q4_K, w, x.copy(), k, n)) < 1e-3
+
+
+def test_lazy_copy_chunk_and_free_of_device_held_buffers(lib, oracle, lazy):
+    k, n = 512, 256
+    w = synth.make_weights(Q4_K, n, k, seed=65)
+    _, x = lazy(k, 1)
+    hy, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=66)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    gncx.check(lib)
+    src = np.arange(16, dtype=np.float32)
+    lib.gncx_ram_copy_chunk(hy, 8, ptr(src), 0, src.nbytes)   # into a buffer the device holds
+    want = oracle.matvec(Q4_K, w, x.copy(), k, n)
+    want[2:18] = src
+    assert rel_l2(y, want) < 1e-3 and np.array_equal(y[2:18], src)
+    # freeing a buffer whose newest data is on the device
+    h2 = lib.gncx_ram_alloc_colored(4 * n, 2, 3, 5)
+    y2 = np.ctypeslib.as_array((C.c_float * n).from_address(lib.gncx_ram_get_ptr(h2)))
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y2.ctypes.data, None)
+    del y2
+    lib.gncx_ram_free(h2)
+    gncx.check(lib)
+
+
+def test_lazy_decode_equals_synchronous_host_buffers(lib, torch_mod, tmp_path):
+    """The streamer's decode through buffers from gncx_ram_alloc_colored and
+    the 4-phase token array, with lazy coherence and without: identical
+    logits, token arrays and KV caches."""
+    import gncx_amd.decode as dec
+    from test_gpu_decode import small_shape
+    dec.write_model_gguf(tmp_path / "m.gguf", small_shape(), seed=34)
+    m = dec.load_model_gguf(tmp_path / "m.gguf")
+    runs = []
+    try:
+        for lazy_mode in (0, 1):
+            lib.gncx_hip_set_host_coherence(lazy_mode)
+            d = dec.Decoder(lib, torch_mod, m, max_seq=16, device="cpu", host="ram", tokens=True)
+            try:
+                tok, logits, toks = 11, [], []
+                for pos in range(6):
+                    a = d.forward_token(tok, pos).numpy().copy()
+                    gncx.check(lib)
+                    logits.append(a)
+                    toks.append(bytes(d.tokens))
+                    tok = d.greedy(d.logits)
+                kc = d.kc[1].numpy()[:6].copy()
+                vc = d.vc[0].numpy()[:6].copy()
+                runs.append((logits, toks, kc, vc))
+            finally:
+                lib.gncx_hip_set_host_coherence(0)
+                d.close()
+        (la, ta, ka, va), (lb, tb, kb, vb) = runs
+        for i in range(len(la)):
+            assert np.array_equal(la[i], lb[i]), i
+            assert ta[i] == tb[i], i
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        assert np.abs(ka).sum() > 0
+    finally:
+        lib.gncx_hip_set_host_coherence(0)
+        lib.gncx_hip_weight_forget(None)
+        lib.gncx_hip_kv_forget(None)
