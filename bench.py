@@ -254,10 +254,10 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     del d
     torch.cuda.empty_cache()
     host_runs = {}
-    for lazy in (0, 1):
+    for lazy, driver in ((0, "python"), (1, "python"), (0, "c"), (1, "c")):
         lib.gncx_hip_set_host_coherence(lazy)
         dh = dec.Decoder(lib, torch, model, max_seq=host_prompt + host_tokens + 1, device="cpu", host="ram",
-                         tokens=True)
+                         tokens=True, driver=driver)
         try:
             tok_h = dh.greedy(dh.prefill(prompt[:host_prompt]))
             seq = []
@@ -265,15 +265,15 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             for i in range(host_tokens):
                 tok_h = dh.greedy(dh.forward_token(tok_h, host_prompt + i))
                 seq.append(tok_h)
-            host_runs[lazy] = ((time.perf_counter() - t0) / host_tokens, seq)
+            host_runs[lazy, driver] = ((time.perf_counter() - t0) / host_tokens, seq)
             pkg.check(lib)
         finally:
             lib.gncx_hip_set_host_coherence(0)
             dh.close()
             del dh
             lib.gncx_hip_kv_forget(None)
-    host_s, host_lazy_s = host_runs[0][0], host_runs[1][0]
-    assert host_runs[0][1] == host_runs[1][1], "lazy host buffers changed the greedy tokens"
+    host_tok_s = {k: round(1.0 / v[0], 1) for k, v in host_runs.items()}
+    assert all(v[1] == host_runs[0, "python"][1] for v in host_runs.values()), "host-buffer runs disagree"
     weight_bytes = model.blob.numel()
     kv_bytes = 2 * s.n_layers * s.kv_dim * 4 * (prompt_len + n_tokens)  # K and V rows read at the mid position
     del model
@@ -292,12 +292,16 @@ def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
             "prefill_tok_s": round(prompt_len / prefill_s, 1),
             "prefill_s_fused": round(prefill_fused_s, 3), "prefill_tok_s_fused": round(prompt_len / prefill_fused_s, 1),
             "prefill_fused_vs_unfused_logits_rel_l2": round(prefill_rel, 7), "decode_tokens_each": n_tokens,
-            "decode_tok_s_host_buffers": round(1.0 / host_s, 1),
-            "decode_tok_s_host_buffers_lazy": round(1.0 / host_lazy_s, 1),
+            "decode_tok_s_host_buffers": host_tok_s[0, "python"],
+            "decode_tok_s_host_buffers_lazy": host_tok_s[1, "python"],
+            "decode_tok_s_host_buffers_native_caller": host_tok_s[0, "c"],
+            "decode_tok_s_host_buffers_native_caller_lazy": host_tok_s[1, "c"],
             "host_buffers_positions": f"{host_prompt}..{host_prompt + host_tokens - 1} (every call's inputs and "
                                       "outputs in host buffers from gncx_ram_alloc_colored and the 4-phase token "
-                                      "array, as the unchanged streamer passes them; _lazy: the same with "
-                                      "gncx_hip_set_host_coherence(1), same greedy tokens)",
+                                      "array, as the unchanged streamer passes them, issued from Python or "
+                                      "(_native_caller) from gncx_streamer_replay.so as LuaJIT's FFI issues "
+                                      "them; _lazy: with gncx_hip_set_host_coherence(1); all four runs pick the "
+                                      "same greedy tokens)",
             "weights_bytes": weight_bytes, "model_build_s": round(build_s, 2),
             "model": "Qwen3-8B-shaped random-init: 36 layers, hidden 4096, 32/8 heads x 128, FFN 12288, "
                      "vocab 151936; Q4_K attention/FFN, tied Q6_K token_embd as lm_head",

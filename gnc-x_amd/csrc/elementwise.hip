@@ -56,6 +56,61 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_long_kernel(float* __restri
     }
 }
 
+// The 4-phase telemetry encode of one vector (reference cpp:842-889) by one
+// work-group of kNormThreads: the largest |v| (at least 1e-9), the scale to
+// the layer's integer range 9 R_k (R_k the repunit of k ones), then per
+// element the rounded integer, its diagonal digit d (nearest multiple of R_k,
+// at most 9), the residual from d R_k and the two sign bits, packed as the
+// 4-byte token {phase, d, |residual| mod 2^16}.  Every float step is the
+// reference's, correctly rounded and uncontracted, so the tokens are
+// bit-exact.  qscale[0] receives the quant scale and qscale[1] (as a
+// uint32) the cancellation count sum_d min(#positive, #negative) over the
+// digits d (cpp:882-887).  red: kNormThreads / 64 floats of LDS.
+__device__ void encode_row(const float* v, int32_t dim, int32_t lay_k, uint32_t* __restrict tokens,
+                           float* __restrict qscale, float* red) {
+    __shared__ uint32_t signs[2][10];
+    if (threadIdx.x < 20) signs[threadIdx.x / 10][threadIdx.x % 10] = 0;
+    float m = 1e-9f;
+    for (int32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float a = fabsf(v[i]);
+        m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float t = __shfl_xor(m, o, 64);
+        m = t > m ? t : m;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x / 64); ++w) m = red[w] > m ? red[w] : m;
+    int64_t r_k = 1;
+    for (int i = 0; i < lay_k; ++i) r_k = r_k * 10 + 1;
+    const float target = static_cast<float>(9 * r_k);
+    const float to_int = __fdiv_rn(target, m);
+    if (threadIdx.x == 0) *qscale = __fdiv_rn(m, target);
+    const float inv_rk = __fdiv_rn(1.0f, static_cast<float>(r_k));
+    const float half_rk = static_cast<float>(r_k >> 1);
+    for (int32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const int64_t val = static_cast<int64_t>(rintf(__fmul_rn(v[i], to_int)));
+        const int64_t av = val >= 0 ? val : -val;
+        int32_t d = static_cast<int32_t>(__fmul_rn(__fadd_rn(static_cast<float>(av), half_rk), inv_rk));
+        if (d > 9) d = 9;
+        const int64_t anchor = static_cast<int64_t>(d) * r_k;
+        const int64_t res = val - (val >= 0 ? anchor : -anchor);
+        const uint32_t ares = static_cast<uint32_t>(static_cast<uint16_t>(res >= 0 ? res : -res));
+        const uint32_t phase = (val >= 0 ? 2u : 0u) | (res >= 0 ? 1u : 0u);
+        tokens[i] = phase | (static_cast<uint32_t>(d) << 8) | (ares << 16);
+        __hip_atomic_fetch_add(&signs[val >= 0 ? 0 : 1][d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t c = 0;
+        for (int d = 0; d < 10; ++d) c += signs[0][d] < signs[1][d] ? signs[0][d] : signs[1][d];
+        reinterpret_cast<uint32_t*>(qscale)[1] = c;
+    }
+}
+
 // RMSNorm of one row per work-group (cpp:789-833): x and gamma are read once
 // as float4 (kept in registers for rows up to 16384 values), the sum of
 // squares is a fp32 tree over the work-group, y = (x * inv) * gamma.
@@ -64,12 +119,14 @@ constexpr int kNormRegs = 4;  // float4 per thread held in registers
 
 // ADD: x is the residual stream h (one row), updated in place to h + r
 // before it is normalised -- the fp32 add of the separate vec_add kernel, so
-// the result is the same bit for bit.
-template <bool ADD>
+// the result is the same bit for bit.  ENC: the 4-phase encode of the
+// normalised row follows in the same work-group (one row).
+template <bool ADD, bool ENC = false>
 // (x and xo are the same row under ADD: no __restrict on the row pointers)
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* __restrict g,
                                                                int32_t dim, float eps, float* out, int32_t vec4,
-                                                               const float* r, float* xo) {
+                                                               const float* r, float* xo, int32_t lay_k = 0,
+                                                               uint32_t* tokens = nullptr, float* qscale = nullptr) {
 #pragma clang fp contract(off)
     __shared__ float part[kNormThreads / 64];
     const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
@@ -137,6 +194,11 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
         y4[t] = make_float4(a.x * inv * b.x, a.y * inv * b.y, a.z * inv * b.z, a.w * inv * b.w);
     }
     for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) yr[i] = xr[i] * inv * g[i];
+    if constexpr (ENC) {
+        __threadfence_block();
+        __syncthreads();
+        encode_row(yr, dim, lay_k, tokens, qscale, part);
+    }
 }
 
 __global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable t, int32_t n_heads,
@@ -412,6 +474,18 @@ hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* o
 hipError_t launch_geglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(geglu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, gate, up, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_encode(const float* x, const float* gamma, int32_t dim, float eps, float* out,
+                                 int32_t layer_k, uint32_t* tokens, float* qscale, hipStream_t stream) {
+    if (dim <= 0) return hipSuccess;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma) |
+                         reinterpret_cast<uintptr_t>(out);
+    const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
+    const int32_t k = layer_k < 0 ? 0 : (layer_k > 17 ? 17 : layer_k);
+    hipLaunchKernelGGL((rmsnorm_kernel<false, true>), dim3(1), dim3(kNormThreads), 0, stream, x, gamma, dim, eps, out,
+                       vec4, nullptr, nullptr, k, tokens, qscale);
     return hipGetLastError();
 }
 

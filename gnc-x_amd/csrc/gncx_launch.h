@@ -141,6 +141,13 @@ hipError_t launch_swiglu(const float* gate, const float* up, int32_t n, float* o
                          hipStream_t stream);
 // GELU(tanh approximation)(gate)*up (reference cpp:2018-2033).
 hipError_t launch_geglu(const float* gate, const float* up, int32_t n, float* out, hipStream_t stream);
+// launch_rmsnorm of one row, then in the same kernel the 4-phase telemetry
+// tokens of the result (reference cpp:842-889) as packed {phase, d,
+// |residual|} words, the quant scale in qscale[0] and the cancellation count
+// (uint32) in qscale[1]; layer_k clamped to [0, 17].  tokens and qscale may
+// be page-locked host memory.
+hipError_t launch_rmsnorm_encode(const float* x, const float* gamma, int32_t dim, float eps, float* out,
+                                 int32_t layer_k, uint32_t* tokens, float* qscale, hipStream_t stream);
 // tanh softcap in place (reference cpp:1726-1731).
 hipError_t launch_softcap(float* y, int32_t n, float softcap, hipStream_t stream);
 // One embedding row (reference cpp:693-780), scale folded like the reference.

@@ -57,7 +57,10 @@ using namespace gncx;
 
 // The one lock of the library; t_in_call marks the thread that holds it (the
 // page-fault handler of the lazy host buffers must not take it twice).
+// Before the lock is released, a call's writes to lazy host buffers that the
+// host reads back get their copies to the host queued (queue_readbacks).
 thread_local bool t_in_call = false;
+void queue_readbacks();
 struct CallLock {
     std::mutex m;
     void lock() {
@@ -65,6 +68,7 @@ struct CallLock {
         t_in_call = true;
     }
     void unlock() {
+        queue_readbacks();
         t_in_call = false;
         m.unlock();
     }
@@ -504,8 +508,22 @@ struct HostBuffer {
     uint8_t l1_set = 0;
     uint8_t* twin = nullptr;  // device copy (lazy buffers)
     Home home = Home::kHost;
+    // read-back ahead of the host: a buffer the host read after a call wrote
+    // it gets, after each later write, a copy queued into page-locked staging
+    // as the writing call returns, so the host's next access only waits for
+    // that copy; dropped after kReadbackMisses copies the host did not use
+    bool readback = false;
+    uint8_t* stage = nullptr;
+    hipEvent_t staged_ev = nullptr;
+    uint64_t writes = 0;      // calls that wrote the device copy
+    uint64_t staged = ~0ull;  // value of writes the staged copy holds
+    int misses = 0;
+    bool queued = false;      // in g_readbacks
 };
 std::map<uintptr_t, HostBuffer*> g_bufs;  // by block address
+std::vector<HostBuffer*> g_readbacks;     // written by the current call
+constexpr size_t kReadbackMax = size_t{1} << 20;
+constexpr int kReadbackMisses = 4;
 int g_lazy = -1;                           // -1: not read from the environment yet
 struct sigaction g_prev_segv;
 
@@ -593,7 +611,19 @@ void on_segv(int sig, siginfo_t* si, void* uc) {
         const uintptr_t hi = (reinterpret_cast<uintptr_t>(b->ptr) + b->bytes + pg - 1) & ~(pg - 1);
         if (a < lo || a >= hi) return;
         const char* where = "lazy host buffer access";
+        if (b->home == Home::kDevice && b->stage && b->staged == b->writes) {
+            // the copy queued when the last writer returned
+            if (check(hipEventSynchronize(b->staged_ev), where) && protect(*b, PROT_READ | PROT_WRITE)) {
+                std::memcpy(b->ptr, b->stage, b->bytes);
+                b->misses = 0;
+                b->staged = ~0ull;
+                b->home = protect(*b, PROT_READ) ? Home::kShared : Home::kHost;
+                handled = true;
+                return;
+            }
+        }
         if (b->home == Home::kDevice) {
+            if (b->bytes <= kReadbackMax) b->readback = true;
             if (!download(*b, where)) {
                 (void)protect(*b, PROT_READ | PROT_WRITE);  // the data is lost; keep the program running
                 b->home = Home::kHost;
@@ -627,6 +657,36 @@ void on_segv(int sig, siginfo_t* si, void* uc) {
         return;
     }
     g_prev_segv.sa_handler(sig);
+}
+
+void queue_readbacks() {
+    if (g_readbacks.empty()) return;
+    for (HostBuffer* b : g_readbacks) {
+        b->queued = false;
+        if (b->home != Home::kDevice || !b->readback) continue;
+        if (b->staged != ~0ull && ++b->misses >= kReadbackMisses) {  // the host left the last copy unread
+            b->readback = false;
+            continue;
+        }
+        const char* where = "lazy host buffer read-back";
+        if (!b->stage) {
+            void* p = nullptr;
+            if (hipHostMalloc(&p, b->bytes, hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                b->readback = false;
+                continue;
+            }
+            b->stage = static_cast<uint8_t*>(p);
+            if (!check(hipEventCreateWithFlags(&b->staged_ev, hipEventDisableTiming), where)) {
+                b->readback = false;
+                continue;
+            }
+        }
+        if (check(hipMemcpyAsync(b->stage, b->twin, b->bytes, hipMemcpyDeviceToHost, g_rt.stream), where) &&
+            check(hipEventRecord(b->staged_ev, g_rt.stream), where))
+            b->staged = b->writes;
+    }
+    g_readbacks.clear();
 }
 
 // [p, p + bytes) inside a lazy buffer: its address in the device copy, after
@@ -676,6 +736,13 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
             return nullptr;
         }
         b->home = Home::kDevice;
+    }
+    if (access & kWr) {
+        ++b->writes;
+        if (b->readback && !b->queued) {
+            b->queued = true;
+            g_readbacks.push_back(b);
+        }
     }
     return reinterpret_cast<T*>(b->twin + (a - lo));
 }
@@ -1205,9 +1272,9 @@ GNCX_API void gncx_fetch_token_embedding_bf16(const uint8_t* mmap_base, size_t t
                     "gncx_fetch_token_embedding_bf16");
 }
 
-// cpp:789-890.  The norm runs on the device; when out_tokens is given the
-// 4-phase telemetry encode (cpp:842-889) runs on the host over the normed
-// values, exactly as the reference forms it.
+// cpp:789-890.  The norm and, when out_tokens is given, the 4-phase
+// telemetry encode (cpp:842-889) run on the device; the tokens are the
+// reference's bit for bit (same rounding at every step).
 GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const uint8_t* mmap_base,
                                              size_t norm_weight_offset, int32_t dim, float eps, int32_t layer_k,
                                              float* out_normed_fp32, GNCXCompactToken* out_tokens,
@@ -1228,48 +1295,29 @@ GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const ui
     bool host = false;
     float* o = out_target(out_normed_fp32, dim, g_rt.o, host, where);
     if (!o) return;
-    if (!check(launch_rmsnorm(x, g, 1, dim, eps, o, g_rt.stream), where)) return;
-    if (!finish_out(out_normed_fp32, o, dim, host, where)) return;
     if (out_tokens == nullptr) {
+        if (!check(launch_rmsnorm(x, g, 1, dim, eps, o, g_rt.stream), where)) return;
+        if (!finish_out(out_normed_fp32, o, dim, host, where)) return;
         if (out_quant_scale) *out_quant_scale = 1.0f;
         return;
     }
-    std::vector<float> tmp;
-    const float* v = out_normed_fp32;
-    if (!host) {
-        tmp.resize(dim);
-        if (!check(hipMemcpy(tmp.data(), out_normed_fp32, sizeof(float) * dim, hipMemcpyDeviceToHost), where)) return;
-        v = tmp.data();
-    }
-    // repunit R_k = (10^(k+1)-1)/9 and diagonal anchors d*R_k (cpp:61-83)
-    constexpr int kMaxK = 17;
-    const int lay_k = std::clamp(layer_k, 0, kMaxK);
-    int64_t r_k = 1;
-    for (int i = 0; i < lay_k; ++i) r_k = r_k * 10 + 1;
-    float max_abs = 1e-9f;
-    for (int32_t j = 0; j < dim; ++j) max_abs = std::max(max_abs, std::fabs(v[j]));
-    const float target = static_cast<float>(9 * r_k);
-    const float to_int = target / max_abs;
-    if (out_quant_scale) *out_quant_scale = max_abs / target;
-    const float inv_rk = 1.0f / static_cast<float>(r_k);
-    const float half_rk = static_cast<float>(r_k >> 1);
-    std::array<uint32_t, 10> pos{}, neg{};
-    for (int32_t j = 0; j < dim; ++j) {
-        const int64_t val = static_cast<int64_t>(std::nearbyint(v[j] * to_int));
-        const int64_t av = val >= 0 ? val : -val;
-        int32_t da = static_cast<int32_t>((static_cast<float>(av) + half_rk) * inv_rk);
-        if (da > 9) da = 9;
-        const uint8_t d = static_cast<uint8_t>(da);
-        const int64_t anchor = static_cast<int64_t>(d) * r_k;
-        const int64_t sres = val - (val >= 0 ? anchor : -anchor);
-        const uint16_t ares = static_cast<uint16_t>(sres >= 0 ? sres : -sres);
-        const uint8_t b1 = val >= 0 ? 1u : 0u, b0 = sres >= 0 ? 1u : 0u;
-        out_tokens[j] = GNCXCompactToken{static_cast<uint8_t>((b1 << 1) | b0), d, ares};
-        pos[d] += b1;
-        neg[d] += b1 ^ 1u;
-    }
-    uint64_t c = 0;
-    for (int d = 0; d < 10; ++d) c += std::min(pos[d], neg[d]);
+    // the encode runs on the device in the norm's kernel and writes tokens,
+    // scale and cancellation count straight into a page-locked slot: one wait
+    const size_t tok_words = round_up(static_cast<size_t>(dim), 64);
+    PinnedSlot* sl = pinned_slot(sizeof(uint32_t) * (tok_words + 2), where);
+    if (!sl) return;
+    uint32_t* ht = static_cast<uint32_t*>(sl->p);
+    if (!check(launch_rmsnorm_encode(x, g, dim, eps, o, layer_k, ht, reinterpret_cast<float*>(ht + tok_words),
+                                     g_rt.stream),
+               where))
+        return;
+    if (!check(hipEventRecord(sl->ev, g_rt.stream), where)) return;
+    sl->pending = true;
+    if (host && !d2h(out_normed_fp32, o, sizeof(float) * dim, where)) return;
+    if (!sync_out(where)) return;
+    std::memcpy(out_tokens, ht, sizeof(uint32_t) * dim);
+    if (out_quant_scale) std::memcpy(out_quant_scale, ht + tok_words, sizeof(float));
+    const uint64_t c = ht[tok_words + 1];
     g_norm_epoch_cancellations = c;
     g_norm_epoch_tokens_ptr = out_tokens;
 }
@@ -2232,11 +2280,14 @@ GNCX_API void gncx_ram_free(void* ram_handle) {
     std::lock_guard<CallLock> lk(g_mu);
     forget_range(reinterpret_cast<uintptr_t>(h->ptr), reinterpret_cast<uintptr_t>(h->ptr) + h->bytes);
     g_bufs.erase(reinterpret_cast<uintptr_t>(h->block));
+    g_readbacks.erase(std::remove(g_readbacks.begin(), g_readbacks.end(), h), g_readbacks.end());
     if (h->twin) {
         // queued work may still use the device copy
         (void)hipStreamSynchronize(g_rt.stream);
         (void)hipFree(h->twin);
     }
+    if (h->staged_ev) (void)hipEventDestroy(h->staged_ev);
+    if (h->stage) (void)hipHostFree(h->stage);
     if (h->pinned) {
         // pending deferred write-backs never target freed memory: they are
         // flushed before the call that queued them returns

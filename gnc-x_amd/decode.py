@@ -249,7 +249,8 @@ class Decoder:
     caches mirrored by device twins, residual adds on the host."""
 
     def __init__(self, lib, torch, model: Model, max_seq: int, fused: bool = False, device: str = "cuda",
-                 native: bool = False, host: str = "torch", tokens: bool = False, layer_k: int = 3):
+                 native: bool = False, host: str = "torch", tokens: bool = False, layer_k: int = 3,
+                 driver: str = "python"):
         s = model.shape
         self.lib, self.torch, self.m, self.s, self.fused, self.native = lib, torch, model, s, fused, native
         if native and device != "cuda":
@@ -312,6 +313,9 @@ class Decoder:
         from . import GNCXCompactToken
         self.tokens = (GNCXCompactToken * max(s.embed, s.q_dim, s.ffn))() if tokens else None
         self.qscale = (C.c_float * 1)()
+        if driver not in ("python", "c"):
+            raise ValueError("driver is 'python' or 'c'")
+        self.driver, self._replay = driver, None
         self.max_seq = max_seq
         self.scale = 1.0 / (s.head_dim ** 0.5)
         self._qkv = self._gu = None  # gncx_hip_matvec_multi arguments, built on first fused use
@@ -439,6 +443,26 @@ class Decoder:
         return self.token_log[pos:pos + n].tolist()
 
     # -- lua/gncx_streamer.lua:759-965 ------------------------------------------
+    def _replay_token(self, token: int, pos: int):
+        """forward_token issued from native code (gnc-x_amd/bin/gncx_streamer_replay.so)."""
+        if self._replay is None:
+            from . import LIB_PATH, GNCXTelemetryStats
+            if self._native is None:
+                self._native_structs()
+            so = C.CDLL(str(LIB_PATH.parent / "gncx_streamer_replay.so"))
+            fn = so.gncx_replay_forward_token
+            fn.restype = C.c_int
+            fn.argtypes = [C.c_void_p] * 6 + [C.c_int32] * 4
+            self._replay = (so, fn, (C.c_int32 * self.s.n_layers)(*self.crivo), GNCXTelemetryStats())
+        _, fn, crivo, tel = self._replay
+        _, model, _, _, state = self._native
+        tk = C.addressof(self.tokens) if self.tokens is not None else None
+        rc = fn(C.addressof(model), C.addressof(state), tk, C.addressof(self.qscale), C.addressof(tel),
+                C.addressof(crivo), self.layer_k, int(token), int(pos), 1)
+        if rc != 0:
+            raise RuntimeError(self.lib.gncx_hip_last_error().decode())
+        return self.logits
+
     def forward_token(self, token: int, pos: int):
         s, L = self.s, self.lib
         if pos >= self.max_seq:
@@ -446,6 +470,8 @@ class Decoder:
         if self.native:
             self._step(token, pos, False)
             return self.logits
+        if self.driver == "c":
+            return self._replay_token(token, pos)
         h, nrm = self.hidden.data_ptr(), self.normed.data_ptr()
         q, k, v, a = self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.attn.data_ptr()
         pr, ga, up, ac = self.proj.data_ptr(), self.gate.data_ptr(), self.up.data_ptr(), self.act.data_ptr()

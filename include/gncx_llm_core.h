@@ -113,7 +113,7 @@ void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactToken* q_t
 void gncx_apply_rope_xor11(float* q_vec, float* k_vec, GNCXCompactToken* q_tokens, int32_t n_heads,
                            int32_t n_kv_heads, int32_t head_dim, int32_t pos, float freq_base);
 
-/* RMSNorm (device) + optional 4-phase telemetry encode (host).  Replaces
+/* RMSNorm + optional 4-phase telemetry encode, both on the device.  Replaces
  * cpp:789-890 (called at streamer.lua:793-803, 877-887, 939-949). */
 void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const uint8_t* mmap_base, size_t norm_weight_offset,
                                     int32_t dim, float eps, int32_t layer_k, float* out_normed_fp32,

@@ -552,6 +552,37 @@ void orc_swiglu(const float* gate, const float* up, int32_t n, float* out) {
     }
 }
 
+/* cpp:842-889: the 4-phase telemetry encode of v[dim].  Tokens are written
+ * as packed words phase | d << 8 | |residual| << 16 (the 4-byte
+ * GNCXCompactToken of cpp:267-271 read little-endian); returns the quant
+ * scale.  r_k is the repunit of k ones (cpp:61-83). */
+float orc_encode_4phase(const float* v, int32_t dim, int32_t layer_k, uint32_t* tokens) {
+    const int32_t k = layer_k < 0 ? 0 : (layer_k > 17 ? 17 : layer_k);
+    int64_t r_k = 1;
+    for (int32_t i = 0; i < k; ++i) r_k = r_k * 10 + 1;
+    float max_abs = 1e-9f;
+    for (int32_t j = 0; j < dim; ++j) {
+        const float a = fabsf(v[j]);
+        if (a > max_abs) max_abs = a;
+    }
+    const float target = (float)(9 * r_k);
+    const float to_int = target / max_abs;
+    const float inv_rk = 1.0f / (float)r_k;
+    const float half_rk = (float)(r_k >> 1);
+    for (int32_t j = 0; j < dim; ++j) {
+        const int64_t val = (int64_t)nearbyintf(v[j] * to_int);
+        const int64_t av = val >= 0 ? val : -val;
+        int32_t d = (int32_t)(((float)av + half_rk) * inv_rk);
+        if (d > 9) d = 9;
+        const int64_t anchor = (int64_t)d * r_k;
+        const int64_t res = val - (val >= 0 ? anchor : -anchor);
+        const uint32_t ares = (uint16_t)(res >= 0 ? res : -res);
+        const uint32_t phase = (val >= 0 ? 2u : 0u) | (res >= 0 ? 1u : 0u);
+        tokens[j] = phase | ((uint32_t)d << 8) | (ares << 16);
+    }
+    return max_abs / target;
+}
+
 /* cpp:2018-2033: tanh-approximated GELU of gate times up, with the
  * reference's constants and association. */
 void orc_geglu(const float* gate, const float* up, int32_t n, float* out) {

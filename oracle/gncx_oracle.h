@@ -66,6 +66,7 @@ void     orc_attention_step(const float* q, const float* k_new, const float* v_n
                             int32_t write_kv, float* out);
 void     orc_swiglu(const float* gate, const float* up, int32_t n, float* out);
 void     orc_geglu(const float* gate, const float* up, int32_t n, float* out);
+float    orc_encode_4phase(const float* v, int32_t dim, int32_t layer_k, uint32_t* tokens);
 void     orc_fetch_embedding(int32_t type, const uint8_t* table, int32_t token, int32_t dim,
                              float scale, float* out);
 

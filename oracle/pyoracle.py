@@ -59,6 +59,7 @@ class Oracle:
             "orc_attention_step": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
             "orc_swiglu": (None, [_vp, _vp, _i32, _vp]),
             "orc_geglu": (None, [_vp, _vp, _i32, _vp]),
+            "orc_encode_4phase": (_f32, [_vp, _i32, _i32, _vp]),
             "orc_fetch_embedding": (None, [_i32, _vp, _i32, _i32, _f32, _vp]),
         }
         for name, (res, args) in sig.items():
@@ -107,6 +108,13 @@ class Oracle:
         out = np.empty_like(x)
         self.lib.orc_rmsnorm(_ptr(x), _ptr(np.ascontiguousarray(gamma, dtype=np.float32)), x.size, eps, _ptr(out))
         return out
+
+    def encode(self, v, layer_k):
+        """(tokens as packed uint32 words, quant scale) of the 4-phase encode."""
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        tok = np.zeros(v.size, dtype=np.uint32)
+        qs = self.lib.orc_encode_4phase(_ptr(v), v.size, layer_k, _ptr(tok))
+        return tok, np.float32(qs)
 
     def rmsnorm_heads(self, v, gamma, n_heads, head_dim, eps):
         v = np.array(v, dtype=np.float32, copy=True)
@@ -261,6 +269,17 @@ class Reference:
         g = np.ascontiguousarray(gamma, dtype=np.float32)
         self.lib.gncx_rmsnorm_and_encode_4phase(_ptr(x), _ptr(g), 0, x.size, eps, 0, _ptr(out), None, None)
         return out
+
+    def rmsnorm_encode(self, x, gamma, eps, layer_k):
+        """(normed, tokens as packed uint32 words, quant scale)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty_like(x)
+        tok = np.zeros(x.size, dtype=np.uint32)
+        qs = np.zeros(1, dtype=np.float32)
+        g = np.ascontiguousarray(gamma, dtype=np.float32)
+        self.lib.gncx_rmsnorm_and_encode_4phase(_ptr(x), _ptr(g), 0, x.size, eps, layer_k, _ptr(out), _ptr(tok),
+                                                _ptr(qs))
+        return out, tok, qs[0]
 
     def swiglu(self, g, u):
         g = np.ascontiguousarray(g, dtype=np.float32)

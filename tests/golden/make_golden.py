@@ -117,6 +117,12 @@ def main() -> None:
     ux = rng.standard_normal(2048).astype(np.float32)
     data["swi_g"], data["swi_u"], data["swi_y"] = gx, ux, ref.swiglu(gx, ux)
 
+    # the 4-phase encode of the normed vector at several sieve orders
+    for lk in (0, 2, 3, 9, 17):
+        yk, tk, qk = ref.rmsnorm_encode(hx, hg, 1e-6, lk)
+        assert np.array_equal(yk, data["rms_y"])
+        data[f"enc_tok_k{lk}"], data[f"enc_qs_k{lk}"] = tk, np.float32(qk)
+
     # GeGLU over the tanh range and its saturation, with an odd tail
     gg = np.concatenate([np.linspace(-12, 12, 2001), rng.standard_normal(50) * 3]).astype(np.float32)
     gg[7] = 0.0

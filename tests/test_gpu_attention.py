@@ -6,6 +6,8 @@ reference call sequence, and the per-head RMSNorm / RoPE / SwiGLU / RMSNorm /
 embedding companions."""
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -258,6 +260,22 @@ def test_rmsnorm_swiglu_embeddings(lib, golden, oracle):
         assert np.array_equal(e, golden[f"emb_{name}_y5"])
         fn(ptr(tab), 0, 11, 512, 0.37, ptr(e))
         assert np.array_equal(e, golden[f"emb_{name}_y11s"])
+
+
+@pytest.mark.parametrize("lk", [0, 2, 3, 9, 17])
+def test_rmsnorm_encode_tokens_bitexact(lib, golden, lk):
+    """The 4-phase encode runs on the device: its tokens and quant scale equal
+    the reference's bit for bit, for host and for device outputs."""
+    x, g = golden["rms_x"].copy(), golden["rms_g"].copy()
+    out = np.zeros_like(x)
+    tok = (gncx.GNCXCompactToken * x.size)()
+    qs = np.zeros(1, np.float32)
+    lib.gncx_rmsnorm_and_encode_4phase(ptr(x), ptr(g), 0, x.size, 1e-6, lk, ptr(out), C.addressof(tok), ptr(qs))
+    gncx.check(lib)
+    got = np.frombuffer(bytes(tok), dtype=np.uint32)
+    assert np.array_equal(got, golden[f"enc_tok_k{lk}"])
+    assert qs[0] == golden[f"enc_qs_k{lk}"]
+    assert rel_l2(out, golden["rms_y"]) < 1e-6
 
 
 PREFILL_CASES = [

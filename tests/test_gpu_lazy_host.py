@@ -137,17 +137,18 @@ def test_lazy_copy_chunk_and_free_of_device_held_buffers(lib, oracle, lazy):
 
 def test_lazy_decode_equals_synchronous_host_buffers(lib, torch_mod, tmp_path):
     """The streamer's decode through buffers from gncx_ram_alloc_colored and
-    the 4-phase token array, with lazy coherence and without: identical
-    logits, token arrays and KV caches."""
+    the 4-phase token array, with lazy coherence and without, issued from
+    Python and from the native replay of forward_token: identical logits,
+    token arrays and KV caches."""
     import gncx_amd.decode as dec
     from test_gpu_decode import small_shape
     dec.write_model_gguf(tmp_path / "m.gguf", small_shape(), seed=34)
     m = dec.load_model_gguf(tmp_path / "m.gguf")
     runs = []
     try:
-        for lazy_mode in (0, 1):
+        for lazy_mode, driver in ((0, "python"), (1, "python"), (0, "c"), (1, "c")):
             lib.gncx_hip_set_host_coherence(lazy_mode)
-            d = dec.Decoder(lib, torch_mod, m, max_seq=16, device="cpu", host="ram", tokens=True)
+            d = dec.Decoder(lib, torch_mod, m, max_seq=16, device="cpu", host="ram", tokens=True, driver=driver)
             try:
                 tok, logits, toks = 11, [], []
                 for pos in range(6):
@@ -162,12 +163,13 @@ def test_lazy_decode_equals_synchronous_host_buffers(lib, torch_mod, tmp_path):
             finally:
                 lib.gncx_hip_set_host_coherence(0)
                 d.close()
-        (la, ta, ka, va), (lb, tb, kb, vb) = runs
-        for i in range(len(la)):
-            assert np.array_equal(la[i], lb[i]), i
-            assert ta[i] == tb[i], i
-        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+        la, ta, ka, va = runs[0]
         assert np.abs(ka).sum() > 0
+        for r, (lb, tb, kb, vb) in enumerate(runs[1:], 1):
+            for i in range(len(la)):
+                assert np.array_equal(la[i], lb[i]), (r, i)
+                assert ta[i] == tb[i], (r, i)
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), r
     finally:
         lib.gncx_hip_set_host_coherence(0)
         lib.gncx_hip_weight_forget(None)

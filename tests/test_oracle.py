@@ -368,6 +368,31 @@ def test_geglu(oracle, golden):
     assert rel_l2(y, want) < 1e-6
 
 
+@pytest.mark.parametrize("lk", [0, 2, 3, 9, 17])
+def test_encode_4phase(oracle, golden, lk):
+    """Tokens and quant scale bit-exact with the reference's encode of the
+    same normed vector; the tokens reconstruct the rounded integers
+    sign * d R_k + residual (|residual| below 2^16 here) and, at k = 0
+    (R_k = 1), d is the integer itself with no residual."""
+    v = golden["rms_y"]
+    tok, qs = oracle.encode(v, lk)
+    assert np.array_equal(tok, golden[f"enc_tok_k{lk}"])
+    assert qs == golden[f"enc_qs_k{lk}"]
+    phase, d, ares = tok & 0xFF, (tok >> 8) & 0xFF, (tok >> 16).astype(np.int64)
+    r_k = int("1" * (lk + 1))
+    sign = np.where(phase >> 1, 1, -1)
+    rsign = np.where(phase & 1, 1, -1)
+    val = sign * d.astype(np.int64) * r_k + rsign * ares
+    target = np.float32(9 * r_k)
+    to_int = target / np.float32(np.abs(v).max())
+    want = np.rint((v * to_int).astype(np.float32)).astype(np.int64)
+    if lk <= 3:
+        assert np.array_equal(val, want)
+    if lk == 0:
+        assert np.array_equal(d.astype(np.int64), np.abs(want)) and np.all(ares == 0)
+    assert np.all(d <= 9)
+
+
 def test_oracle_against_live_reference(oracle, ref):
     """Where the reference library is built (this container), compare on a
     fresh seed as well."""
