@@ -237,8 +237,9 @@ struct WRaw<kQ6_K> {
     }
 };
 
-// Y tile of (64 WM) tokens x (64 WN) rows per work-group of 4 waves (2 x 2);
-// each wave owns WM x WN 32x32 accumulator tiles.  K advances 64 per step
+// Y tile of (32 WM MW) tokens x (64 WN) rows per work-group of 2 MW waves
+// (MW along the tokens, 2 along the rows); each wave owns WM x WN 32x32
+// accumulator tiles.  K advances 64 per step
 // through two LDS buffers: token rows [tokens][64 + 8 pad] fp16 and weight
 // rows [rows][64 + 8 pad] fp16.  In step s the MFMAs consume LDS buffer
 // s % 2 while the loads for later steps are in flight, then step s + 1's
@@ -256,18 +257,21 @@ constexpr int kMfKs = 64;
 constexpr int kMfLd = kMfKs + 8;  // halves per LDS row (16-byte aligned, staggers banks)
 constexpr int32_t kMfOob = 0x7ffffff0;  // a buffer offset past any resource
 
-template <int TYPE, int WM, int WN>
-__global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __restrict w, size_t rbytes,
+template <int TYPE, int WM, int WN, int MW = 2>
+__global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kernel(const uint8_t* __restrict w,
+                                                                                   size_t rbytes,
                                                             const _Float16* __restrict xh,
                                                             const float* __restrict rscale, int32_t b, int32_t k,
                                                             int32_t n, float* __restrict y, int32_t kchunk,
                                                             float* __restrict part) {
-    constexpr int BM = 64 * WM, BN = 64 * WN;
-    constexpr int XCH = BM * 8 / 256;  // 16-byte activation chunks per thread and step
+    constexpr int THREADS = 128 * MW;
+    constexpr int BM = 32 * WM * MW, BN = 64 * WN;
+    static_assert(2 * BN <= THREADS, "one thread per 32-value weight segment of a step");
+    constexpr int XCH = BM * 8 / THREADS;  // 16-byte activation chunks per thread and step
     __shared__ __align__(16) _Float16 xs[2][BM * kMfLd];
     __shared__ __align__(16) _Float16 ws[2][BN * kMfLd];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv & 1, wn = wv >> 1;
+    const int wm = wv % MW, wn = wv / MW;
     const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int32_t kb = blockIdx.z * kchunk;
     const int32_t ke = min(k, kb + kchunk);
@@ -281,7 +285,7 @@ __global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // activation chunks c = tid + 256 i: token row c / 8 of the tile, halves
+    // activation chunks c = tid + THREADS i: token row c / 8 of the tile, halves
     // 8 (c % 8) .. + 8 of the step; one resource over the tile's token rows
     const int32_t rows_here = min(BM, b - t0);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -304,7 +308,7 @@ __global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __
     auto gload_x = [&](int32_t k0) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + 256 * i, r = c >> 3, seg = c & 7;
+            const int c = tid + THREADS * i, r = c >> 3, seg = c & 7;
             const int32_t kx = k0 + 8 * seg;
             const int32_t off = kx < ke ? (r * k + kx) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void matbatch_mfma_kernel(const uint8_t* __
     auto lstore = [&](int set, int buf, int32_t k0) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + 256 * i, r = c >> 3, seg = c & 7;
+            const int c = tid + THREADS * i, r = c >> 3, seg = c & 7;
             *reinterpret_cast<uint4*>(&xs[buf][r * kMfLd + 8 * seg]) = xr[i];
         }
         if (tid < 2 * BN) {
@@ -405,18 +409,28 @@ __global__ __launch_bounds__(kThreads) void matbatch_reduce_kernel(const float* 
 struct MfmaPlan {
     int wm, wn;
     int32_t splits, kchunk;
+    int mw = 2;  // waves along the tokens (4: 512-thread work-groups)
 };
 
-// Largest tile whose grid fills every CU with as many work-groups as its LDS
-// lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for 64 x 64); otherwise
-// 64 x 64 tiles with K split until it does (ranges of at least 256).
-// (A 256 x 128 tile, 478 registers per lane and 110 KB of LDS, is not used:
-// its one launch ended the host process with a segmentation fault whose cause
-// was not found.)
+// From 256 tokens, 256-token tiles of 8 waves (one work-group per CU, 111 KB
+// of LDS): 256 x 128 when that gives at least 192 tiles, else 256 x 64 when
+// that does (with fewer, split K on 64 x 64 tiles measured faster).  Twice the tokens per dequantised weight step, with the
+// dequantising waves and MFMA-only waves sharing each SIMD, measured 1.1-1.4x
+// the 128 x 128 tile (Q4_K 4096 x 14336 at B = 512: 111 vs 141 us; 4096 x 4096
+// at B = 2048: 116 vs 149 us) and bit-identical results (same K order).
+// Otherwise the largest tile whose grid fills every CU with as many
+// work-groups as its LDS lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for
+// 64 x 64), else 64 x 64 tiles with K split until it does (ranges of at
+// least 256).
 MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
     auto tiles = [&](int wm, int wn) {
         return static_cast<int64_t>((n + 64 * wn - 1) / (64 * wn)) * ((b + 64 * wm - 1) / (64 * wm));
     };
+    if (b >= 256) {
+        const int64_t mt = (b + 255) / 256;
+        if (static_cast<int64_t>((n + 127) / 128) * mt >= 192) return {2, 2, 1, k, 4};
+        if (static_cast<int64_t>((n + 63) / 64) * mt >= 192) return {2, 1, 1, k, 4};
+    }
     const int cand[3][3] = {{2, 2, 2}, {2, 1, 2}, {1, 1, 4}};
     for (const auto& c : cand)
         if (tiles(c[0], c[1]) >= 256 * c[2]) return {c[0], c[1], 1, k};
@@ -430,12 +444,13 @@ MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
     return {1, 1, splits, kchunk};
 }
 
-template <int TYPE, int WM, int WN>
+template <int TYPE, int WM, int WN, int MW = 2>
 hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xh, const float* rscale, int32_t b, int32_t k,
                          int32_t n, float* y, const MfmaPlan& p, float* part, hipStream_t stream) {
-    const dim3 grid((n + 64 * WN - 1) / (64 * WN), (b + 64 * WM - 1) / (64 * WM), p.splits);
-    hipLaunchKernelGGL((matbatch_mfma_kernel<TYPE, WM, WN>), grid, dim3(256), 0, stream, w, row_bytes(TYPE, k), xh,
-                       rscale, b, k, n, y, p.kchunk, part);
+    constexpr int BM = 32 * WM * MW;
+    const dim3 grid((n + 64 * WN - 1) / (64 * WN), (b + BM - 1) / BM, p.splits);
+    hipLaunchKernelGGL((matbatch_mfma_kernel<TYPE, WM, WN, MW>), grid, dim3(128 * MW), 0, stream, w,
+                       row_bytes(TYPE, k), xh, rscale, b, k, n, y, p.kchunk, part);
     return hipGetLastError();
 }
 
@@ -446,7 +461,9 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
-    if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, rscale, b, k, n, y, p, part, stream);
+    if (p.mw == 4 && p.wn == 2) e = launch_mfma_t<TYPE, 2, 2, 4>(w, xh, rscale, b, k, n, y, p, part, stream);
+    else if (p.mw == 4) e = launch_mfma_t<TYPE, 2, 1, 4>(w, xh, rscale, b, k, n, y, p, part, stream);
+    else if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, rscale, b, k, n, y, p, part, stream);
     else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
     else e = launch_mfma_t<TYPE, 1, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;

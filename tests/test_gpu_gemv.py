@@ -205,6 +205,8 @@ MATBATCH_CASES = [
         reason="ran the 256x128 MFMA tile, whose one launch ended the process with a host segmentation fault; "
                "that tile is switched off and this case stays off the GPU until the cause is found")),
     (Q4_K, 256, 8192, 500), (Q6_K, 256, 16384, 128), (Q4_K, 256, 16384, 512), (Q6_K, 512, 8192, 520),
+    # the 256-token tiles of 8 waves (256 x 128 and 256 x 64), ragged B and N
+    (Q6_K, 256, 24576, 260), (Q4_K, 256, 8192, 300), (Q8_0, 512, 6000, 257),
 ]
 
 
