@@ -600,13 +600,15 @@ bool try_band_ext_type(int32_t type, const BandMats& m, const float* x, int32_t 
     }
 }
 
-// ONE for 16-wave groups with at least kOneMinRowWaves row-waves, TWO otherwise
+// ONE for 16-wave groups with at least kOneMinRowWaves row-waves, and for
+// Q4_K / Q8_0 rows split into three or more K-slices (Q4_K 12288 x 4096:
+// 8.2 vs 8.8 us under TWO; Q8_0 14336 x 4096: 14.3 vs 15.5 us); TWO otherwise
 template <int TYPE, int THREADS>
 bool try_band(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream) {
     const int32_t nwk = (Slot<TYPE>::slots(k) + 63) / 64;
-    if (THREADS == 1024 && nwk >= 1 && (THREADS / 64) / nwk >= kOneMinRowWaves &&
-        try_band_sched<TYPE, THREADS, kSchedOne>(m, x, k, n, stream))
-        return true;
+    const bool one = nwk >= 1 && ((THREADS / 64) / nwk >= kOneMinRowWaves ||
+                                  (nwk >= 3 && (TYPE == kQ4_K || TYPE == kQ8_0)));
+    if (THREADS == 1024 && one && try_band_sched<TYPE, THREADS, kSchedOne>(m, x, k, n, stream)) return true;
     return try_band_sched<TYPE, THREADS, kSchedTwo>(m, x, k, n, stream);
 }
 
@@ -615,7 +617,10 @@ template <int TYPE>
 hipError_t launch_band(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream, bool& used) {
     const int32_t groups = n < kBandGroups ? n : kBandGroups;
     const size_t per_group = row_bytes(TYPE, k) * static_cast<size_t>(n) / static_cast<size_t>(groups);
-    used = (per_group > kBandStreamBytes && try_band<TYPE, kBandThreadsStream>(m, x, k, n, stream)) ||
+    // Q6_K rows of three or more K-slices also stream best with 8 waves
+    // (14336 x 4096: 13.5 vs 14.3 us; 12288 x 4096: 11.9 vs 12.8 us)
+    const bool q6_long = TYPE == kQ6_K && (Slot<TYPE>::slots(k) + 63) / 64 >= 3;
+    used = ((per_group > kBandStreamBytes || q6_long) && try_band<TYPE, kBandThreadsStream>(m, x, k, n, stream)) ||
            try_band<TYPE, kBandThreads>(m, x, k, n, stream);
     return used ? hipGetLastError() : hipSuccess;
 }

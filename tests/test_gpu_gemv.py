@@ -71,6 +71,8 @@ MATVEC_CASES = [
     (Q4_0, 4096, 4096), (Q4_K, 4096, 14336), (Q6_K, 14336, 4096), (Q8_0, 4096, 4096), (Q4_K, 4096, 4096),
     (Q4_K, 12288, 4096), (Q6_K, 4096, 2048), (Q4_0, 1024, 333), (Q8_0, 96, 7), (Q4_K, 256, 1),
     (Q6_K, 512, 65), (BF16, 4096, 512),
+    # rows split into 3 to 7 K-slices under each schedule, ragged row counts
+    (Q8_0, 14336, 4099), (Q4_K, 14336, 1000), (Q6_K, 12288, 777), (Q4_K, 12288, 12288),
 ]
 
 
