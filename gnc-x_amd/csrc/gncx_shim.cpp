@@ -130,6 +130,10 @@ struct DevWeight {
     uint8_t* d = nullptr;
     size_t bytes = 0;
     uint64_t sig = 0;
+    // inside a mapping from gncx_gla_map_readonly or a buffer from
+    // gncx_ram_alloc*: unmapping, freeing or copying into it drops this copy,
+    // so a hit needs neither the pointer query nor the content signature
+    bool tracked = false;
 };
 
 struct KVTwin {
@@ -196,12 +200,14 @@ void forget_weight(uintptr_t key) {
     g_rt.weights.erase(it);
 }
 
+bool tracked_host_range(const void* p, size_t bytes);
+
 // Device view of `bytes` weight bytes at p (host: uploaded once, cached).
 const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where) {
-    if (is_device_ptr(p)) return p;
     const uintptr_t key = reinterpret_cast<uintptr_t>(p);
-    const uint64_t sig = host_signature(p, bytes);
     auto it = g_rt.weights.find(key);
+    if (it != g_rt.weights.end() && it->second.tracked && it->second.bytes >= bytes) return it->second.d;
+    if (is_device_ptr(p)) return p;
     if (it != g_rt.weights.end()) {
         if (it->second.bytes >= bytes && it->second.sig == host_signature(p, it->second.bytes))
             return it->second.d;
@@ -209,7 +215,8 @@ const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where)
     }
     DevWeight w;
     w.bytes = bytes;
-    w.sig = sig;
+    w.sig = host_signature(p, bytes);
+    w.tracked = tracked_host_range(p, bytes);
     void* d = nullptr;
     // 256 B aligned, plus slack so no vector load near the end leaves the allocation
     if (!check(hipMalloc(&d, round_up(bytes, 256) + 256), where)) return nullptr;
@@ -542,6 +549,20 @@ HostBuffer* buffer_at(uintptr_t a) {
     --it;
     HostBuffer* b = it->second;
     return a < it->first + b->block_bytes ? b : nullptr;
+}
+
+// mappings from gncx_gla_map_readonly: base -> bytes
+std::map<uintptr_t, size_t> g_maps;
+
+bool tracked_host_range(const void* p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = g_maps.upper_bound(a);
+    if (it != g_maps.begin()) {
+        --it;
+        if (a + bytes <= it->first + it->second) return true;
+    }
+    const HostBuffer* b = buffer_at(a);
+    return b && a >= reinterpret_cast<uintptr_t>(b->ptr) && a + bytes <= reinterpret_cast<uintptr_t>(b->ptr) + b->bytes;
 }
 
 size_t page_bytes() {
@@ -2179,6 +2200,10 @@ GNCX_API void* gncx_gla_map_readonly(const char* filepath, size_t* out_size) {
     (void)posix_fadvise(fd, 0, static_cast<off_t>(bytes), POSIX_FADV_WILLNEED);
     (void)madvise(p, bytes, MADV_WILLNEED);
     auto* h = new MappedFile{fd, static_cast<const uint8_t*>(p), bytes};
+    {
+        std::lock_guard<CallLock> lk(g_mu);
+        g_maps[reinterpret_cast<uintptr_t>(p)] = bytes;
+    }
     if (out_size) *out_size = bytes;
     return h;
 }
@@ -2195,6 +2220,7 @@ GNCX_API void gncx_gla_unmap(void* opaque_handle) {
     {
         std::lock_guard<CallLock> lk(g_mu);
         forget_range(reinterpret_cast<uintptr_t>(h->base), reinterpret_cast<uintptr_t>(h->base) + h->bytes);
+        g_maps.erase(reinterpret_cast<uintptr_t>(h->base));
     }
     munmap(const_cast<uint8_t*>(h->base), h->bytes);
     close(h->fd);
