@@ -161,3 +161,24 @@ def test_decode_structs_match_header(tmp_path):
         assert C.sizeof(py[s]) == got[(s, "sizeof")], s
         for f in fs:
             assert getattr(py[s], f).offset == got[(s, f)], (s, f)
+
+
+def test_streamer_replay_library_links_against_the_core(built):
+    """gncx_streamer_replay.so (the native caller used to time the unchanged
+    streamer's call sequence) loads, resolves its calls in this very core
+    library, and exports its one entry point."""
+    replay = gncx.LIB_PATH.parent / "gncx_streamer_replay.so"
+    assert replay.exists()
+    lib = gncx.load()
+    so = C.CDLL(str(replay))
+    assert so.gncx_replay_forward_token is not None
+    out = subprocess.run(["readelf", "-d", str(replay)], capture_output=True, text=True, check=True).stdout
+    assert "gncx_llm_core.so" in out
+    # its NEEDED entry binds to the core by SONAME (the reference build, loaded
+    # by path in the same process, has none), so the library state is shared
+    core = subprocess.run(["readelf", "-d", str(gncx.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    assert "Library soname: [gncx_llm_core.so]" in core
+    maps = pathlib.Path(f"/proc/{__import__('os').getpid()}/maps").read_text()
+    ours = {ln.split()[-1] for ln in maps.splitlines() if ln.endswith("gnc-x_amd/bin/gncx_llm_core.so")}
+    assert len(ours) == 1, ours
+    assert lib.gncx_hip_last_status is not None
