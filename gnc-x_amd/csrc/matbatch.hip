@@ -5,19 +5,21 @@
 // on its own to per-32 int8 blocks (cpp:1506-1510), then each output is the
 // same integer block dot as the matvec; the output is row-major out[t*N + m].
 //
-// Quantised weights (Q4_0, Q8_0, Q4_K, Q6_K) go through the matrix cores:
-//   1. act_f16_kernel quantises each token row exactly as the reference does
-//      and stores the quantised activations q * d / s as fp16 [B x K] (one
-//      rounding of an exactly quantised value; s is a power-of-two row scale
-//      the MFMA epilogue multiplies back),
-//   2. matbatch_mfma_kernel streams 64-wide K steps: the work-group's weight
-//      rows are dequantised block by block (fp32 arithmetic, one fp16
-//      rounding) into LDS, its token rows are copied into LDS, and each wave
-//      runs v_mfma_f32_32x32x16_f16 tiles with fp32 accumulation.
-// fp16 rounding of both operands keeps Y within about 3e-4 relative L2 of the
-// reference's integer block dots (measured on the CPU for all four formats);
-// the per-32-block scales make an exact int8 MFMA path pay ~3 VALU operations
-// per output and block, several times the matrix-core time.
+// Quantised weights (Q4_0, Q8_0, Q4_K, Q6_K) go through the fp16 matrix
+// cores with both operands carried as fp16 pairs (hi, lo):
+//   1. act_hilo_kernel quantises each token row exactly as the reference
+//      does and stores each quantised activation q * d / s as an fp16 pair
+//      (s is a power-of-two row scale the MFMA epilogue multiplies back),
+//   2. matbatch_mfma_kernel streams 32-wide K steps: the work-group's weight
+//      rows are dequantised block by block in fp32 and split into fp16 pairs
+//      in LDS, its token rows are copied into LDS, and each wave runs three
+//      v_mfma_f32_32x32x16_f16 per tile and K slice (hi x hi, lo x hi,
+//      hi x lo) with fp32 accumulation.
+// Each product is then exact to about 2^-22, and Y lands within about 2e-7
+// relative L2 of the reference's integer block dots (fp16 operands alone:
+// 3e-4).  An int8 MFMA path would be exact too, but its per-32-block scales
+// cost ~3 VALU operations per output and block, several times the
+// matrix-core time of the three fp16 products.
 // BF16 weights (fp32 activations, cpp:1432-1461) use the slot-dot kernel: a
 // wave per (row, token).
 #include <hip/hip_runtime.h>
@@ -63,21 +65,29 @@ __global__ __launch_bounds__(kThreads) void matbatch_rowtok_kernel(const uint8_t
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
-    const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
-    const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
-    return lo | (hi << 16);
+// fp16 pair (hi, lo) of a float: hi = fp16(v) and lo = fp16(v - hi), with
+// v - hi exact in fp32, so hi + lo carries 22 significant bits of v.
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
+    const _Float16 la = static_cast<_Float16>(a - static_cast<float>(ha));
+    const _Float16 lb = static_cast<_Float16>(b - static_cast<float>(hb));
+    hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+    lo = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, la)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lb)) << 16);
 }
 
-// fp16(q * d / s) of the reference's per-32 quantisation of row blockIdx.x of
-// x (cpp:955-995), with s the power of two at or above the row's largest |x|
-// (stored in rscale; the MFMA epilogue multiplies by it again).  The exact
-// rescale puts every value in [-1, 1], so activations far beyond fp16's range
-// (SwiGLU outputs of 1e5 and more) keep fp16's relative precision.  One
-// work-group per row: the row maximum first, then 8 lanes per 32-block,
+// The reference's per-32 quantisation of row blockIdx.x of x (cpp:955-995),
+// each quantised value a = q * d (one fp32 rounding) scaled by 1 / s, where
+// s is the power of two above the row's largest |x| (stored in rscale; the
+// MFMA epilogue multiplies it back, exactly), and stored as its fp16 pair
+// (hi, lo): xhl holds, per 8 elements, 16 bytes of hi then 16 bytes of lo.
+// The rescale keeps every value in [-1, 1], so activations far beyond fp16's
+// range (SwiGLU outputs of 1e5 and more) keep the pair's relative precision.
+// One work-group per row: the row maximum first, then 8 lanes per 32-block,
 // 4 values per lane.
-__global__ __launch_bounds__(kThreads) void act_f16_kernel(const float* __restrict x, int32_t k,
-                                                           uint2* __restrict xh, float* __restrict rscale) {
+__global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
+                                                            uint2* __restrict xhl, float* __restrict rscale) {
     __shared__ float red[kThreads / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
@@ -96,28 +106,37 @@ __global__ __launch_bounds__(kThreads) void act_f16_kernel(const float* __restri
     const float sc = m > 0.0f && m <= 3.0e38f ? ldexpf(1.0f, ilogbf(m) + 1) : 1.0f;  // power of two > m
     const float inv = 1.0f / sc;                                       // exact
     if (threadIdx.x == 0) rscale[row] = sc;
-    uint2* out = xh + static_cast<size_t>(row) * tasks;
+    uint2* out = xhl + static_cast<size_t>(row) * tasks * 2;
     // whole 8-lane groups take the same trip count (tasks and kThreads are multiples of 8)
     for (int32_t t = threadIdx.x; t < tasks; t += kThreads) {
         int q0, q1, q2, q3;
         float d;
         quantize_values(xr[t], q0, q1, q2, q3, d);
-        out[t] = make_uint2(pack_half2(static_cast<float>(q0) * d * inv, static_cast<float>(q1) * d * inv),
-                            pack_half2(static_cast<float>(q2) * d * inv, static_cast<float>(q3) * d * inv));
+        uint2 hi, lo;
+        split2((static_cast<float>(q0) * d) * inv, (static_cast<float>(q1) * d) * inv, hi.x, lo.x);
+        split2((static_cast<float>(q2) * d) * inv, (static_cast<float>(q3) * d) * inv, hi.y, lo.y);
+        // task t is elements 4t .. 4t + 3: chunk t / 2 of 8, half t % 2
+        uint2* c = out + 4 * (t >> 1) + (t & 1);
+        c[0] = hi;
+        c[2] = lo;
     }
 }
 
-// Weights e0 .. e0 + 31 (e0 a multiple of 32) of one row: raw block bytes
-// loaded into registers (WRaw::load, issued two K steps ahead of their use),
-// then dequantised in fp32 and rounded once to fp16 pairs (WRaw::get); an
-// all-zero block (what an empty BufRow reads) dequantises to zeros.  Formulas:
-// Q4_0 d (q - 8) (cpp:1023-1030), Q8_0 d q, Q4_K (d sc) q - dmin m
-// (cpp:1135-1178), Q6_K (d sc) q (cpp:742-757).
+// Weights e0 .. e0 + 15 (e0 a multiple of 16) of one row: raw block bytes
+// loaded into registers (WSeg::load, issued two K steps ahead of their use),
+// then dequantised in fp32 (WSeg::get) and split into fp16 pairs on their way
+// into LDS; an all-zero block (what a past-the-end buffer load reads)
+// dequantises to zeros.  Formulas: Q4_0 d (q - 8), elements j and j + 16 in
+// the low and high nibbles of byte j (cpp:1023-1030); Q8_0 d q; Q4_K
+// (d sc) q - dmin m with sub-block j of chunk c in the low (j even) or high
+// nibbles of bytes 32c .. 32c + 31 (cpp:1135-1178); Q6_K (d sc) (q - 32) with
+// element l + 32 g of a 128-half from ql[l + 32 (g & 1)] (nibble g / 2),
+// qh[l] >> 2g and scale l / 16 + 2g (cpp:742-757).
 template <int TYPE>
-struct WRaw;
+struct WSeg;
 
 template <>
-struct WRaw<kQ4_0> {
+struct WSeg<kQ4_0> {
     uint32_t d, sh;
     Raw16 qs;
     template <class Row>
@@ -127,149 +146,137 @@ struct WRaw<kQ4_0> {
         sh = r.sh(blk + 2u);
         raw16_load(qs, r, blk + 2u, sh);
     }
-    __device__ __forceinline__ void get(int32_t, uint32_t (&o)[16]) const {
+    __device__ __forceinline__ void get(int32_t e0, float (&v)[16]) const {
         const float dv = half_bits_to_float(d);
         const uint4 q = raw16_get(qs, sh);
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        const int s = 4 * ((e0 >> 4) & 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = w[i] & 0x0f0f0f0fu, hi = (w[i] >> 4) & 0x0f0f0f0fu;
-            o[2 * i] = pack_half2(dv * static_cast<float>(static_cast<int>(lo & 15u) - 8),
-                                  dv * static_cast<float>(static_cast<int>((lo >> 8) & 15u) - 8));
-            o[2 * i + 1] = pack_half2(dv * static_cast<float>(static_cast<int>((lo >> 16) & 15u) - 8),
-                                      dv * static_cast<float>(static_cast<int>(lo >> 24) - 8));
-            o[8 + 2 * i] = pack_half2(dv * static_cast<float>(static_cast<int>(hi & 15u) - 8),
-                                      dv * static_cast<float>(static_cast<int>((hi >> 8) & 15u) - 8));
-            o[8 + 2 * i + 1] = pack_half2(dv * static_cast<float>(static_cast<int>((hi >> 16) & 15u) - 8),
-                                          dv * static_cast<float>(static_cast<int>(hi >> 24) - 8));
-        }
+        for (int i = 0; i < 16; ++i)
+            v[i] = dv * static_cast<float>(static_cast<int>((w[i >> 2] >> (s + 8 * (i & 3))) & 15u) - 8);
     }
 };
 
 template <>
-struct WRaw<kQ8_0> {
+struct WSeg<kQ8_0> {
     uint32_t d, sh;
-    Raw16 lo, hi;
+    Raw16 qs;
     template <class Row>
     __device__ __forceinline__ void load(const Row& r, int32_t e0) {
         const uint32_t blk = static_cast<uint32_t>(e0 / 32) * 34u;
         d = r.ldu16(blk);
-        sh = r.sh(blk + 2u);
-        raw16_load(lo, r, blk + 2u, sh);
-        raw16_load(hi, r, blk + 18u, sh);
+        const uint32_t o = blk + 2u + 16u * static_cast<uint32_t>((e0 >> 4) & 1);
+        sh = r.sh(o);
+        raw16_load(qs, r, o, sh);
     }
-    __device__ __forceinline__ void get(int32_t, uint32_t (&o)[16]) const {
+    __device__ __forceinline__ void get(int32_t, float (&v)[16]) const {
         const float dv = half_bits_to_float(d);
-        const uint4 a = raw16_get(lo, sh), b = raw16_get(hi, sh);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint4 q = raw16_get(qs, sh);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int v0 = static_cast<int8_t>(w[i] & 0xffu), v1 = static_cast<int8_t>((w[i] >> 8) & 0xffu);
-            const int v2 = static_cast<int8_t>((w[i] >> 16) & 0xffu), v3 = static_cast<int8_t>(w[i] >> 24);
-            o[2 * i] = pack_half2(dv * static_cast<float>(v0), dv * static_cast<float>(v1));
-            o[2 * i + 1] = pack_half2(dv * static_cast<float>(v2), dv * static_cast<float>(v3));
-        }
+        for (int i = 0; i < 16; ++i)
+            v[i] = dv * static_cast<float>(static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu));
     }
 };
 
 template <>
-struct WRaw<kQ4_K> {
-    u32x4 hdr, a, b;
+struct WSeg<kQ4_K> {
+    u32x4 hdr, q;
     template <class Row>
     __device__ __forceinline__ void load(const Row& r, int32_t e0) {
-        const uint32_t blk = static_cast<uint32_t>(e0 / 256) * 144u, c = static_cast<uint32_t>(e0 % 256) / 64u;
+        const uint32_t blk = static_cast<uint32_t>(e0 / 256) * 144u, rr = static_cast<uint32_t>(e0 % 256);
         hdr = r.ld16(blk);
-        a = r.ld16(blk + 16u + 32u * c);
-        b = r.ld16(blk + 32u + 32u * c);
+        q = r.ld16(blk + 16u + 32u * (rr / 64u) + (rr % 32u));
     }
-    __device__ __forceinline__ void get(int32_t e0, uint32_t (&o)[16]) const {
-        const int j = (e0 % 256) / 32, sh = 4 * (j & 1);
+    __device__ __forceinline__ void get(int32_t e0, float (&v)[16]) const {
+        const int j = (e0 % 256) / 32, s = 4 * (j & 1);
         int sc, mn;
         k4_scale_min(j, hdr.y, hdr.z, hdr.w, sc, mn);
-        const float s = half_bits_to_float(hdr.x & 0xffffu) * static_cast<float>(sc);
+        const float a = half_bits_to_float(hdr.x & 0xffffu) * static_cast<float>(sc);
         const float m = half_bits_to_float(hdr.x >> 16) * static_cast<float>(mn);
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t q = (w[i] >> sh) & 0x0f0f0f0fu;
-            o[2 * i] = pack_half2(s * static_cast<float>(q & 15u) - m, s * static_cast<float>((q >> 8) & 15u) - m);
-            o[2 * i + 1] =
-                pack_half2(s * static_cast<float>((q >> 16) & 15u) - m, s * static_cast<float>(q >> 24) - m);
-        }
+        for (int i = 0; i < 16; ++i) v[i] = a * static_cast<float>((w[i >> 2] >> (s + 8 * (i & 3))) & 15u) - m;
     }
 };
 
 template <>
-struct WRaw<kQ6_K> {
-    Raw16 l0, l1, h0, h1;
+struct WSeg<kQ6_K> {
+    Raw16 ql, qh;
     uint32_t scw, d, sh;
     template <class Row>
     __device__ __forceinline__ void load(const Row& r, int32_t e0) {
         const uint32_t blk = static_cast<uint32_t>(e0 / 256) * 210u;
-        const uint32_t rr = static_cast<uint32_t>(e0 % 256), h = rr / 128u, grp = (rr % 128u) / 32u;
-        const uint32_t ql = blk + 64u * h + ((grp & 1u) ? 32u : 0u), qh = blk + 128u + 32u * h;
+        const uint32_t rr = static_cast<uint32_t>(e0 % 256), h = rr / 128u, g = (rr % 128u) / 32u, l0 = rr % 32u;
         sh = r.sh(blk);  // every field offset used here is even: one shift for all
-        raw16_load(l0, r, ql, sh);
-        raw16_load(l1, r, ql + 16u, sh);
-        raw16_load(h0, r, qh, sh);
-        raw16_load(h1, r, qh + 16u, sh);
-        scw = r.ldu16(blk + 192u + 8u * h + 2u * grp);  // sc of elements 0-15 and 16-31
+        raw16_load(ql, r, blk + 64u * h + 32u * (g & 1u) + l0, sh);
+        raw16_load(qh, r, blk + 128u + 32u * h + l0, sh);
+        scw = r.ldu16(blk + 192u + 8u * h + 2u * g);  // scales l0 / 16 + 2g of this half
         d = r.ldu16(blk + 208u);
     }
-    __device__ __forceinline__ void get(int32_t e0, uint32_t (&o)[16]) const {
-        const int grp = ((e0 % 256) % 128) / 32;
-        const float dv = half_bits_to_float(d);
-        const float s0 = dv * static_cast<float>(static_cast<int8_t>(scw & 0xffu));
-        const float s1 = dv * static_cast<float>(static_cast<int8_t>(scw >> 8));
-        const uint4 a = raw16_get(l0, sh), b = raw16_get(l1, sh), c = raw16_get(h0, sh), e = raw16_get(h1, sh);
-        const uint32_t L[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        const uint32_t H[8] = {c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w};
-        const int lsh = grp >= 2 ? 4 : 0, hsh = 2 * grp;
+    __device__ __forceinline__ void get(int32_t e0, float (&v)[16]) const {
+        const int rr = e0 % 256, g = (rr % 128) / 32, l0 = rr % 32;
+        const float s = half_bits_to_float(d) * static_cast<float>(static_cast<int8_t>((scw >> (l0 >= 16 ? 8 : 0)) & 0xffu));
+        const uint4 a = raw16_get(ql, sh), b = raw16_get(qh, sh);
+        const uint32_t L[4] = {a.x, a.y, a.z, a.w}, H[4] = {b.x, b.y, b.z, b.w};
+        const int lsh = 4 * (g >> 1), hsh = 2 * g;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float s = i < 4 ? s0 : s1;
-            const uint32_t q = ((L[i] >> lsh) & 0x0f0f0f0fu) | (((H[i] >> hsh) & 0x03030303u) << 4);
-            o[2 * i] = pack_half2(s * static_cast<float>(static_cast<int>(q & 63u) - 32),
-                                  s * static_cast<float>(static_cast<int>((q >> 8) & 63u) - 32));
-            o[2 * i + 1] = pack_half2(s * static_cast<float>(static_cast<int>((q >> 16) & 63u) - 32),
-                                      s * static_cast<float>(static_cast<int>(q >> 24) - 32));
+        for (int i = 0; i < 16; ++i) {
+            const int sh8 = 8 * (i & 3);
+            const int q = static_cast<int>(((L[i >> 2] >> (lsh + sh8)) & 15u) | (((H[i >> 2] >> (hsh + sh8)) & 3u) << 4));
+            v[i] = s * static_cast<float>(q - 32);
         }
     }
 };
 
 // Y tile of (32 WM MW) tokens x (64 WN) rows per work-group of 2 MW waves
 // (MW along the tokens, 2 along the rows); each wave owns WM x WN 32x32
-// accumulator tiles.  K advances 64 per step
-// through two LDS buffers: token rows [tokens][64 + 8 pad] fp16 and weight
-// rows [rows][64 + 8 pad] fp16.  In step s the MFMAs consume LDS buffer
-// s % 2 while the loads for later steps are in flight, then step s + 1's
-// registers are written to the other buffer; one barrier per step.  All loads
-// are buffer loads whose out-of-range reads return 0 without a memory request
-// (tokens past B, K past the range, rows past N), so each wave issues the same
-// loads every step and each wait covers exactly the loads it needs.
+// accumulator tiles.  Both operands are fp16 pairs (hi, lo), and each 16-wide
+// K slice runs three v_mfma_f32_32x32x16_f16 per tile: x_hi w_hi + x_lo w_hi +
+// x_hi w_lo (x_lo w_lo is below 2^-22 of the product).  With fp32
+// accumulation the result is within about 2e-7 relative L2 of the
+// reference's integer block dots (measured on the CPU and the GPU for all
+// four formats), where fp16 operands alone reach 3e-4.
+// K advances 32 per step through two LDS buffers, each holding token rows
+// [tokens][32 + 8 pad] and weight rows [rows][32 + 8 pad] as hi and lo
+// arrays.  In step s the MFMAs consume buffer s % 2 while the loads for
+// later steps are in flight, then step s + 1's registers are written to the
+// other buffer; one barrier per step.  All loads are buffer loads whose
+// out-of-range reads return 0 without a memory request (tokens past B, K past
+// the range, rows past N), so each wave issues the same loads every step and
+// each wait covers exactly the loads it needs.
 // MFMA operand layouts (v_mfma_f32_32x32x16_f16): lane l holds
 // A[l % 32][8 (l / 32) .. + 8] and B[8 (l / 32) .. + 8][l % 32]; accumulator
 // register r of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 // blockIdx.z selects a K range of kchunk (split K); with gridDim.z > 1 the
 // tile goes to part[z][t][m] and matbatch_reduce_kernel adds the ranges in
 // order.
-constexpr int kMfKs = 64;
+constexpr int kMfKs = 32;
 constexpr int kMfLd = kMfKs + 8;  // halves per LDS row (16-byte aligned, staggers banks)
-constexpr int32_t kMfOob = 0x7ffffff0;  // a buffer offset past any resource
+// a buffer offset past any resource (resources here are below 2^30 bytes);
+// small field offsets may still be added to it without leaving int32
+constexpr int32_t kMfOob = 0x7ff00000;
+
+template <int WM, int WN, int MW>
+constexpr size_t mfma_lds_bytes() {
+    return 2 * 2 * static_cast<size_t>(32 * WM * MW + 64 * WN) * kMfLd * sizeof(_Float16);
+}
 
 template <int TYPE, int WM, int WN, int MW = 2>
 __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kernel(const uint8_t* __restrict w,
                                                                                    size_t rbytes,
-                                                            const _Float16* __restrict xh,
+                                                            const _Float16* __restrict xhl,
                                                             const float* __restrict rscale, int32_t b, int32_t k,
                                                             int32_t n, float* __restrict y, int32_t kchunk,
                                                             float* __restrict part) {
     constexpr int THREADS = 128 * MW;
     constexpr int BM = 32 * WM * MW, BN = 64 * WN;
-    static_assert(2 * BN <= THREADS, "one thread per 32-value weight segment of a step");
-    constexpr int XCH = BM * 8 / THREADS;  // 16-byte activation chunks per thread and step
-    __shared__ __align__(16) _Float16 xs[2][BM * kMfLd];
-    __shared__ __align__(16) _Float16 ws[2][BN * kMfLd];
+    static_assert(2 * BN <= THREADS, "one thread per 16-value weight piece of a step");
+    constexpr int XCH = BM * 4 / THREADS;  // 16-byte chunks of 8 values (hi and lo each) per thread and step
+    static_assert(XCH * THREADS == BM * 4, "whole chunks per thread");
+    static_assert(mfma_lds_bytes<WM, WN, MW>() <= 160 * 1024, "LDS of one CU");
+    __shared__ __align__(16) _Float16 xs[2][2][BM * kMfLd];  // [buffer][hi, lo]
+    __shared__ __align__(16) _Float16 ws[2][2][BN * kMfLd];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -285,13 +292,14 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // activation chunks c = tid + THREADS i: token row c / 8 of the tile, halves
-    // 8 (c % 8) .. + 8 of the step; one resource over the tile's token rows
+    // activation chunks c = tid + THREADS i: token row c / 4 of the tile,
+    // values 8 (c % 4) .. + 8 of the step, hi at byte 32 j and lo at 32 j + 16
+    // of chunk j = (row k + value) / 8; one resource over the tile's token rows
     const int32_t rows_here = min(BM, b - t0);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(xh + static_cast<size_t>(t0) * k), static_cast<short>(0),
-        rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-    // weight segment tid (row tid / 2 of the tile, 32 values at 32 (tid % 2))
+        const_cast<_Float16*>(xhl + static_cast<size_t>(t0) * k * 2), static_cast<short>(0),
+        rows_here * k * 2 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    // weight piece tid (row tid / 2 of the tile, 16 values at 16 (tid % 2))
     // for tid < 2 BN, through one resource over the tile's rows
     const int wrow = tid >> 1, wseg = tid & 1;
     const int32_t wrows_here = min(BN, n - n0);
@@ -301,39 +309,51 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
                                               wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
     wrs.base = tid < 2 * BN && wrow < wrows_here ? wrow * static_cast<int32_t>(rbytes) : kMfOob / 2;
 
-    uint4 xr[XCH];
-    WRaw<TYPE> wr[2];
+    uint4 xr[XCH][2];
+    WSeg<TYPE> wr[2];
     // activation chunks of one step; past the range an offset past the
     // resource reads zeros
     auto gload_x = [&](int32_t k0) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + THREADS * i, r = c >> 3, seg = c & 7;
+            const int c = tid + THREADS * i, r = c >> 2, seg = c & 3;
             const int32_t kx = k0 + 8 * seg;
-            const int32_t off = kx < ke ? (r * k + kx) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-            xr[i] = make_uint4(v.x, v.y, v.z, v.w);
+            const int32_t off = kx < ke ? (r * k + kx) * 2 * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
+            const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+            const u32x4 l = __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16, 0, 0);
+            xr[i][0] = make_uint4(h.x, h.y, h.z, h.w);
+            xr[i][1] = make_uint4(l.x, l.y, l.z, l.w);
         }
     };
     // raw weight blocks of one step into register set `set`; past the range
-    // a row offset past the resource reads zeros (k, ke are multiples of 32)
+    // (k, ke are multiples of 32) the row base moves past the resource, so
+    // every field reads zeros without a memory request
     auto gload_w = [&](int set, int32_t k0) {
-        const int32_t kw = k0 + 32 * wseg;
-        wr[set].load(wrs, kw < ke ? kw : 1 << 24);
+        const int32_t kw = k0 + 16 * wseg;
+        TileRow r = wrs;
+        if (kw >= ke) r.base = kMfOob / 2;
+        wr[set].load(r, kw < ke ? kw : 0);
     };
     auto lstore = [&](int set, int buf, int32_t k0) {
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int c = tid + THREADS * i, r = c >> 3, seg = c & 7;
-            *reinterpret_cast<uint4*>(&xs[buf][r * kMfLd + 8 * seg]) = xr[i];
+            const int c = tid + THREADS * i, r = c >> 2, seg = c & 3;
+            *reinterpret_cast<uint4*>(&xs[buf][0][r * kMfLd + 8 * seg]) = xr[i][0];
+            *reinterpret_cast<uint4*>(&xs[buf][1][r * kMfLd + 8 * seg]) = xr[i][1];
         }
         if (tid < 2 * BN) {
-            uint32_t o[16];
-            const int32_t kw = k0 + 32 * wseg;
-            wr[set].get(kw < ke ? kw : 0, o);
-            uint4* dst = reinterpret_cast<uint4*>(&ws[buf][wrow * kMfLd + 32 * wseg]);
+            float v[16];
+            const int32_t kw = k0 + 16 * wseg;
+            wr[set].get(kw < ke ? kw : 0, v);
+            uint32_t hi[8], lo[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+            for (int i = 0; i < 8; ++i) split2(v[2 * i], v[2 * i + 1], hi[i], lo[i]);
+            uint4* dh = reinterpret_cast<uint4*>(&ws[buf][0][wrow * kMfLd + 16 * wseg]);
+            uint4* dl = reinterpret_cast<uint4*>(&ws[buf][1][wrow * kMfLd + 16 * wseg]);
+            dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+            dl[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
         }
     };
 
@@ -341,18 +361,34 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kMfKs; kk += 16) {
-            half8 av[WM], bv[WN];
+            half8 ah[WM], al[WM], bh[WN], bl[WN];
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
-                av[i] = *reinterpret_cast<const half8*>(&xs[buf][(wm * 32 * WM + 32 * i + li) * kMfLd + kk + lk]);
+            for (int i = 0; i < WM; ++i) {
+                const int o = (wm * 32 * WM + 32 * i + li) * kMfLd + kk + lk;
+                ah[i] = *reinterpret_cast<const half8*>(&xs[buf][0][o]);
+                al[i] = *reinterpret_cast<const half8*>(&xs[buf][1][o]);
+            }
 #pragma unroll
-            for (int j = 0; j < WN; ++j)
-                bv[j] = *reinterpret_cast<const half8*>(&ws[buf][(wn * 32 * WN + 32 * j + li) * kMfLd + kk + lk]);
+            for (int j = 0; j < WN; ++j) {
+                const int o = (wn * 32 * WN + 32 * j + li) * kMfLd + kk + lk;
+                bh[j] = *reinterpret_cast<const half8*>(&ws[buf][0][o]);
+                bl[j] = *reinterpret_cast<const half8*>(&ws[buf][1][o]);
+            }
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
                 for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -445,27 +481,28 @@ MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
 }
 
 template <int TYPE, int WM, int WN, int MW = 2>
-hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xh, const float* rscale, int32_t b, int32_t k,
+hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xhl, const float* rscale, int32_t b, int32_t k,
                          int32_t n, float* y, const MfmaPlan& p, float* part, hipStream_t stream) {
     constexpr int BM = 32 * WM * MW;
     const dim3 grid((n + 64 * WN - 1) / (64 * WN), (b + BM - 1) / BM, p.splits);
     hipLaunchKernelGGL((matbatch_mfma_kernel<TYPE, WM, WN, MW>), grid, dim3(128 * MW), 0, stream, w,
-                       row_bytes(TYPE, k), xh, rscale, b, k, n, y, p.kchunk, part);
+                       row_bytes(TYPE, k), xhl, rscale, b, k, n, y, p.kchunk, part);
     return hipGetLastError();
 }
 
 template <int TYPE>
-hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xh,
+hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                        float* rscale, float* part, hipStream_t stream) {
-    hipLaunchKernelGGL(act_f16_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xh), rscale);
+    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
+                       rscale);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
-    if (p.mw == 4 && p.wn == 2) e = launch_mfma_t<TYPE, 2, 2, 4>(w, xh, rscale, b, k, n, y, p, part, stream);
-    else if (p.mw == 4) e = launch_mfma_t<TYPE, 2, 1, 4>(w, xh, rscale, b, k, n, y, p, part, stream);
-    else if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xh, rscale, b, k, n, y, p, part, stream);
-    else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
-    else e = launch_mfma_t<TYPE, 1, 1>(w, xh, rscale, b, k, n, y, p, part, stream);
+    if (p.mw == 4 && p.wn == 2) e = launch_mfma_t<TYPE, 2, 2, 4>(w, xhl, rscale, b, k, n, y, p, part, stream);
+    else if (p.mw == 4) e = launch_mfma_t<TYPE, 2, 1, 4>(w, xhl, rscale, b, k, n, y, p, part, stream);
+    else if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xhl, rscale, b, k, n, y, p, part, stream);
+    else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
+    else e = launch_mfma_t<TYPE, 1, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     const size_t count = static_cast<size_t>(b) * n;
     size_t g = (count + kThreads - 1) / kThreads;
@@ -490,10 +527,10 @@ hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int3
 
 }  // namespace
 
-// fp16 quantised activations [B x K], their row scales [B], then the split-K
-// partials [splits x B x N]
+// fp16 pairs of the quantised activations [B x K x 2], their row scales [B],
+// then the split-K partials [splits x B x N]
 static size_t xh_bytes(int32_t b, int32_t k) {
-    return (static_cast<size_t>(b) * k * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
+    return (static_cast<size_t>(b) * k * 2 * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
 }
 static size_t rscale_bytes(int32_t b) { return (static_cast<size_t>(b) * sizeof(float) + 255) & ~static_cast<size_t>(255); }
 
@@ -518,15 +555,15 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     } else if ((wa & 3u) != 0) {
         return hipErrorInvalidValue;
     }
-    _Float16* xh = static_cast<_Float16*>(workspace);
+    _Float16* xhl = static_cast<_Float16*>(workspace);
     float* rscale = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k));
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k) + rscale_bytes(b));
-    if ((reinterpret_cast<uintptr_t>(xh) & 255u) != 0) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
     switch (type) {
-    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xh, rscale, part, stream);
-    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xh, rscale, part, stream);
-    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xh, rscale, part, stream);
-    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xh, rscale, part, stream);
+    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
+    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
+    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xhl, rscale, part, stream);
+    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream);
     case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }

@@ -24,8 +24,64 @@
 #include "gncx_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
+
+/* ---- row-parallel driver ---------------------------------------------- */
+
+/* Output rows are split into contiguous chunks, one pthread each, as the
+ * reference's pool splits them (cpp:169-208).  Every row is computed by
+ * exactly one thread with the same scalar arithmetic, so the result does not
+ * depend on the thread count.  Threads: $ORC_THREADS, else the online CPUs,
+ * at most 16. */
+typedef void (*orc_rows_fn)(void* ctx, int32_t m0, int32_t m1);
+
+typedef struct {
+    orc_rows_fn fn;
+    void* ctx;
+    int32_t m0, m1;
+} orc_chunk;
+
+static void* orc_chunk_main(void* p) {
+    const orc_chunk* c = (const orc_chunk*)p;
+    c->fn(c->ctx, c->m0, c->m1);
+    return NULL;
+}
+
+int32_t orc_threads(void) {
+    const char* e = getenv("ORC_THREADS");
+    long t = e && e[0] ? strtol(e, NULL, 10) : sysconf(_SC_NPROCESSORS_ONLN);
+    if (t < 1) t = 1;
+    if (t > 16) t = 16;
+    return (int32_t)t;
+}
+
+static void orc_parallel_rows(int32_t n, int32_t min_rows, orc_rows_fn fn, void* ctx) {
+    int32_t t = orc_threads();
+    if (min_rows < 1) min_rows = 1;
+    if (t > n / min_rows) t = n / min_rows;
+    if (t <= 1) {
+        fn(ctx, 0, n);
+        return;
+    }
+    orc_chunk chunks[16];
+    pthread_t tid[16];
+    int started[16];
+    const int32_t per = (n + t - 1) / t;
+    for (int32_t i = 0; i < t; ++i) {
+        chunks[i].fn = fn;
+        chunks[i].ctx = ctx;
+        chunks[i].m0 = i * per < n ? i * per : n;
+        chunks[i].m1 = (i + 1) * per < n ? (i + 1) * per : n;
+        started[i] = i > 0 && pthread_create(&tid[i], NULL, orc_chunk_main, &chunks[i]) == 0;
+        if (i > 0 && !started[i]) fn(ctx, chunks[i].m0, chunks[i].m1);
+    }
+    fn(ctx, chunks[0].m0, chunks[0].m1);
+    for (int32_t i = 1; i < t; ++i)
+        if (started[i]) pthread_join(tid[i], NULL);
+}
 
 /* ---- scalar decoders ------------------------------------------------- */
 
@@ -332,16 +388,43 @@ float orc_dot_row(int32_t type, const uint8_t* row, const orc_act_q8* act, int32
 
 /* ---- matvec / matbatch / lm_head -------------------------------------- */
 
+typedef struct {
+    int32_t type;
+    const uint8_t* w;
+    const float* x;
+    const orc_act_q8* act;
+    int32_t k;
+    size_t rb;
+    float* y;
+} mv_ctx;
+
+static void mv_rows(void* p, int32_t m0, int32_t m1) {
+    const mv_ctx* c = (const mv_ctx*)p;
+    for (int32_t m = m0; m < m1; ++m) c->y[m] = orc_dot_row(c->type, c->w + (size_t)m * c->rb, c->act, c->k, c->x);
+}
+
 /* cpp:1327-1471.  Unknown types leave y untouched (cpp:1362-1462). */
 void orc_matvec(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n, float* y) {
     if (type != ORC_Q4_0 && type != ORC_Q8_0 && type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_BF16)
         return;
     orc_act_q8* act = (orc_act_q8*)malloc(sizeof(orc_act_q8) * (size_t)(k / 32 > 0 ? k / 32 : 1));
     orc_quantize_act_q8(x, k, act);
-    const size_t rb = orc_row_bytes(type, k);
-    for (int32_t m = 0; m < n; ++m) y[m] = orc_dot_row(type, w + (size_t)m * rb, act, k, x);
+    mv_ctx c = {type, w, x, act, k, orc_row_bytes(type, k), y};
+    orc_parallel_rows(n, 64, mv_rows, &c);
     free(act);
 }
+
+typedef struct {
+    int32_t type;
+    const uint8_t* w;
+    const float* x;
+    const orc_act_q8* act;
+    int32_t b, k, n;
+    size_t rb;
+    float* y;
+} mb_ctx;
+
+static void mb_rows(void* p, int32_t m0, int32_t m1);
 
 /* cpp:1495-1692.  Each token row is quantised on its own (cpp:1506-1510);
  * the per-type inner loops differ from matvec in association and in which
@@ -353,9 +436,19 @@ void orc_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int
     const int32_t nb = k / 32;
     orc_act_q8* act = (orc_act_q8*)malloc(sizeof(orc_act_q8) * (size_t)nb * (size_t)(b > 0 ? b : 1));
     for (int32_t t = 0; t < b; ++t) orc_quantize_act_q8(x + (size_t)t * k, k, act + (size_t)t * nb);
-    const size_t rb = orc_row_bytes(type, k);
-    for (int32_t m = 0; m < n; ++m) {
-        const uint8_t* row = w + (size_t)m * rb;
+    mb_ctx c = {type, w, x, act, b, k, n, orc_row_bytes(type, k), y};
+    orc_parallel_rows(n, 4, mb_rows, &c);
+    free(act);
+}
+
+static void mb_rows(void* p, int32_t m0, int32_t m1) {
+    const mb_ctx* c = (const mb_ctx*)p;
+    const int32_t type = c->type, b = c->b, k = c->k, n = c->n, nb = k / 32;
+    const orc_act_q8* act = c->act;
+    const float* x = c->x;
+    float* y = c->y;
+    for (int32_t m = m0; m < m1; ++m) {
+        const uint8_t* row = c->w + (size_t)m * c->rb;
         for (int32_t t = 0; t < b; ++t) {
             const orc_act_q8* a = act + (size_t)t * nb;
             float acc = 0.0f;
@@ -404,7 +497,6 @@ void orc_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int
             y[(size_t)t * n + m] = acc;
         }
     }
-    free(act);
 }
 
 /* cpp:1713-1732: matvec on the tied embedding, then optional tanh softcap. */

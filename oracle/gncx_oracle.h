@@ -6,8 +6,10 @@
  * product (gnc-x_amd/) never links, loads or falls back to it.
  *
  * Every function restates one reference routine of
- * csrc/gncx_llm_kernels.cpp (cited per function in gncx_oracle.c) as plain,
- * single-threaded scalar C compiled with -ffp-contract=off.  Integer and byte
+ * csrc/gncx_llm_kernels.cpp (cited per function in gncx_oracle.c) as plain
+ * scalar C compiled with -ffp-contract=off; matvec / matbatch / lm_head split
+ * their output rows over pthreads, each row computed by one thread, so the
+ * results do not depend on the thread count.  Integer and byte
  * work (fp16 decode, block dequantisation, Q8 activation quantisation, block
  * integer dots) is bit-exact with the reference; float accumulation follows
  * the reference's association but not its compiler's FMA contraction.
@@ -37,6 +39,9 @@ typedef struct {
 float    orc_fp16_to_fp32(uint16_t h);
 float    orc_bf16_to_fp32(uint16_t b);
 size_t   orc_row_bytes(int32_t type, int32_t k);
+/* Threads used by the row-parallel functions ($ORC_THREADS, else the online
+ * CPUs, at most 16). */
+int32_t  orc_threads(void);
 
 void     orc_quantize_act_q8(const float* x, int32_t k, orc_act_q8* out);
 

@@ -1,0 +1,88 @@
+"""GPU: the Qwen3-8B-shaped model end to end at its own widths, against the
+oracle-composed model (tests/oracle_model.py).
+
+Shape: hidden 4096, 32 query and 8 KV heads of 128, SwiGLU FFN 12288, vocab
+151936, Q4_K layer matrices, and the tied Q6_K token_embd as both embedding
+table and lm_head (lua/gncx_streamer.lua:951-962).  Each run prefills a prompt
+through matbatch (lua/gncx_streamer.lua:968-1208), then decodes greedily
+(:759-965), teacher-forced on both sides: the library is fed the tokens the
+oracle's logits pick.  Bar: logits within 1e-3 relative L2 after the prompt
+and after every decode step.
+
+Both the streamer's own call sequence (per-token RMSNorm, heads-RMSNorm, RoPE
+and attention calls) and the library's fused extensions (batched norms, one
+causal attention pass) run over the same model and are held to the same bar.
+All 36 layers run with a short prompt; a 300-token prompt, which takes the
+256-token matbatch tiles and several causal attention blocks, runs 4 layers
+at the full widths.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import gncx, rel_l2
+from oracle_model import OracleModel
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _teacher_forced(lib, torch, oracle, model, prompt, n_decode, max_seq):
+    import gncx_amd.decode as dec
+
+    ref = OracleModel(oracle, model, max_seq=max_seq)
+    for pos, tok in enumerate(prompt[:-1]):
+        ref.step(tok, pos, logits=False)
+    want = [ref.step(prompt[-1], len(prompt) - 1)]
+    toks = []
+    for i in range(n_decode):
+        toks.append(int(np.argmax(want[-1])))
+        want.append(ref.step(toks[-1], len(prompt) + i))
+    print(f"oracle tokens {toks}", flush=True)
+    for fused in (False, True):
+        d = dec.Decoder(lib, torch, model, max_seq=max_seq, fused=fused)
+        got = d.prefill(prompt).cpu().numpy()
+        gncx.check(lib)
+        errs = [rel_l2(got, want[0])]
+        picks = [int(np.argmax(got))]
+        for i, tok in enumerate(toks):
+            got = d.forward_token(tok, len(prompt) + i).cpu().numpy()
+            gncx.check(lib)
+            errs.append(rel_l2(got, want[i + 1]))
+            picks.append(int(np.argmax(got)))
+        print(f"layers={model.shape.n_layers} prompt={len(prompt)} fused={fused} rel_l2="
+              + " ".join(f"{e:.2e}" for e in errs) + f" library picks {picks[:-1]}", flush=True)
+        assert all(np.isfinite(errs)) and max(errs) < TOL, errs
+        del d
+
+
+def test_qwen3_8b_36_layers(lib, oracle, torch_mod):
+    import gncx_amd.decode as dec
+
+    torch = torch_mod
+    model = dec.build_model(torch, dec.QWEN3_8B, seed=2024)
+    try:
+        rng = np.random.default_rng(11)
+        prompt = [int(t) for t in rng.integers(0, dec.QWEN3_8B.vocab, 24)]
+        _teacher_forced(lib, torch, oracle, model, prompt, n_decode=3, max_seq=32)
+    finally:
+        lib.gncx_hip_weight_forget(None)
+        del model
+        torch.cuda.empty_cache()
+
+
+def test_qwen3_8b_widths_300_token_prompt(lib, oracle, torch_mod):
+    import gncx_amd.decode as dec
+
+    torch = torch_mod
+    shape = dec.Qwen3Shape(n_layers=4)
+    model = dec.build_model(torch, shape, seed=7)
+    try:
+        rng = np.random.default_rng(12)
+        prompt = [int(t) for t in rng.integers(0, shape.vocab, 300)]
+        _teacher_forced(lib, torch, oracle, model, prompt, n_decode=2, max_seq=320)
+    finally:
+        lib.gncx_hip_weight_forget(None)
+        del model
+        torch.cuda.empty_cache()
