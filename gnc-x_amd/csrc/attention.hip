@@ -1017,6 +1017,15 @@ size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t wind
     return sizeof(float) * static_cast<size_t>(n_split) * n_heads * (head_dim + 2) + 256;
 }
 
+size_t attention_workspace_need(const AttnArgs& a) {
+    if (a.n_heads <= 0 || a.n_kv_heads <= 0 || a.pos < 0 || a.n_heads % a.n_kv_heads != 0) return 0;
+    const int32_t G = a.n_heads / a.n_kv_heads;
+    const bool mq = a.head_dim == 128 && G >= 16 && G <= kMqHeads && !a.norm_qk && !a.rope;
+    const Plan pl = mq ? make_mq_plan(a.pos, a.sliding_window, a.n_kv_heads)
+                       : make_plan(a.pos, a.sliding_window, a.n_kv_heads, G, a.head_dim);
+    return sizeof(float) * static_cast<size_t>(pl.n_split) * a.n_heads * (a.head_dim + 2);
+}
+
 hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (a.n_heads <= 0 || a.n_kv_heads <= 0 || a.pos < 0) return hipErrorInvalidValue;
     if (a.n_heads % a.n_kv_heads != 0) return hipErrorInvalidValue;

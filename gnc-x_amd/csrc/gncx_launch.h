@@ -96,6 +96,9 @@ struct AttnArgs {
     float* k_out;             // prologue result for k_new written back (optional)
 };
 size_t attention_workspace_bytes(int32_t n_heads, int32_t head_dim, int32_t window);
+// The workspace launch_attention(a, ...) uses for its split plan (at most
+// attention_workspace_bytes); 0 for arguments it rejects.
+size_t attention_workspace_need(const AttnArgs& a);
 
 // Causal prefill of `batch` tokens at positions pos0 .. pos0 + batch - 1: per
 // token the heads-RMSNorm + RoPE prologue (q and k in place), its K/V row
@@ -162,5 +165,14 @@ hipError_t launch_fetch_embedding_dev(int32_t type, const uint8_t* table, const 
 size_t argmax_workspace_bytes(int32_t n);
 hipError_t launch_argmax(const float* x, int32_t n, int32_t* out, int32_t* log, void* workspace, size_t ws_bytes,
                          hipStream_t stream);
+
+// Fixed device scratch of the no-allocation decode step (noalloc.hip): a
+// file-scope device array of kNoAllocScratchBytes per GPU.  The argmax
+// partials use its first kNoAllocArgmaxBytes, the attention partials the
+// rest.  noalloc_scratch returns this device's copy's address, looked up once
+// per device (with that device current) and kept.
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
+constexpr size_t kNoAllocArgmaxBytes = size_t{64} << 10;
+hipError_t noalloc_scratch(int device, void** out);
 
 }  // namespace gncx

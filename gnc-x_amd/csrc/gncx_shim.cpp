@@ -1361,6 +1361,9 @@ GNCX_API int gncx_hip_init(int device) {
     if (e != hipSuccess) return static_cast<int>(e);
     g_rt.device = device;
     g_rt.ready = true;
+    // the no-allocation step's scratch on this device (noalloc.hip)
+    void* scratch = nullptr;
+    if (!check(noalloc_scratch(device, &scratch), "gncx_hip_init")) return g_last_code;
     return 0;
 }
 
@@ -1949,10 +1952,24 @@ bool plan_state(const GNCXDecodeModel& m, const GNCXDecodeState& s, const char* 
 
 }  // namespace
 
-GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id,
-                                  int32_t pos, int32_t greedy) {
-    std::lock_guard<CallLock> lk(g_mu);
-    const char* where = "gncx_hip_decode_step";
+namespace {
+
+// The scratch of one step: the attention split-K partials (reused by every
+// layer, stream-ordered) and the argmax partials.
+struct StepScratch {
+    void* attn;
+    size_t attn_bytes;
+    void* argmax;
+    size_t argmax_bytes;
+};
+
+// The whole step.  fixed == nullptr: scratch from the library's growable
+// device buffers (and host weights uploaded once, as everywhere).  fixed !=
+// nullptr: the caller's scratch, and nothing is allocated: the weights must
+// already be device memory, and a step needing more scratch than given is
+// rejected before anything is enqueued.
+int decode_step_impl(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id, int32_t pos,
+                     int32_t greedy, const StepScratch* fixed, const char* where) {
     if (!model || !state || !model->layers || !model->base) {
         set_error(where, "model (with base and layers) and state are required", -1);
         return -1;
@@ -1972,7 +1989,12 @@ GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecode
         set_error(where, "token id past the vocabulary", -1);
         return -1;
     }
-    if (!ensure_runtime(where) || !plan_model(m, where) || !plan_state(m, s, where)) return -1;
+    if (!ensure_runtime(where)) return -1;
+    if (fixed && !is_device_ptr(m.base)) {
+        set_error(where, "the weights (model->base) must be device memory: this entry point uploads nothing", -1);
+        return -1;
+    }
+    if (!plan_model(m, where) || !plan_state(m, s, where)) return -1;
     const DecodePlan& P = g_plan;
     const hipStream_t st = g_rt.stream;
     const int32_t E = m.embed, Q = m.n_heads * m.head_dim, KV = m.n_kv_heads * m.head_dim, F = m.ffn;
@@ -1986,7 +2008,39 @@ GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecode
         }
         rp = &rope;
     }
-    if (!g_rt.ws.ensure(attention_workspace_bytes(m.n_heads, m.head_dim, pos + 1), where)) return -1;
+    StepScratch sc{};
+    if (fixed) {
+        // the split plan of this step's attention (the same for every layer)
+        AttnArgs probe{};
+        probe.pos = pos;
+        probe.n_heads = m.n_heads;
+        probe.n_kv_heads = m.n_kv_heads;
+        probe.head_dim = m.head_dim;
+        probe.write_kv = 1;
+        probe.norm_qk = m.qk_norm ? 1 : 0;
+        probe.rope = rp;
+        const size_t need_attn = attention_workspace_need(probe);
+        const size_t need_argmax = greedy ? argmax_workspace_bytes(m.vocab) : 0;
+        if (need_attn > fixed->attn_bytes || need_argmax > fixed->argmax_bytes) {
+            char msg[192];
+            std::snprintf(msg, sizeof(msg),
+                          "this step needs %zu B of attention and %zu B of argmax scratch; the fixed scratch holds "
+                          "%zu and %zu B",
+                          need_attn, need_argmax, fixed->attn_bytes, fixed->argmax_bytes);
+            set_error(where, msg, static_cast<int>(hipErrorInvalidValue));
+            return -1;
+        }
+        sc = *fixed;
+    } else {
+        if (!g_rt.ws.ensure(attention_workspace_bytes(m.n_heads, m.head_dim, pos + 1), where)) return -1;
+        sc.attn = g_rt.ws.p;
+        sc.attn_bytes = g_rt.ws.cap;
+        if (greedy) {
+            if (!g_rt.aux.ensure(argmax_workspace_bytes(m.vocab), where)) return -1;
+            sc.argmax = g_rt.aux.p;
+            sc.argmax_bytes = g_rt.aux.cap;
+        }
+    }
 
     // embedding row of the token (cpp:693-760), into hidden[0]
     int cur = 0;
@@ -2072,7 +2126,7 @@ GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecode
         a.k_gamma = d.k_norm;
         a.eps = m.eps;
         a.rope = rp;
-        if (!check(launch_attention(a, g_rt.ws.p, g_rt.ws.cap, st), where)) return -1;
+        if (!check(launch_attention(a, sc.attn, sc.attn_bytes, st), where)) return -1;
         // O projection
         if (!check(launch_gemv(L.attn_output.ggml_type, d.o, s.attn, Q, E, s.proj, st), where)) return -1;
         // gate / up with SwiGLU
@@ -2099,14 +2153,35 @@ GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecode
     // final residual add + RMSNorm, then the tied lm_head (cpp:1713-1732)
     if (!check(launch_add_rmsnorm(H[cur], delta, P.onorm_dev, E, m.eps, s.normed, st), where)) return -1;
     if (!check(launch_gemv(m.token_embd.ggml_type, P.embd_dev, s.normed, E, m.vocab, s.logits, st), where)) return -1;
-    if (greedy) {
-        if (!g_rt.aux.ensure(argmax_workspace_bytes(m.vocab), where) ||
-            !check(launch_argmax(s.logits, m.vocab, s.token, s.token_log ? s.token_log + pos : nullptr, g_rt.aux.p,
-                                 g_rt.aux.cap, st),
-                   where))
-            return -1;
-    }
+    if (greedy && !check(launch_argmax(s.logits, m.vocab, s.token, s.token_log ? s.token_log + pos : nullptr,
+                                       sc.argmax, sc.argmax_bytes, st),
+                         where))
+        return -1;
     return 0;
+}
+
+}  // namespace
+
+GNCX_API int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id,
+                                  int32_t pos, int32_t greedy) {
+    std::lock_guard<CallLock> lk(g_mu);
+    return decode_step_impl(model, state, token_id, pos, greedy, nullptr, "gncx_hip_decode_step");
+}
+
+// gncx_hip_decode_step with its scratch in this GPU's fixed device array
+// (noalloc.hip) and no allocation of any kind: weights and every state
+// buffer must already be device memory.  Calls that overlap on one GPU share
+// the array and race.
+GNCX_API int gncx_hip_decode_step_noalloc(const GNCXDecodeModel* model, const GNCXDecodeState* state,
+                                          int32_t token_id, int32_t pos, int32_t greedy) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_decode_step_noalloc";
+    if (!ensure_runtime(where)) return -1;
+    void* base = nullptr;
+    if (!check(noalloc_scratch(g_rt.device, &base), where)) return -1;
+    StepScratch fixed{static_cast<char*>(base) + kNoAllocArgmaxBytes, kNoAllocScratchBytes - kNoAllocArgmaxBytes,
+                      base, kNoAllocArgmaxBytes};
+    return decode_step_impl(model, state, token_id, pos, greedy, &fixed, where);
 }
 
 // index of the first largest logit, on the device (the greedy pick of the

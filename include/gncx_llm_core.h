@@ -372,6 +372,20 @@ typedef struct GNCXDecodeState {
 } GNCXDecodeState;
 int gncx_hip_decode_step(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id, int32_t pos,
                          int32_t greedy);
+/* gncx_hip_decode_step without any allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid it).  No counterpart in the reference.  Its scratch (attention
+ * split-K partials and argmax partials) lives in a fixed device array of
+ * 8 MiB per GPU, held until the process ends, instead of device memory the
+ * library allocates; model->base and every state buffer must already be
+ * device memory (nothing is uploaded).  A step needing more scratch than the
+ * array holds (split plans of more than about 500 chunks, e.g. one KV head
+ * at a context past 16k) is rejected with an error before anything is
+ * enqueued.  Results are bit-identical with gncx_hip_decode_step.  Calls that
+ * overlap on one GPU share the array and race; serialise them.  Returns 0, or
+ * -1 with gncx_hip_last_error set. */
+int gncx_hip_decode_step_noalloc(const GNCXDecodeModel* model, const GNCXDecodeState* state, int32_t token_id,
+                                 int32_t pos, int32_t greedy);
 /* *out_index = index of the first largest of values[0..n) (NaN never wins):
  * the greedy pick of the streamer's sampler without its repetition penalty
  * (lua/gncx_streamer.lua:1229-1272), on the device.  Device pointers; values
