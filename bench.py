@@ -129,10 +129,16 @@ def time_gemv(pkg, lib, torch, t, k, n, steps, warmup, copies, seed=1):
     }
 
 
-def time_matbatch(pkg, lib, torch, t, k, n, b, steps, copies):
+ROTATE_BYTES = 512 << 20  # weight copies rotated per shape: twice the 256 MB Infinity Cache
+
+
+def time_matbatch(pkg, lib, torch, t, k, n, b, steps):
     """gncx_xfold_universal_matbatch with device pointers; one HIP-event pair
-    around `steps` back-to-back calls (act quantisation + the MFMA product)."""
+    around `steps` back-to-back calls (act quantisation + the MFMA product),
+    rotating weight copies of at least 512 MB in all."""
     w_host = pkg.synth.make_weights(t, n, k, seed=11)
+    copies = max(2, -(-ROTATE_BYTES // w_host.nbytes))
+    steps = max(steps, copies)
     ws = [torch.from_numpy(w_host).cuda() for _ in range(copies)]
     x = torch.from_numpy(pkg.synth.make_activations(b, k, seed=12).reshape(b, k)).cuda()
     y = torch.zeros(b, n, dtype=torch.float32, device="cuda")
@@ -157,7 +163,26 @@ def time_matbatch(pkg, lib, torch, t, k, n, b, steps, copies):
     torch.cuda.empty_cache()
     return {"us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
             "frac_fp16_mfma_peak": round(flops / (us * 1e-6) / MFMA_FP16_PEAK, 4),
-            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "weight_copies": copies}
+
+
+MATBATCH_SHAPES = {"q4k_4096x4096": (12, 4096, 4096), "q4k_4096x14336": (12, 4096, 14336),
+                   "q6k_14336x4096": (14, 14336, 4096)}
+PREFILL_SHAPES = {"q4k_4096x4096_b2048": (12, 4096, 4096), "q4k_4096x12288_b2048": (12, 4096, 12288),
+                  "q4k_12288x4096_b2048": (12, 12288, 4096)}
+
+
+def matbatch_extras(pkg, lib, torch, steps=20):
+    """Matbatch at B = 64 / 256 / 512 on the prefill shapes, and the B = 2048
+    prefill matrices of the Qwen3-8B-shaped model.  GFLOP/s count 2 B K N
+    (the useful products); the kernel issues three fp16 MFMA products each."""
+    mb = {}
+    for name, (tt, kk, nn) in MATBATCH_SHAPES.items():
+        for bb in (64, 256, 512):
+            mb[f"{name}_b{bb}"] = time_matbatch(pkg, lib, torch, tt, kk, nn, bb, steps)
+    for name, (tt, kk, nn) in PREFILL_SHAPES.items():
+        mb[name] = time_matbatch(pkg, lib, torch, tt, kk, nn, 2048, 10)
+    return mb
 
 
 def time_attention(lib, torch, H, KV, hd, ctx, sw, steps, copies):
@@ -388,6 +413,8 @@ def main() -> int:
     ap.add_argument("--decode-only", choices=["streamer", "fused", "native"], default=None,
                     help="only the decode measurement: prefill the prompt (fused), then --decode-tokens greedy "
                          "tokens through one call sequence, and print its rate (for kernel profiles)")
+    ap.add_argument("--matbatch-only", action="store_true",
+                    help="only the matbatch measurements (for kernel profiles)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -416,6 +443,9 @@ def main() -> int:
     if args.decode_only:
         print(json.dumps(decode_only(pkg, lib, torch, args.decode_only, args.decode_prompt, args.decode_tokens)),
               flush=True)
+        return 0
+    if args.matbatch_only:
+        print(json.dumps({"matbatch": matbatch_extras(pkg, lib, torch)}), flush=True)
         return 0
 
     t, k, n = pkg.Q4_K, 4096, 14336
@@ -449,12 +479,7 @@ def main() -> int:
             r = time_attention(lib, torch, H, KV, hd, ctx, sw, 50, cp)
             att[name] = {"us_per_step": round(r["us_per_step"], 2), "gbps": round(r["gbps"], 1)}
         extra["attention"] = att
-        mb = {}
-        for name, (tt, kk, nn) in {"q4k_4096x4096": (pkg.Q4_K, 4096, 4096), "q4k_4096x14336": (pkg.Q4_K, 4096, 14336),
-                                   "q6k_14336x4096": (pkg.Q6_K, 14336, 4096)}.items():
-            for bb in (64, 256, 512):
-                mb[f"{name}_b{bb}"] = time_matbatch(pkg, lib, torch, tt, kk, nn, bb, 20, 4)
-        extra["matbatch"] = mb
+        extra["matbatch"] = matbatch_extras(pkg, lib, torch)
     if not args.no_decode:
         extra["decode_qwen3_8b"] = time_decode(pkg, lib, torch, args.decode_prompt, args.decode_tokens)
 

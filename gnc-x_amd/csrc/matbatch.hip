@@ -20,6 +20,11 @@
 // 3e-4).  An int8 MFMA path would be exact too, but its per-32-block scales
 // cost ~3 VALU operations per output and block, several times the
 // matrix-core time of the three fp16 products.
+// Q4_K (the layer format of the prefill workloads) has its own kernel,
+// matbatch_q4k_kernel: its weights are sc q, small integers exact in fp16,
+// with d and dmin fixed per 256-value super-block, so it needs two products
+// per K slice (x_hi, x_lo) and folds d and the dmin min term in once per
+// super-block.
 // BF16 weights (fp32 activations, cpp:1432-1461) use the slot-dot kernel: a
 // wave per (row, token).
 #include <hip/hip_runtime.h>
@@ -86,8 +91,13 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // range (SwiGLU outputs of 1e5 and more) keep the pair's relative precision.
 // One work-group per row: the row maximum first, then 8 lanes per 32-block,
 // 4 values per lane.
+// With pq given (K a multiple of 256), also each 32-block's sum of the
+// quantised activations, P = (sum q) * d / s, as an fp16 pair: per token row
+// and 256-value super-block, 8 hi then 8 lo values (the Q4_K kernel's min
+// term, cpp:1177-1178).
 __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
-                                                            uint2* __restrict xhl, float* __restrict rscale) {
+                                                            uint2* __restrict xhl, float* __restrict rscale,
+                                                            _Float16* __restrict pq) {
     __shared__ float red[kThreads / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
@@ -119,6 +129,20 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
         uint2* c = out + 4 * (t >> 1) + (t & 1);
         c[0] = hi;
         c[2] = lo;
+        if (pq) {
+            // the 8 lanes of block t / 8: quad sums, then lane i adds lane 7 - i
+            const int s4 = quad_sum(q0 + q1 + q2 + q3);
+            const int sum = s4 + __builtin_amdgcn_mov_dpp(s4, 0x141, 0xf, 0xf, false);
+            if ((t & 7) == 0) {
+                const int32_t blk = t >> 3;
+                const float pv = (static_cast<float>(sum) * d) * inv;
+                const _Float16 ph = static_cast<_Float16>(pv);
+                const _Float16 pl = static_cast<_Float16>(pv - static_cast<float>(ph));
+                _Float16* pr = pq + (static_cast<size_t>(row) * (k / 256) + blk / 8) * 16 + (blk & 7);
+                pr[0] = ph;
+                pr[8] = pl;
+            }
+        }
     }
 }
 
@@ -431,6 +455,302 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
         }
 }
 
+// ---- Q4_K: exact integer weights, one scale per super-block ---------------
+//
+// Q4_K weights are d * (sc q) - dmin * m (cpp:1135-1178) with sc q an integer
+// of at most 945, exact in fp16, and d, dmin fixed over a 256-value
+// super-block.  So the weight operand is sc q itself and each 16-wide K slice
+// costs two products (x_hi, x_lo against it); a super-block's accumulator D is
+// folded into the output once per super-block, acc += d D, where d belongs to
+// the lane's weight row (the accumulator column), so it is a per-lane scalar.
+// The min term, dmin sum_j m_j P_j with P_j = d_x sum q over 32-block j (also
+// an fp16 pair, from act_hilo_kernel), is one v_mfma_f32_32x32x8_f16 pair per
+// super-block over its 8 blocks.
+//
+// LDS rows hold 32 fp16 (64 B), the 16-byte segment index XORed with
+// (row / 4) % 4: an MFMA operand read (16 lanes = 16 rows, one segment) and a
+// staging write (16 lanes = 4 rows x 4 segments, or 8 rows x 2) each touch 16
+// distinct groups of 4 banks.
+__device__ __forceinline__ int swz(int row, int seg) { return row * 32 + 8 * (seg ^ ((row >> 2) & 3)); }
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+// Work-group of MW x NW waves (MW along the tokens, NW along the rows), each
+// owning WM x WN 32x32 accumulator tiles: a Y tile of (32 WM MW) tokens x
+// (32 WN NW) rows.  K advances 32 per step (one 32-block of Q4_K, 8 steps per
+// super-block).  Activations stream through a ring of 4 LDS stages filled by
+// direct-to-LDS buffer loads issued 3 steps ahead (each lane loads the chunk
+// that belongs at its position of the swizzled layout, so no registers hold
+// them); raw weight blocks are loaded two steps ahead into two register sets
+// and written to a double-buffered LDS array as sc q; a super-block's P values
+// are loaded during its predecessor, and its d, dmin and mins are staged by
+// the threads that dequantise its first block.
+constexpr int kXStages = 4;
+// s_waitcnt vmcnt(n) with no lgkm / exp wait (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+template <int WM, int WN, int MW, int NW>
+__global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1) void matbatch_q4k_kernel(
+    const uint8_t* __restrict w, size_t rbytes, const _Float16* __restrict xhl, const _Float16* __restrict pq,
+    const float* __restrict rscale, int32_t b, int32_t k, int32_t n, float* __restrict y, int32_t kchunk,
+    float* __restrict part) {
+    constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
+    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
+    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage and half; whole blocks per wave
+    static_assert(XBLK % WAVES == 0, "whole activation blocks per wave");
+    static_assert(2 * BN <= THREADS && BM <= THREADS, "one weight piece and one P row per thread at most");
+    // ring stages as separate arrays: the compiler then sees that a
+    // direct-to-LDS load into one stage does not alias reads of another and
+    // inserts no wait for it before those reads
+    __shared__ __align__(16) _Float16 xs0[2][BM * 32], xs1[2][BM * 32], xs2[2][BM * 32], xs3[2][BM * 32];
+    static_assert(kXStages == 4, "four ring arrays");
+    auto xstage = [&](int stage) -> _Float16(*)[BM * 32] {
+        return stage == 0 ? xs0 : stage == 1 ? xs1 : stage == 2 ? xs2 : xs3;
+    };
+    __shared__ __align__(16) _Float16 ws[2][BN * 32];            // [step parity] sc q
+    __shared__ __align__(16) _Float16 sp[2][2][BM * 8];          // [super-block parity][hi, lo] P of 8 blocks
+    __shared__ __align__(16) _Float16 smn[2][BN * 8];            // [super-block parity] mins of 8 blocks
+    __shared__ __align__(8) float sdm[2][BN][2];                 // [super-block parity] d, dmin
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv % MW, wn = wv / MW;
+    const int li = lane & 31, lh = lane >> 5;
+    const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int32_t kb = blockIdx.z * kchunk;
+    const int32_t ke = min(k, kb + kchunk);
+    const int32_t nsb = (ke - kb) / 256;
+    const int32_t sbs_row = k / 256;
+
+    const int32_t rows_here = min(BM, b - t0);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(xhl + static_cast<size_t>(t0) * k * 2), static_cast<short>(0),
+        rows_here * k * 2 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * sbs_row * 16), static_cast<short>(0),
+        rows_here * sbs_row * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    const int wrow = tid >> 1, whalf = tid & 1;
+    const int32_t wrows_here = min(BN, n - n0);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
+        wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
+    const int32_t wbase = tid < 2 * BN && wrow < wrows_here ? wrow * static_cast<int32_t>(rbytes) : kMfOob / 2;
+
+    floatx16 acc[WM][WN], D[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = D[i][j][r] = 0.0f;
+
+    uint4 pr[2];
+    u32x4 hdr[2], qv[2];
+    // activations of the step at k0 into ring stage `stage`: block blk (token
+    // rows 16 blk .. + 16) is 64 lanes x 16 B; lane L lands at segment
+    // position L % 4 of row L / 4, which holds logical segment
+    // (L % 4) ^ ((row / 4) % 4).  Past the range: zeros.
+    auto dma_x = [&](int stage, int32_t k0) {
+#pragma unroll
+        for (int blk = wv; blk < XBLK; blk += WAVES) {
+            const int row = 16 * blk + (lane >> 2);
+            const int lseg = (lane & 3) ^ ((row >> 2) & 3);
+            const int32_t off = k0 < ke ? (row * k + k0 + 8 * lseg) * 2 * static_cast<int32_t>(sizeof(_Float16))
+                                        : kMfOob;
+            _Float16(*xs)[BM * 32] = xstage(stage);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[0][blk * 16 * 32], 16, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[1][blk * 16 * 32], 16, off + 16, 0, 0, 0);
+        }
+    };
+    constexpr int kXLoads = 2 * (XBLK / WAVES);  // ring loads per wave and step
+    auto gload_p = [&](int32_t k0) {  // P of the super-block starting at k0
+        const int32_t off = k0 < ke && tid < BM
+                                ? (tid * sbs_row + k0 / 256) * 16 * static_cast<int32_t>(sizeof(_Float16))
+                                : kMfOob;
+        const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0);
+        const u32x4 l = __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, 0);
+        pr[0] = make_uint4(h.x, h.y, h.z, h.w);
+        pr[1] = make_uint4(l.x, l.y, l.z, l.w);
+    };
+    // header and the 16 code bytes of piece (wrow, whalf) of the 32-block at
+    // k0; past the range the base moves past the resource (reads zeros)
+    auto gload_w = [&](int set, int32_t k0) {
+        const int32_t base = k0 < ke ? wbase : kMfOob / 2;
+        const int32_t kk = k0 < ke ? k0 : 0;
+        const int32_t blk = (kk / 256) * 144, rr = kk % 256;
+        hdr[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk, 0, 0);
+        qv[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk + 16 + 32 * (rr / 64) + 16 * whalf, 0, 0);
+    };
+    // weights of the step at k0 from register set `set` into LDS buffer
+    // `buf`; at a super-block's first step also its P, d, dmin and mins
+    // (parity `sbp`)
+    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int sbp) {
+        if (tid < 2 * BN) {
+            const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
+            int sc, mn;
+            k4_scale_min(j, hdr[set].y, hdr[set].z, hdr[set].w, sc, mn);
+            const uint32_t qw[4] = {qv[set].x, qv[set].y, qv[set].z, qv[set].w};
+            uint32_t o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t a = (qw[e >> 1] >> (sh + 16 * (e & 1))) & 15u;
+                const uint32_t c = (qw[e >> 1] >> (sh + 16 * (e & 1) + 8)) & 15u;
+                const _Float16 ha = static_cast<_Float16>(static_cast<float>(static_cast<int>(a) * sc));
+                const _Float16 hc = static_cast<_Float16>(static_cast<float>(static_cast<int>(c) * sc));
+                o[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hc)) << 16);
+            }
+            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
+            if (sb_first && whalf == 0) {
+                sdm[sbp][wrow][0] = half_bits_to_float(hdr[set].x & 0xffffu);
+                sdm[sbp][wrow][1] = half_bits_to_float(hdr[set].x >> 16);
+                uint32_t m2[4];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj += 2) {
+                    int s0, m0, s1, m1;
+                    k4_scale_min(jj, hdr[set].y, hdr[set].z, hdr[set].w, s0, m0);
+                    k4_scale_min(jj + 1, hdr[set].y, hdr[set].z, hdr[set].w, s1, m1);
+                    const _Float16 h0 = static_cast<_Float16>(static_cast<float>(m0));
+                    const _Float16 h1 = static_cast<_Float16>(static_cast<float>(m1));
+                    m2[jj / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+                }
+                *reinterpret_cast<uint4*>(&smn[sbp][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
+            }
+        }
+        if (sb_first && tid < BM) {
+            *reinterpret_cast<uint4*>(&sp[sbp][0][tid * 8]) = pr[0];
+            *reinterpret_cast<uint4*>(&sp[sbp][1][tid * 8]) = pr[1];
+        }
+    };
+    // two K16 slices of one step (D starts each super-block at 0)
+    auto compute = [&](int stage, int buf) {
+        _Float16(*xs)[BM * 32] = xstage(stage);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            half8 ah[WM], al[WM], bw[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int o = swz(wm * 32 * WM + 32 * i + li, 2 * kk + lh);
+                ah[i] = *reinterpret_cast<const half8*>(&xs[0][o]);
+                al[i] = *reinterpret_cast<const half8*>(&xs[1][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                bw[j] = *reinterpret_cast<const half8*>(&ws[buf][swz(wn * 32 * WN + 32 * j + li, 2 * kk + lh)]);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], D[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], D[i][j], 0, 0, 0);
+        }
+    };
+    // acc += d D - dmin (P . m) for super-block parity sbp
+    auto fold = [&](int sbp) {
+        float dv[WN], mv[WN];
+        half4 mn[WN];
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int r = wn * 32 * WN + 32 * j + li;
+            dv[j] = sdm[sbp][r][0];
+            mv[j] = -sdm[sbp][r][1];
+            mn[j] = *reinterpret_cast<const half4*>(&smn[sbp][r * 8 + 4 * lh]);
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(D[i][j][r], dv[j], acc[i][j][r]);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int r = wm * 32 * WM + 32 * i + li;
+            const half4 ph = *reinterpret_cast<const half4*>(&sp[sbp][0][r * 8 + 4 * lh]);
+            const half4 pl = *reinterpret_cast<const half4*>(&sp[sbp][1][r * 8 + 4 * lh]);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+#pragma unroll
+                for (int r2 = 0; r2 < 16; ++r2) D[i][j][r2] = 0.0f;
+                D[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ph, mn[j], D[i][j], 0, 0, 0);
+                D[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(pl, mn[j], D[i][j], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[i][j][r] = fmaf(D[i][j][r], mv[j], acc[i][j][r]);
+                    D[i][j][r] = 0.0f;
+                }
+    };
+
+    // Prologue: steps 0-2 into ring stages 0-2, step 0's weights and its
+    // super-block's constants into LDS, step 1's weights in register set 1.
+    // Loads are issued in the order P, x0, w0, x1, w1, x2 so that vmcnt(8)
+    // covers the first ring stage.
+    gload_p(kb);
+    dma_x(0, kb);
+    gload_w(0, kb);
+    dma_x(1, kb + 32);
+    gload_w(1, kb + 32);
+    dma_x(2, kb + 64);
+    lstore(0, 0, kb, true, 0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXLoads + 2));
+    __syncthreads();
+    // Per step: (P at the 7th step of a super-block), the ring load 3 steps
+    // ahead, the weights 2 steps ahead; compute; the next step's weights into
+    // LDS; then a wait for the ring stage the next step reads, whose load was
+    // issued two steps ago: the loads issued since then are at most
+    // 2 + 2 (w) + 2 kXLoads (ring) + 2 (P).
+    for (int32_t sb = 0; sb < nsb; ++sb) {
+        const int32_t s0 = kb + sb * 256;
+        const int sbp = sb & 1;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const int32_t k0 = s0 + 32 * st;
+            const int buf = st & 1;  // 8 steps per super-block keep every parity static
+            if (st == 6) gload_p(s0 + 256);
+            dma_x((st + 3) & 3, k0 + 96);
+            gload_w(buf, k0 + 64);
+            // the two waves on each SIMD take the step's MFMA and VALU phases
+            // in opposite orders (staging writes the other weight buffer), so
+            // the barrier does not line up both waves' matrix-core work
+            if (wv < WAVES / 2) {
+                compute(st & 3, buf);
+                if (st == 7) fold(sbp);
+                if (k0 + 32 < ke) lstore(buf ^ 1, buf ^ 1, k0 + 32, st == 7, sbp ^ 1);
+            } else {
+                if (k0 + 32 < ke) lstore(buf ^ 1, buf ^ 1, k0 + 32, st == 7, sbp ^ 1);
+                compute(st & 3, buf);
+                if (st == 7) fold(sbp);
+            }
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXLoads + 4));
+            __syncthreads();
+        }
+    }
+    float* dst = gridDim.z > 1 ? part + static_cast<size_t>(blockIdx.z) * b * n : y;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int32_t mm = n0 + wn * 32 * WN + 32 * j + li;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rscale[t];
+            }
+        }
+}
+
 // y = sum over the split K ranges, added in range order (deterministic)
 __global__ __launch_bounds__(kThreads) void matbatch_reduce_kernel(const float* __restrict part, int32_t splits,
                                                                    size_t count, float* __restrict y) {
@@ -494,7 +814,7 @@ template <int TYPE>
 hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                        float* rscale, float* part, hipStream_t stream) {
     hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
-                       rscale);
+                       rscale, static_cast<_Float16*>(nullptr));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
@@ -503,6 +823,63 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
     else if (p.wn == 2) e = launch_mfma_t<TYPE, 2, 2>(w, xhl, rscale, b, k, n, y, p, part, stream);
     else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
     else e = launch_mfma_t<TYPE, 1, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
+    if (e != hipSuccess || p.splits == 1) return e;
+    const size_t count = static_cast<size_t>(b) * n;
+    size_t g = (count + kThreads - 1) / kThreads;
+    if (g > 4096) g = 4096;
+    hipLaunchKernelGGL(matbatch_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(kThreads), 0, stream, part,
+                       p.splits, count, y);
+    return hipGetLastError();
+}
+
+// Q4_K tiles: (waves along tokens, along rows, tiles per wave along each)
+struct Q4kPlan {
+    int cfg;  // 0: 128 x 256 (8 waves); 2: 128 x 128 (4 waves, one work-group per CU); 3: 64 x 64 (4 waves)
+    int32_t splits, kchunk;
+};
+
+// Measured on Q4_K 4096 x 4096, 4096 -> 14336 (B = 64, 256, 512) and the
+// B = 2048 prefill matrices: 128 x 256 tiles once they fill three quarters of
+// the CUs (B = 512 on the gate/up shape, every B = 2048 shape); 128 x 128 at
+// one work-group per CU when those do (B = 256 on 4096 -> 14336: 147 against
+// 181 us); otherwise 64 x 64 tiles with K split until about 512 work-groups
+// run (ranges of whole super-blocks).
+Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
+    auto tiles = [&](int bm, int bn) {
+        return static_cast<int64_t>((n + bn - 1) / bn) * ((b + bm - 1) / bm);
+    };
+    if (b >= 512 && tiles(128, 256) >= 192) return {0, 1, k};
+    if (b >= 128 && tiles(128, 128) >= 192) return {2, 1, k};
+    const int64_t t = tiles(64, 64);
+    int32_t splits = static_cast<int32_t>((512 + t - 1) / t);
+    if (splits > k / 256) splits = k / 256;
+    if (splits < 1) splits = 1;
+    const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
+    return {3, (k + kchunk - 1) / kchunk, kchunk};
+}
+
+template <int WM, int WN, int MW, int NW>
+hipError_t launch_q4k_t(const uint8_t* w, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
+                        int32_t k, int32_t n, float* y, const Q4kPlan& p, float* part, hipStream_t stream) {
+    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
+    const dim3 grid((n + BN - 1) / BN, (b + BM - 1) / BM, p.splits);
+    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, w,
+                       row_bytes(kQ4_K, k), xhl, pq, rscale, b, k, n, y, p.kchunk, part);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
+                      _Float16* pq, float* rscale, float* part, hipStream_t stream) {
+    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
+                       rscale, pq);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const Q4kPlan p = q4k_plan(b, k, n);
+    switch (p.cfg) {
+    case 0: e = launch_q4k_t<2, 2, 2, 4>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
+    case 2: e = launch_q4k_t<2, 2, 2, 2>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
+    default: e = launch_q4k_t<1, 1, 2, 2>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
+    }
     if (e != hipSuccess || p.splits == 1) return e;
     const size_t count = static_cast<size_t>(b) * n;
     size_t g = (count + kThreads - 1) / kThreads;
@@ -534,11 +911,17 @@ static size_t xh_bytes(int32_t b, int32_t k) {
 }
 static size_t rscale_bytes(int32_t b) { return (static_cast<size_t>(b) * sizeof(float) + 255) & ~static_cast<size_t>(255); }
 
+// Q4_K: the activation sums of each 32-block as fp16 pairs [B x K/256 x 16]
+static size_t pq_bytes(int32_t type, int32_t b, int32_t k) {
+    return type == kQ4_K ? (static_cast<size_t>(b) * (k / 256) * 16 * sizeof(_Float16) + 255) & ~static_cast<size_t>(255)
+                         : 0;
+}
+
 size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n) {
     if (type == kBF16) return 256;
-    const MfmaPlan p = mfma_plan(b, k, n);
-    const size_t parts = p.splits > 1 ? static_cast<size_t>(p.splits) * b * n * sizeof(float) : 0;
-    return xh_bytes(b, k) + rscale_bytes(b) + parts + 256;
+    const int32_t splits = type == kQ4_K ? q4k_plan(b, k, n).splits : mfma_plan(b, k, n).splits;
+    const size_t parts = splits > 1 ? static_cast<size_t>(splits) * b * n * sizeof(float) : 0;
+    return xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b) + parts + 256;
 }
 
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n,
@@ -555,14 +938,16 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     } else if ((wa & 3u) != 0) {
         return hipErrorInvalidValue;
     }
-    _Float16* xhl = static_cast<_Float16*>(workspace);
-    float* rscale = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k));
-    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + xh_bytes(b, k) + rscale_bytes(b));
+    char* ws = static_cast<char*>(workspace);
+    _Float16* xhl = reinterpret_cast<_Float16*>(ws);
+    _Float16* pq = reinterpret_cast<_Float16*>(ws + xh_bytes(b, k));
+    float* rscale = reinterpret_cast<float*>(ws + xh_bytes(b, k) + pq_bytes(type, b, k));
+    float* part = reinterpret_cast<float*>(ws + xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
     switch (type) {
     case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
     case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
-    case kQ4_K: return launch_mfma<kQ4_K>(w, x, b, k, n, y, xhl, rscale, part, stream);
+    case kQ4_K: return launch_q4k(w, x, b, k, n, y, xhl, pq, rscale, part, stream);
     case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream);
     case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
