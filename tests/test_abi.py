@@ -81,6 +81,85 @@ def test_exports_match_reference_signatures(built, ref):
     assert set(REF_CPP_EXPORTS) <= exported(built)
 
 
+# ---- prototypes: return type and parameter types, in order ---------------
+REF_CPP = pathlib.Path("/root/reference/csrc/gncx_llm_kernels.cpp")
+REF_CDEF = pathlib.Path("/root/reference/lua/gncx_streamer.lua")
+
+
+def _strip_comments(text: str) -> str:
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    return re.sub(r"--[^\n]*", " ", text) if "ffi.cdef" in text else text
+
+
+def _norm_type(t: str) -> str:
+    t = re.sub(r"\b(__restrict__|__restrict|restrict|extern|GNCX_LLM_API|GNCX_API)\b", " ", t)
+    t = t.replace('"C"', " ")
+    t = re.sub(r"\bstruct\s+", "", t)
+    t = re.sub(r"\b(GNCX\w+?)Struct\b", r"\1", t)  # the LuaJIT cdef's typedef names
+    t = re.sub(r"\s*\*\s*", "*", t)
+    return re.sub(r"\s+", " ", t).strip()
+
+
+def _param_type(p: str) -> str | None:
+    p = p.strip()
+    if p in ("", "void"):
+        return None
+    m = re.match(r"^(.*[\s*])([A-Za-z_]\w*)$", p)  # the type, then the parameter's name
+    return _norm_type(m.group(1) if m else p)
+
+
+def prototypes(text: str, prefix: str = "") -> dict[str, tuple[str, tuple[str, ...]]]:
+    """name -> (return type, parameter types) of every gncx_* prototype or
+    definition in C text; with prefix, only those whose declaration starts
+    with it (e.g. the export macro)."""
+    text = _strip_comments(text)
+    text = re.sub(r"^[ \t]*#[^\n]*", " ", text, flags=re.M)  # preprocessor lines
+    out = {}
+    for m in re.finditer(r"\b(gncx_\w+)\s*\(", text):
+        name = m.group(1)
+        # the declaration starts after the previous statement or block end
+        start = max(text.rfind(c, 0, m.start()) for c in ";{}]")
+        head = text[start + 1:m.start()]
+        if (prefix and prefix not in head) or "(" in head or "=" in head or "return" in head.split():
+            continue
+        depth, i = 1, m.end()
+        while depth and i < len(text):
+            depth += {"(": 1, ")": -1}.get(text[i], 0)
+            i += 1
+        if not text[i:].lstrip().startswith((";", "{")):
+            continue  # a call, not a declaration
+        params = text[m.end():i - 1]
+        out[name] = (_norm_type(head), tuple(t for t in (_param_type(p) for p in params.split(",")) if t is not None))
+    return out
+
+
+def test_header_prototypes_parse():
+    ours = prototypes(HEADER.read_text())
+    assert set(REF_CPP_EXPORTS) <= set(ours)
+    assert ours["gncx_xfold_universal_matvec"] == (
+        "void", ("const uint8_t*", "size_t", "int32_t", "const float*", "const GNCXCompactToken*", "int32_t",
+                 "int32_t", "float*", "GNCXTelemetryStats*"))
+
+
+@pytest.mark.skipif(not (REF_CPP.exists() and REF_CDEF.exists()), reason="reference sources absent")
+def test_prototypes_match_reference_definitions_and_ffi_cdef():
+    """Every one of the 48 reference entry points: the same return type and
+    the same parameter types in the same order in include/gncx_llm_core.h,
+    in the reference's GNCX_LLM_API definitions (csrc/gncx_llm_kernels.cpp)
+    and in the LuaJIT cdef that binds them (lua/gncx_streamer.lua:16-252)."""
+    ours = prototypes(HEADER.read_text())
+    ref = prototypes(REF_CPP.read_text(), prefix="GNCX_LLM_API")
+    lua = REF_CDEF.read_text()
+    cdef = prototypes(lua[lua.index("ffi.cdef[["):lua.index("]]", lua.index("ffi.cdef[["))])
+    assert set(ref) == set(REF_CPP_EXPORTS), sorted(set(ref) ^ set(REF_CPP_EXPORTS))
+    for name in REF_CPP_EXPORTS:
+        assert ours[name] == ref[name], (name, ours[name], ref[name])
+        if name in cdef:  # the streamer binds a subset (lua/gncx_streamer.lua:16-252)
+            assert ours[name] == cdef[name], (name, ours[name], cdef[name])
+    assert len(set(cdef) & set(REF_CPP_EXPORTS)) >= 40
+
+
 def _has_gpu(lib) -> bool:
     n = C.c_int(0)
     try:
