@@ -26,14 +26,18 @@
 // is no CPU fallback.  GNCX_ABORT_ON_ERROR=1 turns failures into abort().
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <linux/futex.h>
 #include <signal.h>
 #include <sys/mman.h>
+#include <sys/syscall.h>
 #include <sys/stat.h>
 #include <ucontext.h>
 #include <unistd.h>
 
 #include <algorithm>
 #include <array>
+#include <atomic>
+#include <cerrno>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -41,6 +45,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -130,10 +135,18 @@ struct DevWeight {
     uint8_t* d = nullptr;
     size_t bytes = 0;
     uint64_t sig = 0;
-    // inside a mapping from gncx_gla_map_readonly or a buffer from
-    // gncx_ram_alloc*: unmapping, freeing or copying into it drops this copy,
-    // so a hit needs neither the pointer query nor the content signature
-    bool tracked = false;
+    // where the host bytes live (tracked_host_range):
+    //   kMapped     inside a read-only mapping from gncx_gla_map_readonly:
+    //               unmapping drops this copy and nothing can write the
+    //               bytes, so a hit needs neither the pointer query nor the
+    //               content signature;
+    //   kRamBuffer  inside a buffer from gncx_ram_alloc*: freeing it or
+    //               copying into it drops this copy, but the caller may also
+    //               write it with plain stores, so a hit skips the pointer
+    //               query (the range is known host memory) and still checks
+    //               the content signature;
+    //   kUntracked  other host memory: both checks.
+    int trust = 0;
 };
 
 struct KVTwin {
@@ -200,13 +213,21 @@ void forget_weight(uintptr_t key) {
     g_rt.weights.erase(it);
 }
 
-bool tracked_host_range(const void* p, size_t bytes);
+enum WeightTrust : int { kUntracked = 0, kRamBuffer = 1, kMapped = 2 };
+int tracked_host_range(const void* p, size_t bytes);
 
 // Device view of `bytes` weight bytes at p (host: uploaded once, cached).
 const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where) {
     const uintptr_t key = reinterpret_cast<uintptr_t>(p);
     auto it = g_rt.weights.find(key);
-    if (it != g_rt.weights.end() && it->second.tracked && it->second.bytes >= bytes) return it->second.d;
+    if (it != g_rt.weights.end() && it->second.bytes >= bytes) {
+        if (it->second.trust == kMapped) return it->second.d;
+        if (it->second.trust == kRamBuffer) {
+            if (it->second.sig == host_signature(p, it->second.bytes)) return it->second.d;
+            forget_weight(key);
+            it = g_rt.weights.end();
+        }
+    }
     if (is_device_ptr(p)) return p;
     if (it != g_rt.weights.end()) {
         if (it->second.bytes >= bytes && it->second.sig == host_signature(p, it->second.bytes))
@@ -216,7 +237,7 @@ const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where)
     DevWeight w;
     w.bytes = bytes;
     w.sig = host_signature(p, bytes);
-    w.tracked = tracked_host_range(p, bytes);
+    w.trust = tracked_host_range(p, bytes);
     void* d = nullptr;
     // 256 B aligned, plus slack so no vector load near the end leaves the allocation
     if (!check(hipMalloc(&d, round_up(bytes, 256) + 256), where)) return nullptr;
@@ -554,15 +575,17 @@ HostBuffer* buffer_at(uintptr_t a) {
 // mappings from gncx_gla_map_readonly: base -> bytes
 std::map<uintptr_t, size_t> g_maps;
 
-bool tracked_host_range(const void* p, size_t bytes) {
+int tracked_host_range(const void* p, size_t bytes) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     auto it = g_maps.upper_bound(a);
     if (it != g_maps.begin()) {
         --it;
-        if (a + bytes <= it->first + it->second) return true;
+        if (a + bytes <= it->first + it->second) return kMapped;
     }
     const HostBuffer* b = buffer_at(a);
-    return b && a >= reinterpret_cast<uintptr_t>(b->ptr) && a + bytes <= reinterpret_cast<uintptr_t>(b->ptr) + b->bytes;
+    return b && a >= reinterpret_cast<uintptr_t>(b->ptr) && a + bytes <= reinterpret_cast<uintptr_t>(b->ptr) + b->bytes
+               ? kRamBuffer
+               : kUntracked;
 }
 
 size_t page_bytes() {
@@ -604,7 +627,57 @@ bool make_host(HostBuffer& b, const char* where) {
 
 void on_segv(int sig, siginfo_t* si, void* uc);
 
+// Host faults on lazy buffers are resolved off the signal path.  The SIGSEGV
+// handler only does async-signal-safe work: it writes a pointer to a request
+// on its own stack into a pipe and sleeps on a futex in that request.  A
+// resolver thread reads the request, takes the call lock like any library
+// call, makes the buffer's pages current (which may wait on the device, copy
+// and change protections), and wakes the faulting thread, which then retries
+// its access or, for a fault that is not a lazy buffer's, chains to the
+// handler installed before.  So the faulting thread may hold any lock (a
+// libc or HIP-runtime lock included) when it faults: the work that needs
+// locks runs in another thread.  Only a fault taken by the library itself
+// while it holds the call lock is resolved in the handler, as the resolver
+// could never get that lock; the library touches lazy buffers' host pages
+// only through their device copies, so that case is not expected.
+struct FaultRequest {
+    uintptr_t addr;
+    int write;
+    std::atomic<int> done;  // 0 while the resolver works, then 1
+    int handled;
+};
+int g_fault_pipe[2] = {-1, -1};
+ssize_t write_fd(int fd, const void* p, size_t n) { return ::write(fd, p, n); }
+
+bool resolve_fault(uintptr_t a, bool write);
+
+void fault_resolver() {
+    for (;;) {
+        FaultRequest* r = nullptr;
+        const ssize_t got = read(g_fault_pipe[0], &r, sizeof(r));
+        if (got != static_cast<ssize_t>(sizeof(r))) {
+            if (got < 0 && errno == EINTR) continue;
+            return;
+        }
+        bool handled;
+        {
+            std::lock_guard<CallLock> lk(g_mu);
+            handled = resolve_fault(r->addr, r->write != 0);
+        }
+        r->handled = handled ? 1 : 0;
+        r->done.store(1, std::memory_order_release);
+        syscall(SYS_futex, reinterpret_cast<int*>(&r->done), FUTEX_WAKE_PRIVATE, 1, nullptr, nullptr, 0);
+    }
+}
+
 void ensure_segv_handler() {
+    if (g_fault_pipe[0] < 0) {
+        if (pipe2(g_fault_pipe, O_CLOEXEC) != 0) {
+            g_fault_pipe[0] = g_fault_pipe[1] = -1;
+            return;  // no resolver: lazy_ptr reports the failure
+        }
+        std::thread(fault_resolver).detach();
+    }
     struct sigaction cur;
     sigaction(SIGSEGV, nullptr, &cur);
     if ((cur.sa_flags & SA_SIGINFO) && cur.sa_sigaction == on_segv) return;
@@ -616,57 +689,71 @@ void ensure_segv_handler() {
     sigaction(SIGSEGV, &sa, &g_prev_segv);
 }
 
-// A host access to a lazy buffer's protected page: make the host copy
-// current (read-only), or read-write for a write to a read-only page; any
-// other fault goes to the handler that was installed before.
+// A host access to a lazy buffer's protected page (runs in normal thread
+// context, with the call lock held): make the host copy current and
+// read-only, or read-write for a write to a read-only page.  False when the
+// address is not a protected page of a lazy buffer.
+bool resolve_fault(uintptr_t a, bool write) {
+    HostBuffer* b = buffer_at(a);
+    if (!b || b->pinned || !b->twin || b->home == Home::kHost) return false;
+    const uintptr_t pg = page_bytes();
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(b->ptr) & ~(pg - 1);
+    const uintptr_t hi = (reinterpret_cast<uintptr_t>(b->ptr) + b->bytes + pg - 1) & ~(pg - 1);
+    if (a < lo || a >= hi) return false;
+    const char* where = "lazy host buffer access";
+    if (b->home == Home::kDevice && b->stage && b->staged == b->writes) {
+        // the copy queued when the last writer returned
+        if (check(hipEventSynchronize(b->staged_ev), where) && protect(*b, PROT_READ | PROT_WRITE)) {
+            std::memcpy(b->ptr, b->stage, b->bytes);
+            b->misses = 0;
+            b->staged = ~0ull;
+            b->home = protect(*b, PROT_READ) ? Home::kShared : Home::kHost;
+            return true;
+        }
+    }
+    if (b->home == Home::kDevice) {
+        if (b->bytes <= kReadbackMax) b->readback = true;
+        if (!download(*b, where)) {
+            (void)protect(*b, PROT_READ | PROT_WRITE);  // the data is lost; keep the program running
+            b->home = Home::kHost;
+        } else if (protect(*b, PROT_READ)) {
+            b->home = Home::kShared;
+        } else {
+            b->home = Home::kHost;
+        }
+        return true;
+    }
+    if (!write) return true;  // a read that faulted before another thread made the pages readable
+    if (!protect(*b, PROT_READ | PROT_WRITE)) return false;
+    b->home = Home::kHost;
+    return true;
+}
+
 void on_segv(int sig, siginfo_t* si, void* uc) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(si->si_addr);
     // x86-64 page-fault error code: bit 1 set for a write
     const bool write = (static_cast<ucontext_t*>(uc)->uc_mcontext.gregs[REG_ERR] & 2) != 0;
     bool handled = false;
-    auto handle = [&]() {
-        HostBuffer* b = buffer_at(a);
-        if (!b || b->pinned || !b->twin || b->home == Home::kHost) return;
-        const uintptr_t pg = page_bytes();
-        const uintptr_t lo = reinterpret_cast<uintptr_t>(b->ptr) & ~(pg - 1);
-        const uintptr_t hi = (reinterpret_cast<uintptr_t>(b->ptr) + b->bytes + pg - 1) & ~(pg - 1);
-        if (a < lo || a >= hi) return;
-        const char* where = "lazy host buffer access";
-        if (b->home == Home::kDevice && b->stage && b->staged == b->writes) {
-            // the copy queued when the last writer returned
-            if (check(hipEventSynchronize(b->staged_ev), where) && protect(*b, PROT_READ | PROT_WRITE)) {
-                std::memcpy(b->ptr, b->stage, b->bytes);
-                b->misses = 0;
-                b->staged = ~0ull;
-                b->home = protect(*b, PROT_READ) ? Home::kShared : Home::kHost;
-                handled = true;
-                return;
-            }
-        }
-        if (b->home == Home::kDevice) {
-            if (b->bytes <= kReadbackMax) b->readback = true;
-            if (!download(*b, where)) {
-                (void)protect(*b, PROT_READ | PROT_WRITE);  // the data is lost; keep the program running
-                b->home = Home::kHost;
-            } else if (protect(*b, PROT_READ)) {
-                b->home = Home::kShared;
-            } else {
-                b->home = Home::kHost;
-            }
-        } else if (!write) {
-            // a read that faulted before another thread made the pages readable
-        } else if (protect(*b, PROT_READ | PROT_WRITE)) {
-            b->home = Home::kHost;
-        } else {
-            return;
-        }
-        handled = true;
-    };
     if (t_in_call) {
-        handle();  // the library itself touched the buffer: it holds the lock
-    } else {
-        std::lock_guard<CallLock> lk(g_mu);
-        handle();
+        handled = resolve_fault(a, write);  // the library itself holds the call lock
+    } else if (g_fault_pipe[1] >= 0) {
+        const int saved_errno = errno;
+        FaultRequest req;
+        req.addr = a;
+        req.write = write ? 1 : 0;
+        req.done.store(0, std::memory_order_relaxed);
+        req.handled = 0;
+        FaultRequest* rp = &req;
+        ssize_t put;
+        do {
+            put = write_fd(g_fault_pipe[1], &rp, sizeof(rp));
+        } while (put < 0 && errno == EINTR);
+        if (put == static_cast<ssize_t>(sizeof(rp))) {
+            while (req.done.load(std::memory_order_acquire) == 0)
+                syscall(SYS_futex, reinterpret_cast<int*>(&req.done), FUTEX_WAIT_PRIVATE, 0, nullptr, nullptr, 0);
+            handled = req.handled != 0;
+        }
+        errno = saved_errno;
     }
     if (handled) return;
     if (g_prev_segv.sa_flags & SA_SIGINFO) {
@@ -737,6 +824,11 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
         b->home = Home::kHost;  // the pages hold the data
     }
     ensure_segv_handler();
+    if (g_fault_pipe[1] < 0) {
+        set_error(where, "the lazy host buffers' fault resolver could not start", -1);
+        ok = false;
+        return nullptr;
+    }
     if (b->home == Home::kHost) {
         // uploaded for writes too: a call that writes nothing keeps the data
         if (!upload(*b, where)) {

@@ -74,6 +74,41 @@ def test_weights_in_ram_buffer_follow_copy_chunk(lib, oracle):
         lib.gncx_ram_free(h)
 
 
+def test_weights_in_ram_buffer_rewritten_by_plain_stores(lib, oracle):
+    """A gncx_ram buffer is writable memory: weights rewritten there with plain
+    stores (not gncx_ram_copy_chunk) are found changed by the content
+    signature, as for any host memory.  A rewrite that touches none of the
+    signature's probes is the caller's to announce with
+    gncx_hip_weight_forget (weights are immutable in the reference's
+    contract), after which the new bytes are used."""
+    k, n = 2048, 96
+    w = synth.make_weights(Q4_K, n, k, seed=43)
+    w2 = synth.make_weights(Q4_K, n, k, seed=44)
+    w3 = _changed_weights(w2)
+    x = synth.make_activations(1, k, seed=45)
+    want = [oracle.matvec(Q4_K, v, x, k, n) for v in (w, w2, w3)]
+    assert rel_l2(want[1], want[2]) > 20 * TOL
+    off = 4096 + 32
+    h = lib.gncx_ram_alloc_colored(off + w.size, 2, 4, 3)
+    assert h
+    try:
+        base = lib.gncx_ram_get_ptr(h)
+        view = np.ctypeslib.as_array((C.c_uint8 * (off + w.size)).from_address(base))
+        y = np.zeros(n, np.float32)
+        for i, v in enumerate((w, w2)):
+            view[off:off + v.size] = v  # plain stores into the buffer
+            lib.gncx_xfold_universal_matvec(base, off, Q4_K, ptr(x), None, k, n, ptr(y), None)
+            gncx.check(lib)
+            assert rel_l2(y, want[i]) < TOL, i
+        view[off:off + w3.size] = w3
+        lib.gncx_hip_weight_forget(base + off)
+        lib.gncx_xfold_universal_matvec(base, off, Q4_K, ptr(x), None, k, n, ptr(y), None)
+        gncx.check(lib)
+        assert rel_l2(y, want[2]) < TOL
+    finally:
+        lib.gncx_ram_free(h)
+
+
 def test_weights_in_mapped_file_are_dropped_on_unmap(lib, oracle, tmp_path):
     k, n = 2048, 64
     w = synth.make_weights(Q4_K, n, k, seed=43)

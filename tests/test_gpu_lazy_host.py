@@ -174,3 +174,70 @@ def test_lazy_decode_equals_synchronous_host_buffers(lib, torch_mod, tmp_path):
         lib.gncx_hip_set_host_coherence(0)
         lib.gncx_hip_weight_forget(None)
         lib.gncx_hip_kv_forget(None)
+
+
+def test_lazy_fault_inside_lock_holding_libc_call(lib, oracle, lazy, tmp_path):
+    """The first host access to a buffer the device holds happens inside
+    fwrite, which holds the stream's lock while it copies the bytes into its
+    own buffer (1200 bytes: below the stdio buffer, so the copy is a user-space
+    read that faults, not a write(2) that would fail with EFAULT).  The fault
+    is resolved by the library's resolver thread, not in the handler, and the
+    file holds the device's result."""
+    k, n = 512, 300
+    w = synth.make_weights(Q4_K, n, k, seed=71)
+    _, x = lazy(k, 1)
+    _, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=72)
+    want = oracle.matvec(Q4_K, w, x.copy(), k, n)
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    gncx.check(lib)
+    libc = C.CDLL(None)
+    libc.fopen.restype = C.c_void_p
+    libc.fopen.argtypes = [C.c_char_p, C.c_char_p]
+    libc.fwrite.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
+    libc.fclose.argtypes = [C.c_void_p]
+    path = tmp_path / "y.bin"
+    fp = libc.fopen(str(path).encode(), b"wb")
+    assert fp
+    assert libc.fwrite(y.ctypes.data, 4, n, fp) == n
+    assert libc.fclose(fp) == 0
+    got = np.fromfile(path, dtype=np.float32)
+    assert rel_l2(got, want) < 1e-3
+    assert np.array_equal(got, y)
+
+
+def test_lazy_fault_while_another_thread_calls_the_library(lib, oracle, lazy):
+    """A host read of a device-held buffer faults while another thread keeps
+    the library busy with synchronous calls of its own: the resolver waits
+    its turn for the call lock like any call, nothing deadlocks, and both
+    threads get correct results."""
+    import threading
+
+    k, n = 1024, 400
+    w = synth.make_weights(Q4_K, n, k, seed=73)
+    _, x = lazy(k, 1)
+    _, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=74)
+    want = oracle.matvec(Q4_K, w, x.copy(), k, n)
+    w2 = synth.make_weights(Q4_K, 256, 2048, seed=75)
+    x2 = synth.make_activations(1, 2048, seed=76)
+    want2 = oracle.matvec(Q4_K, w2, x2, 2048, 256)
+    errs = []
+
+    def busy():
+        y2 = np.zeros(256, np.float32)  # ordinary host memory: every call waits for its result
+        for _ in range(200):
+            lib.gncx_xfold_universal_matvec(ptr(w2), 0, Q4_K, ptr(x2), None, 2048, 256, ptr(y2), None)
+            errs.append(rel_l2(y2, want2))
+
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    gncx.check(lib)
+    t = threading.Thread(target=busy)
+    t.start()
+    got = y.copy()  # faults while busy() calls the library
+    t.join(timeout=60)
+    assert not t.is_alive()
+    gncx.check(lib)
+    assert rel_l2(got, want) < 1e-3
+    assert len(errs) == 200 and max(errs) < 1e-3
+    lib.gncx_hip_weight_forget(ptr(w2))
