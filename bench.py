@@ -32,6 +32,12 @@ import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 HBM_PEAK_GBPS = 8000.0
+# sources the headline GEMV kernel is built from: a traffic figure measured on
+# other sources is stale and is not reported
+GEMV_SOURCES = ["gnc-x_amd/csrc/gemv.hip", "gnc-x_amd/csrc/gncx_slots.h", "gnc-x_amd/csrc/gncx_device.h",
+                "gnc-x_amd/csrc/gncx_formats.h"]
+TRAFFIC_JSON = ROOT / "profiles" / "traffic_gemv_q4k_4096x14336.json"
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0  # profiles/hbm_counter_calibration.md
 MFMA_FP16_PEAK = 2.5e15  # dense fp16 matrix-core FLOP/s of one MI355X
 METRIC = "Q4_K GEMV HBM GB/s (% of peak); decode tok/s, Qwen3-8B-shaped, 1 GPU"
 
@@ -76,6 +82,53 @@ class HipEvents:
     def destroy(self, evs):
         for e in evs:
             self.hip.hipEventDestroy(e)
+
+
+def sources_sha256(paths) -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for p in paths:
+        h.update(p.encode())
+        h.update((ROOT / p).read_bytes())
+    return h.hexdigest()
+
+
+def headline_traffic():
+    """(HBM bytes per launch or None, note): the figure of TRAFFIC_JSON when
+    it was measured on the current GEMV sources."""
+    if not TRAFFIC_JSON.exists():
+        return None, "no counter measurement"
+    t = json.loads(TRAFFIC_JSON.read_text())
+    if t.get("source_sha256") != sources_sha256(GEMV_SOURCES):
+        return None, "counter measurement is of other GEMV sources (stale)"
+    return t.get("hbm_bytes_per_launch"), "FETCH_SIZE x %.1f + WRITE_SIZE x %.1f per dispatch, median" % (
+        FETCH_SCALE, WRITE_SCALE)
+
+
+def write_traffic_json(fetch_csv: str, write_csv: str, commands: list) -> dict:
+    """profiles/traffic_*.json from the counter CSVs of two rocprofv3 --pmc
+    runs (FETCH_SIZE, then WRITE_SIZE) of the headline loop: the median
+    reading of the GEMV's dispatches, scaled to bytes, stamped with the hash
+    of the GEMV sources it was measured on."""
+    import csv
+
+    def med(path, counter):
+        v = sorted(float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+                   if r["Counter_Name"] == counter and "gemv" in r["Kernel_Name"])
+        return v[len(v) // 2], len(v)
+    f, nf = med(fetch_csv, "FETCH_SIZE")
+    w, _ = med(write_csv, "WRITE_SIZE")
+    hbm = int(round((f * FETCH_SCALE + w * WRITE_SCALE) * 1024))
+    alg = 4096 // 256 * 144 * 14336 + 4 * 4096 + 4 * 14336
+    out = {"kernel": "the headline GEMV (gemv_band_kernel, Q4_K 4096 -> 14336)",
+           "workload": "gncx_xfold_universal_matvec Q4_K 4096->14336, device pointers, 16 rotated weight copies",
+           "hbm_bytes_per_launch": hbm, "algorithmic_bytes_per_launch": alg, "ratio": round(hbm / alg, 4),
+           "fetch_size_kib_per_dispatch_median": f, "write_size_kib_per_dispatch_median": w,
+           "fetch_scale": FETCH_SCALE, "write_scale": WRITE_SCALE, "dispatches": nf, "commands": commands,
+           "scale_from": "hbm_counter_calibration.md",
+           "sources": GEMV_SOURCES, "source_sha256": sources_sha256(GEMV_SOURCES)}
+    TRAFFIC_JSON.write_text(json.dumps(out, indent=1) + "\n")
+    return out
 
 
 def gemv_bytes(pkg, t: int, k: int, n: int) -> int:
@@ -413,12 +466,22 @@ def main() -> int:
     ap.add_argument("--decode-only", choices=["streamer", "fused", "native"], default=None,
                     help="only the decode measurement: prefill the prompt (fused), then --decode-tokens greedy "
                          "tokens through one call sequence, and print its rate (for kernel profiles)")
+    ap.add_argument("--traffic-json", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic_gemv_q4k_4096x14336.json from the counter CSVs of two rocprofv3 "
+                         "--pmc runs (FETCH_SIZE, then WRITE_SIZE) of 'bench.py --no-extra --no-cpu --no-decode' "
+                         "and exit")
     ap.add_argument("--matbatch-only", action="store_true",
                     help="only the matbatch measurements (for kernel profiles)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     args = ap.parse_args()
+    if args.traffic_json:
+        cmd = "rocprofv3 --pmc {c} --output-format csv -d gpurun_out/traffic -o {o} -- python3 bench.py " \
+              "--steps 200 --warmup 20 --no-extra --no-cpu --no-decode"
+        print(json.dumps(write_traffic_json(*args.traffic_json, [cmd.format(c="FETCH_SIZE", o="fetch"),
+                                                                 cmd.format(c="WRITE_SIZE", o="write")])))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (GEMV would shard by output rows, "
               "attention by KV head)", file=sys.stderr)
@@ -451,10 +514,7 @@ def main() -> int:
     t, k, n = pkg.Q4_K, 4096, 14336
     head = time_gemv(pkg, lib, torch, t, k, n, args.steps, args.warmup, args.copies)
     achieved = head["bytes"] / (head["kernel_us_mean"] * 1e-6) / 1e9
-    traffic = None
-    tf = ROOT / "profiles" / "traffic_gemv_q4k_4096x14336.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+    traffic, traffic_note = headline_traffic()
 
     extra = {}
     if not args.no_extra:
@@ -501,7 +561,7 @@ def main() -> int:
                    "bytes_per_step": head["bytes"], "weight_copies_rotated": args.copies,
                    "inputs": "resident in HBM (device pointers through the reference C-ABI)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "kernel_us_mean": round(head["kernel_us_mean"], 3),
                      "timing": "HIP events around the back-to-back timed loop on the library stream"},
         "cpu_baseline": cpu,
