@@ -142,8 +142,9 @@ struct Slot<kQ4_K> {
     };
     struct Act {
         uint4 xl0, xl1, xh0, xh1;  // q of sub-blocks 2c (low nibbles) and 2c+1 (high)
-        float dl, dh;
-        int sl, sh;
+        float dl, dh;              // their block scales
+        float bl, bh;              // block scale x sum of q
+        uint32_t sel;              // byte selector of sub-blocks 2c, 2c+1
     };
     static constexpr int32_t slots(int32_t k) { return (k / 256) * 4; }
     template <class Row>
@@ -156,7 +157,9 @@ struct Slot<kQ4_K> {
     }
     __device__ static __forceinline__ void load_act(Act& a, int s, const int8_t* __restrict q,
                                                     const ActMeta* __restrict meta) {
-        const int ab = (s >> 2) * 8 + 2 * (s & 3);
+#pragma clang fp contract(off)
+        const int c = s & 3;
+        const int ab = (s >> 2) * 8 + 2 * c;
         const int8_t* xq = q + static_cast<size_t>(ab) * 32;
         a.xl0 = lds16(xq);
         a.xl1 = lds16(xq + 16);
@@ -165,12 +168,12 @@ struct Slot<kQ4_K> {
         const ActMeta ml = meta[ab], mh = meta[ab + 1];
         a.dl = ml.d;
         a.dh = mh.d;
-        a.sl = ml.sum;
-        a.sh = mh.sum;
+        a.bl = ml.d * static_cast<float>(ml.sum);
+        a.bh = mh.d * static_cast<float>(mh.sum);
+        a.sel = 0x0c0c0000u | static_cast<uint32_t>(2 * c) | (static_cast<uint32_t>(2 * c + 1) << 8);
     }
-    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int s) {
+    __device__ static __forceinline__ float dot(const Frag& f, const Act& a, int) {
 #pragma clang fp contract(off)
-        const int c = s & 3;
         const uint32_t M = 0x0f0f0f0fu;
         int dl = 0, dh = 0;
         dl = sdot4(f.w0.x & M, a.xl0.x, dl); dh = sdot4((f.w0.x >> 4) & M, a.xh0.x, dh);
@@ -181,15 +184,29 @@ struct Slot<kQ4_K> {
         dl = sdot4(f.w1.y & M, a.xl1.y, dl); dh = sdot4((f.w1.y >> 4) & M, a.xh1.y, dh);
         dl = sdot4(f.w1.z & M, a.xl1.z, dl); dh = sdot4((f.w1.z >> 4) & M, a.xh1.z, dh);
         dl = sdot4(f.w1.w & M, a.xl1.w, dl); dh = sdot4((f.w1.w >> 4) & M, a.xh1.w, dh);
-        int s1, m1, s2, m2;
-        k4_scale_min(2 * c, f.hdr.y, f.hdr.z, f.hdr.w, s1, m1);
-        k4_scale_min(2 * c + 1, f.hdr.y, f.hdr.z, f.hdr.w, s2, m2);
+        // The eight 6-bit scales and mins of the super-block (get_scale_min_k4,
+        // cpp:1112-1120), one per byte with sub-block j in byte j of {lo, hi}
+        // -- sub-blocks 0-3 take the low 6 bits of bytes 0-3 / 4-7, sub-blocks
+        // 4-7 a nibble of bytes 8-11 plus the top 2 bits of bytes 0-3 / 4-7 --
+        // then the two of this slot picked by one byte permute.  The slot's
+        // share is regrouped from the reference's per-block
+        //   dx_j (d sc_j isum_j - dmin m_j sum_j)
+        // as d (sc_1 dx_1 isum_1 + sc_2 dx_2 isum_2) - dmin (m_1 b_1 + m_2 b_2)
+        // with b_j = dx_j sum_j formed once per launch: every term stays exact
+        // up to its fp32 roundings, and the VALU work per row drops by a quarter.
+        const uint32_t y = f.hdr.y, z = f.hdr.z, w = f.hdr.w;
+        const uint32_t sc_lo = y & 0x3f3f3f3fu, mn_lo = z & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (w & M) | ((y >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((w >> 4) & M) | ((z >> 2) & 0x30303030u);
+        const uint32_t sc = __builtin_amdgcn_perm(sc_hi, sc_lo, a.sel);
+        const uint32_t mn = __builtin_amdgcn_perm(mn_hi, mn_lo, a.sel);
         const float d = half_bits_to_float(f.hdr.x & 0xffffu);
         const float dmin = half_bits_to_float(f.hdr.x >> 16);
-        const float d1 = d * static_cast<float>(s1), dm1 = dmin * static_cast<float>(m1);
-        const float d2 = d * static_cast<float>(s2), dm2 = dmin * static_cast<float>(m2);
-        return a.dl * (d1 * static_cast<float>(dl) - dm1 * static_cast<float>(a.sl)) +
-               a.dh * (d2 * static_cast<float>(dh) - dm2 * static_cast<float>(a.sh));
+        const float s1 = static_cast<float>(sc & 0xffu), s2 = static_cast<float>((sc >> 8) & 0xffu);
+        const float m1 = static_cast<float>(mn & 0xffu), m2 = static_cast<float>((mn >> 8) & 0xffu);
+        const float sum = __builtin_fmaf(s2 * a.dh, static_cast<float>(dh), (s1 * a.dl) * static_cast<float>(dl));
+        const float mins = __builtin_fmaf(m2, a.bh, m1 * a.bl);
+        return __builtin_fmaf(-dmin, mins, d * sum);
     }
 };
 
