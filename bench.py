@@ -266,6 +266,21 @@ def time_attention(lib, torch, H, KV, hd, ctx, sw, steps, copies):
     return {"us_per_step": wall_us, "bytes": nbytes, "gbps": nbytes / (wall_us * 1e-6) / 1e9}
 
 
+ATTENTION_SHAPES = {  # name: (query heads, KV heads, head_dim, context, sliding window, KV copies rotated)
+    "gqa32x8_ctx512": (32, 8, 128, 512, 0, 160), "gqa32x8_ctx4096": (32, 8, 128, 4096, 0, 16),
+    "gqa32x8_ctx32768": (32, 8, 128, 32768, 0, 3), "gqa32x8_swa1024": (32, 8, 128, 2048, 1024, 64),
+    "mqa32x1_ctx32768": (32, 1, 128, 32768, 0, 16),
+}
+
+
+def attention_extras(lib, torch, steps=50):
+    att = {}
+    for name, (H, KV, hd, ctx, sw, cp) in ATTENTION_SHAPES.items():
+        r = time_attention(lib, torch, H, KV, hd, ctx, sw, steps, cp)
+        att[name] = {"us_per_step": round(r["us_per_step"], 2), "gbps": round(r["gbps"], 1)}
+    return att
+
+
 def time_decode(pkg, lib, torch, prompt_len, n_tokens, seed=1):
     """Qwen3-8B-shaped random-init model (decode.QWEN3_8B): prefill a random
     prompt through the streamer's prefill call sequence, then greedy decode
@@ -472,6 +487,8 @@ def main() -> int:
                          "and exit")
     ap.add_argument("--matbatch-only", action="store_true",
                     help="only the matbatch measurements (for kernel profiles)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the attention-step measurements (for kernel profiles)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device copies of MIB MiB (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -510,6 +527,9 @@ def main() -> int:
     if args.matbatch_only:
         print(json.dumps({"matbatch": matbatch_extras(pkg, lib, torch)}), flush=True)
         return 0
+    if args.attention_only:
+        print(json.dumps({"attention": attention_extras(lib, torch)}), flush=True)
+        return 0
 
     t, k, n = pkg.Q4_K, 4096, 14336
     head = time_gemv(pkg, lib, torch, t, k, n, args.steps, args.warmup, args.copies)
@@ -530,15 +550,7 @@ def main() -> int:
             gem[name] = {"gbps_wall": round(r["gbps_wall"], 1), "gbps_kernel": round(r["gbps_kernel"], 1),
                          "kernel_us": round(r["kernel_us_mean"], 2), "frac_kernel": round(r["gbps_kernel"] / HBM_PEAK_GBPS, 4)}
         extra["gemv"] = gem
-        att = {}
-        for name, (H, KV, hd, ctx, sw, cp) in {
-            "gqa32x8_ctx512": (32, 8, 128, 512, 0, 160), "gqa32x8_ctx4096": (32, 8, 128, 4096, 0, 16),
-            "gqa32x8_ctx32768": (32, 8, 128, 32768, 0, 3), "gqa32x8_swa1024": (32, 8, 128, 2048, 1024, 64),
-            "mqa32x1_ctx32768": (32, 1, 128, 32768, 0, 16),
-        }.items():
-            r = time_attention(lib, torch, H, KV, hd, ctx, sw, 50, cp)
-            att[name] = {"us_per_step": round(r["us_per_step"], 2), "gbps": round(r["gbps"], 1)}
-        extra["attention"] = att
+        extra["attention"] = attention_extras(lib, torch)
         extra["matbatch"] = matbatch_extras(pkg, lib, torch)
     if not args.no_decode:
         extra["decode_qwen3_8b"] = time_decode(pkg, lib, torch, args.decode_prompt, args.decode_tokens)
