@@ -757,7 +757,7 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p)
 // max / sum pass, so the kernel waits on memory about once.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxSplit = 4096;
-constexpr int kMergeU = 8;
+constexpr int kMergeU = 32;
 
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict part_o,
                                                                    const float* __restrict part_ml, int32_t n_split,
