@@ -547,11 +547,29 @@ struct HostBuffer {
     uint64_t staged = ~0ull;  // value of writes the staged copy holds
     int misses = 0;
     bool queued = false;      // in g_readbacks
+    int prot = PROT_READ | PROT_WRITE;  // current protection of the pages
+    // a buffer the host rewrites after every upload (the residual stream):
+    // once seen kKeepRwAfter times its pages stay read-write after an upload,
+    // which costs one upload per device read instead of a fault per rewrite
+    bool just_uploaded = false;
+    int rewrites = 0;
+    bool keep_rw = false;
+    // a buffer the host reads after every device write (a projection the
+    // host adds to its residual, the logits): once seen kSyncReturnAfter times
+    // in a row, the writing call copies it home before it returns, with no
+    // page protection and no fault; every kSyncReturnRecheck such calls the
+    // fault path runs once again to see that the host still reads it
+    int hits = 0;
+    bool sync_return = false;
+    int sync_returns = 0;
 };
 std::map<uintptr_t, HostBuffer*> g_bufs;  // by block address
 std::vector<HostBuffer*> g_readbacks;     // written by the current call
 constexpr size_t kReadbackMax = size_t{1} << 20;
 constexpr int kReadbackMisses = 4;
+constexpr int kKeepRwAfter = 2;
+constexpr int kSyncReturnAfter = 2;
+constexpr int kSyncReturnRecheck = 64;
 int g_lazy = -1;                           // -1: not read from the environment yet
 struct sigaction g_prev_segv;
 
@@ -594,10 +612,13 @@ size_t page_bytes() {
 }
 
 bool protect(HostBuffer& b, int prot) {
+    if (b.prot == prot) return true;
     const uintptr_t pg = page_bytes();
     const uintptr_t lo = reinterpret_cast<uintptr_t>(b.ptr) & ~(pg - 1);
     const uintptr_t hi = (reinterpret_cast<uintptr_t>(b.ptr) + b.bytes + pg - 1) & ~(pg - 1);
-    return mprotect(reinterpret_cast<void*>(lo), hi - lo, prot) == 0;
+    if (mprotect(reinterpret_cast<void*>(lo), hi - lo, prot) != 0) return false;
+    b.prot = prot;
+    return true;
 }
 
 // device copy -> host pages (made read-write first); waits for queued work
@@ -708,6 +729,8 @@ bool resolve_fault(uintptr_t a, bool write) {
             b->misses = 0;
             b->staged = ~0ull;
             b->home = protect(*b, PROT_READ) ? Home::kShared : Home::kHost;
+            b->just_uploaded = false;
+            if (++b->hits >= kSyncReturnAfter) b->sync_return = true;
             return true;
         }
     }
@@ -726,6 +749,8 @@ bool resolve_fault(uintptr_t a, bool write) {
     if (!write) return true;  // a read that faulted before another thread made the pages readable
     if (!protect(*b, PROT_READ | PROT_WRITE)) return false;
     b->home = Home::kHost;
+    if (b->just_uploaded && ++b->rewrites >= kKeepRwAfter) b->keep_rw = true;
+    b->just_uploaded = false;
     return true;
 }
 
@@ -767,11 +792,43 @@ void on_segv(int sig, siginfo_t* si, void* uc) {
     g_prev_segv.sa_handler(sig);
 }
 
+// A sync-return buffer the call wrote: its copy home, made before the call
+// returns.  False (buffer left device-owned and inaccessible, the fault path
+// takes over) when a step fails.
+bool sync_return(HostBuffer& b, const char* where) {
+    if (!b.stage) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, b.bytes, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        b.stage = static_cast<uint8_t*>(p);
+    }
+    if (!check(hipMemcpyAsync(b.stage, b.twin, b.bytes, hipMemcpyDeviceToHost, g_rt.stream), where) ||
+        !check(hipStreamSynchronize(g_rt.stream), where) || !protect(b, PROT_READ | PROT_WRITE))
+        return false;
+    std::memcpy(b.ptr, b.stage, b.bytes);
+    b.home = Home::kHost;
+    b.staged = ~0ull;
+    return true;
+}
+
 void queue_readbacks() {
     if (g_readbacks.empty()) return;
     for (HostBuffer* b : g_readbacks) {
         b->queued = false;
         if (b->home != Home::kDevice || !b->readback) continue;
+        if (b->sync_return) {
+            const bool recheck = ++b->sync_returns % kSyncReturnRecheck == 0;
+            if (!recheck && sync_return(*b, "lazy host buffer copy home")) continue;
+            // the fault path once more: the host must still read it to come back here
+            b->sync_return = false;
+            b->hits = 0;
+            if (!protect(*b, PROT_NONE)) {
+                (void)make_host(*b, "lazy host buffer copy home");  // the host copy, current
+                continue;
+            }
+        }
         if (b->staged != ~0ull && ++b->misses >= kReadbackMisses) {  // the host left the last copy unread
             b->readback = false;
             continue;
@@ -835,20 +892,29 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
             ok = false;
             return nullptr;
         }
-        if (!protect(*b, PROT_READ)) {
-            set_error(where, "mprotect failed on a lazy host buffer", -1);
-            ok = false;
-            return nullptr;
+        if (b->keep_rw && !(access & kWr)) {
+            // pages stay read-write and the buffer host-owned: the next
+            // device read uploads again, a host rewrite costs nothing
+        } else {
+            if (!protect(*b, PROT_READ)) {
+                set_error(where, "mprotect failed on a lazy host buffer", -1);
+                ok = false;
+                return nullptr;
+            }
+            b->home = Home::kShared;
+            b->just_uploaded = true;
         }
-        b->home = Home::kShared;
     }
     if ((access & kWr) && b->home != Home::kDevice) {
-        if (!protect(*b, PROT_NONE)) {
+        // a sync-return buffer keeps its pages as they are: the writing call
+        // copies it home before it returns (queue_readbacks)
+        if (!b->sync_return && !protect(*b, PROT_NONE)) {
             set_error(where, "mprotect failed on a lazy host buffer", -1);
             ok = false;
             return nullptr;
         }
         b->home = Home::kDevice;
+        b->just_uploaded = false;
     }
     if (access & kWr) {
         ++b->writes;

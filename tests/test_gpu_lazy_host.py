@@ -67,6 +67,37 @@ def test_lazy_matvec_follows_host_reads_and_writes(lib, oracle, lazy):
     assert rel_l2(y, 2 * want) < 1e-3 and y[10] == 246.0
 
 
+def test_lazy_adaptive_policies_keep_results_exact(lib, oracle, lazy):
+    """Buffers whose use settles into a pattern switch policy: an input the
+    host rewrites after every upload keeps read-write pages (and is uploaded
+    again for each device read); an output the host reads after every call
+    is copied home before the writing call returns (and once every 64 such
+    calls goes through the fault path again).  Results stay exact through
+    the switches, through calls whose output the host skips, and through
+    host writes into a buffer that the device then reads."""
+    k, n = 512, 256
+    w = synth.make_weights(Q4_K, n, k, seed=71)
+    _, x = lazy(k, 1)
+    _, y = lazy(n, 2)
+    x[:] = synth.make_activations(1, k, seed=72)
+    for rnd in range(80):  # past both switch points and one re-check of the copy home
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+        gncx.check(lib)
+        assert rel_l2(y, oracle.matvec(Q4_K, w, x.copy(), k, n)) < 1e-3, rnd
+        x[rnd % k] += 0.25  # rewritten after each upload
+    for rnd in range(3):    # outputs the host does not read
+        x[::5] *= -1.0
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, x.ctypes.data, None, k, n, y.ctypes.data, None)
+    gncx.check(lib)
+    want = oracle.matvec(Q4_K, w, x.copy(), k, n)
+    assert rel_l2(y, want) < 1e-3
+    y[:16] = 7.0            # host write into the output, then a device read of it
+    want[:16] = 7.0
+    lib.gncx_hip_vec_add(y.ctypes.data, y.ctypes.data, n)
+    gncx.check(lib)
+    assert rel_l2(y, 2 * want) < 1e-3 and np.all(y[:16] == 14.0)
+
+
 def test_lazy_elementwise_outputs_stay_on_device(lib, golden, lazy):
     """SwiGLU and GeGLU chained through lazy buffers, one in place; the
     outputs are read on the host only at the end."""
