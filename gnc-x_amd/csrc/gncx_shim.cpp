@@ -65,12 +65,15 @@ using namespace gncx;
 // Before the lock is released, a call's writes to lazy host buffers that the
 // host reads back get their copies to the host queued (queue_readbacks).
 thread_local bool t_in_call = false;
+thread_local bool t_keep_pending = false;  // set around the lock of a matvec call
 void queue_readbacks();
+bool flush_pending(const char* where);
 struct CallLock {
     std::mutex m;
     void lock() {
         m.lock();
         t_in_call = true;
+        if (!t_keep_pending) (void)flush_pending("deferred matvec");
     }
     void unlock() {
         queue_readbacks();
@@ -383,8 +386,74 @@ void add_telemetry(GNCXTelemetryStats* t, uint64_t macs, uint64_t canceled, uint
     t->xfold_bucket_merges += merges;
 }
 
+// Deferred matvecs (lazy host buffers only).  The streamer issues the Q, K
+// and V projections, and the gate and up projections, as consecutive matvec
+// calls on one normalised vector whose outputs only the device reads.  Such
+// calls are gathered (same input, type and in_dim, at most kMaxGemvMats) and
+// issued as one multi-matrix launch -- the results are those of separate
+// launches bit for bit -- when the lock is next taken by any other call (or
+// by a matvec that does not join them), including the fault resolver, so
+// every consumer of a deferred output, device or host, finds it issued
+// first.  A deferred call reports success; a failure of the gathered launch
+// is reported by the call that issues it.
+// the shape and alignment rules of launch_gemv (a call that breaks them is
+// not deferred, so its error is reported by the call itself)
+bool check_gemv_args(int32_t type, const uint8_t* w, const float* x, int32_t k) {
+    if (k <= 0 || k > kMaxGemvK || !type_supported(type)) return false;
+    if (type != kBF16 && k % 32 != 0) return false;
+    if ((type == kQ4_K || type == kQ6_K) && k % 256 != 0) return false;
+    if (type == kBF16 && k % 8 != 0) return false;
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w), xa = reinterpret_cast<uintptr_t>(x);
+    if (xa & 15u) return false;
+    if (type == kQ4_K || type == kBF16) return (wa & 15u) == 0 && (row_bytes(type, k) & 15u) == 0;
+    return (wa & 3u) == 0;
+}
+
+struct PendingGemv {
+    int32_t count = 0, type = 0, k = 0;
+    const float* x = nullptr;
+    const uint8_t* w[kMaxGemvMats] = {};
+    int32_t n[kMaxGemvMats] = {};
+    float* y[kMaxGemvMats] = {};
+};
+PendingGemv g_pend;
+
+bool flush_pending(const char* where) {
+    if (g_pend.count == 0) return true;
+    const int32_t c = g_pend.count;
+    g_pend.count = 0;
+    return check(launch_gemv_multi(g_pend.type, c, g_pend.w, g_pend.n, g_pend.x, g_pend.k, g_pend.y, g_rt.stream),
+                 where);
+}
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + bn && y < x + an;
+}
+
+// true when y = W x joins (or starts) the pending group instead of launching
+bool defer_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32_t n, float* y) {
+    const size_t yb = sizeof(float) * static_cast<size_t>(n);
+    bool joins = g_pend.count > 0 && g_pend.count < kMaxGemvMats && g_pend.type == type && g_pend.k == k &&
+                 g_pend.x == x && !overlaps(y, yb, x, sizeof(float) * static_cast<size_t>(k));
+    for (int32_t i = 0; joins && i < g_pend.count; ++i)
+        joins = !overlaps(y, yb, g_pend.y[i], sizeof(float) * static_cast<size_t>(g_pend.n[i]));
+    if (!joins) {
+        if (!flush_pending("deferred matvec")) return false;
+        if (overlaps(y, yb, x, sizeof(float) * static_cast<size_t>(k))) return false;
+        g_pend.type = type;
+        g_pend.k = k;
+        g_pend.x = x;
+    }
+    g_pend.w[g_pend.count] = w;
+    g_pend.n[g_pend.count] = n;
+    g_pend.y[g_pend.count] = y;
+    ++g_pend.count;
+    return true;
+}
+
 bool matvec_impl(const uint8_t* base, size_t off, int32_t type, const float* in_vec, int32_t in_dim, int32_t out_dim, float* out_vec, bool reuse_x,
-                 float softcap, const char* where) {
+                 float softcap, const char* where, bool may_defer = false) {
     if (!ensure_runtime(where)) return false;
     const size_t wbytes = row_bytes(type, in_dim) * static_cast<size_t>(out_dim);
     const uint8_t* w = device_weights(base + off, wbytes, where);
@@ -403,6 +472,10 @@ bool matvec_impl(const uint8_t* base, size_t off, int32_t type, const float* in_
     bool host_out = false;
     float* y = out_target(out_vec, static_cast<size_t>(out_dim), g_rt.y, host_out, where);
     if (!y) return false;
+    if (may_defer && !host_out && softcap == 0.0f && x == in_vec && check_gemv_args(type, w, x, in_dim) &&
+        defer_gemv(type, w, x, in_dim, out_dim, y))
+        return true;
+    if (!flush_pending(where)) return false;
     if (!check(launch_gemv(type, w, x, in_dim, out_dim, y, g_rt.stream), where)) return false;
     if (softcap > 0.0f && !check(launch_softcap(y, out_dim, softcap, g_rt.stream), where)) return false;
     return finish_out(out_vec, y, static_cast<size_t>(out_dim), host_out, where);
@@ -715,6 +788,7 @@ void ensure_segv_handler() {
 // read-only, or read-write for a write to a read-only page.  False when the
 // address is not a protected page of a lazy buffer.
 bool resolve_fault(uintptr_t a, bool write) {
+    (void)flush_pending("lazy host buffer access");
     HostBuffer* b = buffer_at(a);
     if (!b || b->pinned || !b->twin || b->home == Home::kHost) return false;
     const uintptr_t pg = page_bytes();
@@ -854,6 +928,14 @@ void queue_readbacks() {
     g_readbacks.clear();
 }
 
+// a lazy buffer whose data only the device reads back (no host read-back
+// pattern seen): a write to it may be deferred
+bool device_only_lazy(const void* p) {
+    if (g_lazy != 1 || !p) return false;
+    const HostBuffer* b = buffer_at(reinterpret_cast<uintptr_t>(p));
+    return b && !b->pinned && !b->readback && !b->sync_return;
+}
+
 // [p, p + bytes) inside a lazy buffer: its address in the device copy, after
 // making that copy current (read) and taking ownership for the device
 // (write).  Any other pointer comes back unchanged.  A range that leaves its
@@ -886,7 +968,10 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
         ok = false;
         return nullptr;
     }
-    if (b->home == Home::kHost) {
+    // a sync-return buffer that the call overwrites whole is not uploaded
+    // first (its next copy home replaces the pages anyway)
+    const bool whole_output = access == kWr && b->sync_return && a == lo && bytes == b->bytes;
+    if (b->home == Home::kHost && !whole_output) {
         // uploaded for writes too: a call that writes nothing keeps the data
         if (!upload(*b, where)) {
             ok = false;
@@ -1050,8 +1135,12 @@ bool attention_impl(const AttnCall& c, const char* where) {
 GNCX_API void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
                                           const float* in_vec, const GNCXCompactToken* in_tokens, int32_t in_dim,
                                           int32_t out_dim, float* out_vec, GNCXTelemetryStats* telemetry) {
+    t_keep_pending = true;
     std::lock_guard<CallLock> lk(g_mu);
+    t_keep_pending = false;
     bool ok = true;
+    // an output only the device reads may wait in the pending group
+    const bool may_defer = device_only_lazy(out_vec);
     in_vec = lazy_ptr(in_vec, dim_count(in_dim), kRd, ok, "gncx_xfold_universal_matvec");
     out_vec = lazy_ptr(out_vec, dim_count(out_dim), kWr, ok, "gncx_xfold_universal_matvec");
     if (!ok) return;
@@ -1074,7 +1163,7 @@ GNCX_API void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weigh
     }
     if (type_supported(ggml_type) && out_dim > 0 && in_dim > 0)
         matvec_impl(mmap_base, weight_abs_offset, ggml_type, in_vec, in_dim, out_dim, out_vec, reuse,
-                    0.0f, "gncx_xfold_universal_matvec");
+                    0.0f, "gncx_xfold_universal_matvec", may_defer);
     const uint64_t macs = static_cast<uint64_t>(in_dim) * static_cast<uint64_t>(out_dim);
     add_telemetry(telemetry, macs, canceled, static_cast<uint64_t>(in_dim / 32) * static_cast<uint64_t>(out_dim));
 }
