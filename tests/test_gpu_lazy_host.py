@@ -98,6 +98,46 @@ def test_lazy_adaptive_policies_keep_results_exact(lib, oracle, lazy):
     assert rel_l2(y, 2 * want) < 1e-3 and np.all(y[:16] == 14.0)
 
 
+def test_lazy_deferred_matvecs_issue_before_every_consumer(lib, oracle, lazy):
+    """Consecutive matvecs on one device-held input are gathered into one
+    launch (at most four matrices; a differing input, type or in_dim starts a
+    new group).  Every consumer finds them issued: a host read of an output,
+    a later device call reading it, and a matvec whose input is a gathered
+    output.  Results equal the oracle's."""
+    k = 512
+    ns = [96, 160, 256, 64, 128]
+    ws = [synth.make_weights(Q4_K, n, k, seed=80 + i) for i, n in enumerate(ns)]
+    _, x = lazy(k, 1)
+    _, xn = lazy(k, 2)
+    ys = [lazy(n, 3 + i)[1] for i, n in enumerate(ns)]
+    x[:] = synth.make_activations(1, k, seed=90)
+    # xn: a device-held input (the output of a device call), as the streamer's normalised vector
+    lib.gncx_hip_vec_add(xn.ctypes.data, x.ctypes.data, k)
+    for i, w in enumerate(ws):  # five on one input: a group of four, then one more
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, xn.ctypes.data, None, k, ns[i], ys[i].ctypes.data, None)
+    gncx.check(lib)
+    xs = xn.copy()  # host read of the input: every pending matvec is issued first
+    for i, w in enumerate(ws):
+        assert rel_l2(ys[i], oracle.matvec(Q4_K, w, xs, k, ns[i])) < 1e-3, i
+    # gathered outputs (fresh buffers) consumed by a device call, then read on the host
+    us = [lazy(ns[i], 10 + i)[1] for i in range(3)]
+    for i in range(3):
+        lib.gncx_xfold_universal_matvec(ptr(ws[i]), 0, Q4_K, xn.ctypes.data, None, k, ns[i], us[i].ctypes.data, None)
+    lib.gncx_hip_vec_add(us[0].ctypes.data, us[0].ctypes.data, ns[0])
+    gncx.check(lib)
+    assert rel_l2(us[0], 2 * oracle.matvec(Q4_K, ws[0], xs, k, ns[0])) < 1e-3
+    assert rel_l2(us[2], oracle.matvec(Q4_K, ws[2], xs, k, ns[2])) < 1e-3
+    # a matvec whose input is a gathered output (k = 256 = ns[2])
+    wc = synth.make_weights(Q4_K, 64, 256, seed=95)
+    _, u3 = lazy(ns[2], 14)
+    _, z = lazy(64, 15)
+    lib.gncx_xfold_universal_matvec(ptr(ws[2]), 0, Q4_K, xn.ctypes.data, None, k, ns[2], u3.ctypes.data, None)
+    lib.gncx_xfold_universal_matvec(ptr(wc), 0, Q4_K, u3.ctypes.data, None, 256, 64, z.ctypes.data, None)
+    gncx.check(lib)
+    y2 = oracle.matvec(Q4_K, ws[2], xs, k, ns[2])
+    assert rel_l2(z, oracle.matvec(Q4_K, wc, y2, 256, 64)) < 1e-3
+
+
 def test_lazy_elementwise_outputs_stay_on_device(lib, golden, lazy):
     """SwiGLU and GeGLU chained through lazy buffers, one in place; the
     outputs are read on the host only at the end."""
