@@ -65,15 +65,19 @@ using namespace gncx;
 // Before the lock is released, a call's writes to lazy host buffers that the
 // host reads back get their copies to the host queued (queue_readbacks).
 thread_local bool t_in_call = false;
-thread_local bool t_keep_pending = false;  // set around the lock of a matvec call
+// Deferred work of lazy-host-buffer calls (gathered matvecs, an attention
+// prologue) is issued when the lock is next taken, except for the kind the
+// locking call may join (t_keep, set around its lock).
+enum KeepPending { kKeepNone = 0, kKeepGemv = 1, kKeepPrologue = 2 };
+thread_local int t_keep = kKeepNone;
 void queue_readbacks();
-bool flush_pending(const char* where);
+bool flush_pending(const char* where, int keep = kKeepNone);
 struct CallLock {
     std::mutex m;
     void lock() {
         m.lock();
         t_in_call = true;
-        if (!t_keep_pending) (void)flush_pending("deferred matvec");
+        (void)flush_pending("deferred call", t_keep);
     }
     void unlock() {
         queue_readbacks();
@@ -418,12 +422,52 @@ struct PendingGemv {
 };
 PendingGemv g_pend;
 
-bool flush_pending(const char* where) {
+bool flush_gemv(const char* where) {
     if (g_pend.count == 0) return true;
     const int32_t c = g_pend.count;
     g_pend.count = 0;
     return check(launch_gemv_multi(g_pend.type, c, g_pend.w, g_pend.n, g_pend.x, g_pend.k, g_pend.y, g_rt.stream),
                  where);
+}
+
+// Deferred attention prologue (lazy host buffers only).  The streamer follows
+// its Q/K/V projections with heads-RMSNorm of q, heads-RMSNorm of k, RoPE of
+// both and the attention step, each a call of its own on device-held q and k.
+// These are recorded in that order and, when the attention step on the same q
+// and k follows, run as the attention kernel's fused prologue (bit-identical
+// with the separate kernels), the prologue results written back to q and k
+// as the separate calls leave them.  Any other call issues the recorded ones
+// as the separate kernels first.
+struct PendingPrologue {
+    int stage = 0;  // 1: q normalised, 2: k normalised, 4: both rotated
+    float* q = nullptr;
+    float* k = nullptr;
+    const float* gq = nullptr;
+    const float* gk = nullptr;
+    int32_t nq = 0, nk = 0, hd = 0;
+    float eps_q = 0.0f, eps_k = 0.0f;
+    RopeTable rope{};
+};
+PendingPrologue g_pro;
+
+bool flush_prologue(const char* where) {
+    if (g_pro.stage == 0) return true;
+    const int st = g_pro.stage;
+    g_pro.stage = 0;
+    if ((st & 1) && !check(launch_rmsnorm_heads(g_pro.q, g_pro.gq, g_pro.nq, g_pro.hd, g_pro.eps_q, g_rt.stream), where))
+        return false;
+    if ((st & 2) && !check(launch_rmsnorm_heads(g_pro.k, g_pro.gk, g_pro.nk, g_pro.hd, g_pro.eps_k, g_rt.stream), where))
+        return false;
+    if ((st & 4) && !check(launch_rope(g_pro.q, g_pro.k, g_pro.rope, g_pro.nq, g_pro.nk, g_pro.hd, g_rt.stream), where))
+        return false;
+    return true;
+}
+
+bool flush_pending(const char* where, int keep) {
+    bool ok = true;
+    if (keep != kKeepGemv) ok = flush_gemv(where) && ok;
+    if (keep != kKeepPrologue) ok = flush_prologue(where) && ok;
+    return ok;
 }
 
 bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
@@ -439,7 +483,7 @@ bool defer_gemv(int32_t type, const uint8_t* w, const float* x, int32_t k, int32
     for (int32_t i = 0; joins && i < g_pend.count; ++i)
         joins = !overlaps(y, yb, g_pend.y[i], sizeof(float) * static_cast<size_t>(g_pend.n[i]));
     if (!joins) {
-        if (!flush_pending("deferred matvec")) return false;
+        if (!flush_gemv("deferred matvec")) return false;
         if (overlaps(y, yb, x, sizeof(float) * static_cast<size_t>(k))) return false;
         g_pend.type = type;
         g_pend.k = k;
@@ -475,7 +519,7 @@ bool matvec_impl(const uint8_t* base, size_t off, int32_t type, const float* in_
     if (may_defer && !host_out && softcap == 0.0f && x == in_vec && check_gemv_args(type, w, x, in_dim) &&
         defer_gemv(type, w, x, in_dim, out_dim, y))
         return true;
-    if (!flush_pending(where)) return false;
+    if (!flush_gemv(where)) return false;
     if (!check(launch_gemv(type, w, x, in_dim, out_dim, y, g_rt.stream), where)) return false;
     if (softcap > 0.0f && !check(launch_softcap(y, out_dim, softcap, g_rt.stream), where)) return false;
     return finish_out(out_vec, y, static_cast<size_t>(out_dim), host_out, where);
@@ -1135,9 +1179,9 @@ bool attention_impl(const AttnCall& c, const char* where) {
 GNCX_API void gncx_xfold_universal_matvec(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
                                           const float* in_vec, const GNCXCompactToken* in_tokens, int32_t in_dim,
                                           int32_t out_dim, float* out_vec, GNCXTelemetryStats* telemetry) {
-    t_keep_pending = true;
+    t_keep = kKeepGemv;
     std::lock_guard<CallLock> lk(g_mu);
-    t_keep_pending = false;
+    t_keep = kKeepNone;
     bool ok = true;
     // an output only the device reads may wait in the pending group
     const bool may_defer = device_only_lazy(out_vec);
@@ -1252,7 +1296,9 @@ GNCX_API void gncx_mqa_attention_step_ext(const float* q_vec, const float* k_vec
                                           float* k_cache_layer, float* v_cache_layer, int32_t pos, int32_t n_heads,
                                           int32_t n_kv_heads, int32_t head_dim, float attn_scale,
                                           int32_t sliding_window, int32_t write_kv, float* out_attn_vec) {
+    t_keep = kKeepPrologue;
     std::lock_guard<CallLock> lk(g_mu);
+    t_keep = kKeepNone;
     const char* where = "gncx_mqa_attention_step_ext";
     bool ok = true;
     const size_t qn = dim_count(n_heads) * dim_count(head_dim), kvn = dim_count(n_kv_heads) * dim_count(head_dim);
@@ -1263,9 +1309,29 @@ GNCX_API void gncx_mqa_attention_step_ext(const float* q_vec, const float* k_vec
     k_cache_layer = lazy_ptr(k_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
     v_cache_layer = lazy_ptr(v_cache_layer, (dim_count(pos) + 1) * kvn, cache_access, ok, where);
     out_attn_vec = lazy_ptr(out_attn_vec, qn, kWr, ok, where);
-    if (!ok) return;
+    if (!ok) {
+        (void)flush_prologue(where);
+        return;
+    }
     AttnCall c{q_vec, k_vec, v_vec, k_cache_layer, v_cache_layer, pos, n_heads, n_kv_heads, head_dim, attn_scale,
                sliding_window, write_kv, out_attn_vec};
+    // the recorded prologue of this q and k runs inside the attention kernel
+    const int st = g_pro.stage;
+    if ((st == 3 || st == 4 || st == 7) && const_cast<float*>(q_vec) == g_pro.q && const_cast<float*>(k_vec) == g_pro.k &&
+        n_heads == g_pro.nq && n_kv_heads == g_pro.nk && head_dim == g_pro.hd && write_kv && v_vec &&
+        (!(st & 3) || g_pro.eps_q == g_pro.eps_k)) {
+        g_pro.stage = 0;
+        c.norm_qk = (st & 3) ? 1 : 0;
+        c.q_gamma = (st & 3) ? g_pro.gq : nullptr;
+        c.k_gamma = (st & 3) ? g_pro.gk : nullptr;
+        c.eps = g_pro.eps_q;
+        c.rope = (st & 4) ? &g_pro.rope : nullptr;
+        c.q_back = g_pro.q;  // the prologue results, as the separate calls leave q and k
+        c.k_back = g_pro.k;
+        attention_impl(c, where);
+        return;
+    }
+    if (!flush_prologue(where)) return;
     attention_impl(c, where);
 }
 
@@ -1281,19 +1347,52 @@ GNCX_API void gncx_mqa_attention_step(const float* q_vec, const float* k_vec, co
 // cpp:895-953
 GNCX_API void gncx_rmsnorm_inplace_heads(float* vec, const uint8_t* mmap_base, size_t norm_weight_offset,
                                          int32_t has_weight, int32_t n_heads, int32_t head_dim, float eps) {
+    t_keep = kKeepPrologue;
     std::lock_guard<CallLock> lk(g_mu);
+    t_keep = kKeepNone;
     const char* where = "gncx_rmsnorm_inplace_heads";
-    if (n_heads <= 0 || head_dim <= 0 || !ensure_runtime(where)) return;
+    if (n_heads <= 0 || head_dim <= 0 || !ensure_runtime(where)) {
+        (void)flush_prologue(where);
+        return;
+    }
     const float* g = nullptr;
     if (has_weight) {
         g = reinterpret_cast<const float*>(
             device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(head_dim), where));
-        if (!g) return;
+        if (!g) {
+            (void)flush_prologue(where);
+            return;
+        }
     }
     const size_t n = static_cast<size_t>(n_heads) * head_dim;
     bool ok = true;
+    const bool may_defer = device_only_lazy(vec) && head_dim <= 2 * kMaxRopeHalf;
     vec = lazy_ptr(vec, n, kRd | kWr, ok, where);
-    if (!ok) return;
+    if (!ok) {
+        (void)flush_prologue(where);
+        return;
+    }
+    if (may_defer && is_device_ptr(vec)) {
+        if (g_pro.stage == 0) {
+            g_pro.q = vec;
+            g_pro.gq = g;
+            g_pro.nq = n_heads;
+            g_pro.hd = head_dim;
+            g_pro.eps_q = eps;
+            g_pro.stage = 1;
+            return;
+        }
+        if (g_pro.stage == 1 && head_dim == g_pro.hd &&
+            !overlaps(vec, sizeof(float) * n, g_pro.q, sizeof(float) * static_cast<size_t>(g_pro.nq) * g_pro.hd)) {
+            g_pro.k = vec;
+            g_pro.gk = g;
+            g_pro.nk = n_heads;
+            g_pro.eps_k = eps;
+            g_pro.stage = 3;
+            return;
+        }
+    }
+    if (!flush_prologue(where)) return;
     const bool host = !is_device_ptr(vec);
     float* d = host ? const_cast<float*>(stage_in(vec, n, g_rt.q, where)) : vec;
     if (!d) return;
@@ -1306,27 +1405,58 @@ GNCX_API void gncx_apply_rope_xor11_ext(float* q_vec, float* k_vec, GNCXCompactT
                                         const uint8_t* mmap_base, size_t rope_freqs_offset, int32_t has_rope_freqs,
                                         int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t pos,
                                         float freq_base) {
+    t_keep = kKeepPrologue;
     std::lock_guard<CallLock> lk(g_mu);
+    t_keep = kKeepNone;
     const char* where = "gncx_apply_rope_xor11_ext";
-    if (!ensure_runtime(where)) return;
+    if (!ensure_runtime(where)) {
+        (void)flush_prologue(where);
+        return;
+    }
     const int32_t half = head_dim / 2;
     std::array<float, kMaxRopeHalf> fac{};
     const float* factors = nullptr;
     if (has_rope_freqs) {
-        if (half > kMaxRopeHalf || !read_factors(mmap_base, rope_freqs_offset, half, fac, where)) return;
+        if (half > kMaxRopeHalf || !read_factors(mmap_base, rope_freqs_offset, half, fac, where)) {
+            (void)flush_prologue(where);
+            return;
+        }
         factors = fac.data();
     }
     RopeTable t;
     if (!rope_table(pos, head_dim, freq_base, factors, t)) {
         set_error(where, "head_dim must be even and at most 512", -1);
+        (void)flush_prologue(where);
         return;
     }
     const size_t qn = q_vec ? static_cast<size_t>(n_heads) * head_dim : 0;
     const size_t kn = k_vec ? static_cast<size_t>(n_kv_heads) * head_dim : 0;
     bool ok = true;
+    const bool may_defer = q_vec && k_vec && device_only_lazy(q_vec) && device_only_lazy(k_vec);
     q_vec = lazy_ptr(q_vec, qn, kRd | kWr, ok, where);
     k_vec = lazy_ptr(k_vec, kn, kRd | kWr, ok, where);
-    if (!ok) return;
+    if (!ok) {
+        (void)flush_prologue(where);
+        return;
+    }
+    if (may_defer && is_device_ptr(q_vec) && is_device_ptr(k_vec) &&
+        (g_pro.stage == 3 ? q_vec == g_pro.q && k_vec == g_pro.k && n_heads == g_pro.nq &&
+                                n_kv_heads == g_pro.nk && head_dim == g_pro.hd
+                          : g_pro.stage == 0 && !overlaps(q_vec, sizeof(float) * qn, k_vec, sizeof(float) * kn))) {
+        g_pro.q = q_vec;
+        g_pro.k = k_vec;
+        g_pro.nq = n_heads;
+        g_pro.nk = n_kv_heads;
+        g_pro.hd = head_dim;
+        g_pro.rope = t;
+        g_pro.stage |= 4;
+        // telemetry phase flip of the rotated half (cpp:1818-1823, 1829-1831)
+        if (q_tokens)
+            for (int32_t h = 0; h < n_heads; ++h)
+                for (int32_t i = 0; i < half; ++i) q_tokens[h * head_dim + i + half].phase_2bit ^= 0x03u;
+        return;
+    }
+    if (!flush_prologue(where)) return;
     const bool hq = q_vec && !is_device_ptr(q_vec), hk = k_vec && !is_device_ptr(k_vec);
     float* dq = q_vec ? (hq ? const_cast<float*>(stage_in(q_vec, qn, g_rt.q, where)) : q_vec) : nullptr;
     float* dk = k_vec ? (hk ? const_cast<float*>(stage_in(k_vec, kn, g_rt.k, where)) : k_vec) : nullptr;

@@ -138,6 +138,71 @@ def test_lazy_deferred_matvecs_issue_before_every_consumer(lib, oracle, lazy):
     assert rel_l2(z, oracle.matvec(Q4_K, wc, y2, 256, 64)) < 1e-3
 
 
+@pytest.mark.parametrize("interrupt", [False, True])
+def test_lazy_deferred_attention_prologue(lib, lazy, interrupt):
+    """heads-RMSNorm of q and of k, RoPE of both and the attention step on
+    device-held q and k run as the attention kernel's fused prologue in lazy
+    mode; q, k and the cache row are left as the separate calls leave them
+    (bit for bit) and the output matches.  interrupt: a host read of q after
+    its normalisation issues the recorded work as separate kernels."""
+    H, KV, hd, ctx = 32, 8, 128, 200
+    pos, eps, base, scale = ctx - 1, 1e-6, 1e6, 1 / np.sqrt(hd)
+    rng = np.random.default_rng(5)
+    q0 = rng.standard_normal(H * hd, dtype=np.float32)
+    k0 = rng.standard_normal(KV * hd, dtype=np.float32)
+    v0 = rng.standard_normal(KV * hd, dtype=np.float32)
+    kc0 = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    vc0 = rng.standard_normal((ctx, KV * hd), dtype=np.float32)
+    norms = np.concatenate([synth.make_norm_gamma(hd, 1), synth.make_norm_gamma(hd, 2)]).astype(np.float32)
+
+    def run(qh, kh, vh, kch, vch, outh, read_q=None):
+        lib.gncx_rmsnorm_inplace_heads(qh, ptr(norms), 0, 1, H, hd, eps)
+        if read_q is not None:
+            read_q()
+        lib.gncx_rmsnorm_inplace_heads(kh, ptr(norms), hd * 4, 1, KV, hd, eps)
+        lib.gncx_apply_rope_xor11_ext(qh, kh, None, None, 0, 0, H, KV, hd, pos, base)
+        lib.gncx_mqa_attention_step_ext(qh, kh, vh, kch, vch, pos, H, KV, hd, scale, 0, 1, outh)
+        gncx.check(lib)
+
+    # synchronous host buffers: the separate kernels
+    lib.gncx_hip_set_host_coherence(0)
+    try:
+        q1, k1, kc1, vc1 = q0.copy(), k0.copy(), kc0.copy(), vc0.copy()
+        out1 = np.zeros(H * hd, np.float32)
+        run(ptr(q1), ptr(k1), ptr(v0), ptr(kc1), ptr(vc1), ptr(out1))
+        lib.gncx_hip_kv_forget(None)
+    finally:
+        lib.gncx_hip_set_host_coherence(1)
+    # lazy buffers, q and k produced on the device
+    _, qs = lazy(H * hd, 1)
+    _, ks = lazy(KV * hd, 2)
+    _, q = lazy(H * hd, 3)
+    _, k = lazy(KV * hd, 4)
+    _, v = lazy(KV * hd, 5)
+    _, kc = lazy(ctx * KV * hd, 6)
+    _, vc = lazy(ctx * KV * hd, 7)
+    _, out = lazy(H * hd, 8)
+    qs[:], ks[:], v[:] = q0, k0, v0
+    kc[:], vc[:] = kc0.reshape(-1), vc0.reshape(-1)
+    lib.gncx_hip_vec_add(q.ctypes.data, qs.ctypes.data, H * hd)  # q = 0 + q0, device-held
+    lib.gncx_hip_vec_add(k.ctypes.data, ks.ctypes.data, KV * hd)
+    seen = []
+    run(q.ctypes.data, k.ctypes.data, v.ctypes.data, kc.ctypes.data, vc.ctypes.data, out.ctypes.data,
+        (lambda: seen.append(q.copy())) if interrupt else None)
+    assert np.array_equal(q, q1) and np.array_equal(k, k1)
+    assert np.array_equal(kc.reshape(ctx, -1), kc1) and np.array_equal(vc.reshape(ctx, -1), vc1)
+    assert rel_l2(out, out1) < 1e-6
+    if interrupt:
+        q_norm = q0.copy()
+        lib.gncx_hip_set_host_coherence(0)
+        try:
+            lib.gncx_rmsnorm_inplace_heads(ptr(q_norm), ptr(norms), 0, 1, H, hd, eps)
+        finally:
+            lib.gncx_hip_set_host_coherence(1)
+        assert np.array_equal(seen[0], q_norm)
+    lib.gncx_hip_kv_forget(None)
+
+
 def test_lazy_elementwise_outputs_stay_on_device(lib, golden, lazy):
     """SwiGLU and GeGLU chained through lazy buffers, one in place; the
     outputs are read on the host only at the end."""
