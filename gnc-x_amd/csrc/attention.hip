@@ -266,8 +266,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
                     s += qf[h][c].x * kf[c].x + qf[h][c].y * kf[c].y + qf[h][c].z * kf[c].z + qf[h][c].w * kf[c].w;
-#pragma unroll
-                for (int o = 1; o < LPT; o <<= 1) s += __shfl_xor(s, o, 64);
+                s = group_sum<LPT>(s);
                 if (valid && j == 0 && h < nh) sc[h * p.chunk + (tok - ta)] = s * p.scale;
             }
         }
@@ -283,8 +282,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
         if (wv < nh) {
             float* row = sc + wv * p.chunk;
             for (int i = lane; i < len; i += 64) mx = fmaxf(mx, row[i]);
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            mx = wave_max(mx);
             for (int i = lane; i < len; i += 64) {
                 const float e = expf(row[i] - mx);
                 row[i] = e;
@@ -419,6 +417,10 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
 //      lane l holds Q[l % 32][d] and K[t][d] for the 32 dims d of its half
 //      (the order of d inside a dot is free: half g = l / 32 takes dims
 //      64 (w / 2) + 32 g .. + 32), the two dim halves meet in LDS.
+//   softmax: wave w takes heads 8 w .. 8 w + 7 with lane = token; the eight
+//      heads go through each step together (independent DPP max / sum
+//      reductions, no LDS round trips), then lane i < 8 updates the running
+//      max and sum of head 8 w + i.
 //   P V: wave w owns output dims 32 w .. + 32; lane l reads P[l % 32][t] from
 //      LDS and V[t][32 w + l % 32] from HBM for tokens t = 32 g + kk.
 // MFMA layouts (32x32x2 f32): A[l % 32][l / 32], B[l / 32][l % 32], accumulator
@@ -516,21 +518,33 @@ __global__ __launch_bounds__(kThreads) void attn_mq_kernel(AttnParams p) {
             for (int r = 0; r < 16; ++r) spart[dh][8 * (r >> 2) + 4 * g + (r & 3)][32 * tt + li] = sacc[r];
         }
         __syncthreads();
-        // ---- online softmax: wave w updates heads 8 w .. 8 w + 7, lane = token ----
-#pragma unroll
-        for (int hh = 0; hh < 8; ++hh) {
-            const int h = 8 * wv + hh;
+        // ---- online softmax ----
+        {
             const bool valid = sa + lane < tb;
-            const float sv = valid ? (spart[0][h][lane] + spart[1][h][lane]) * p.scale : -1e30f;
-            float mx = sv;
+            float sv[8], mo[8], mn[8], su[8];
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float m_old = m_s[h];
-            const float m_new = fmaxf(m_old, mx);
-            const float e = valid ? expf(sv - m_new) : 0.0f;
-            const float sum = wave_sum(e);
-            pl[h][lane] = e;
-            if (lane == 0) {
+            for (int hh = 0; hh < 8; ++hh) {
+                const int h = 8 * wv + hh;
+                sv[hh] = valid ? (spart[0][h][lane] + spart[1][h][lane]) * p.scale : -1e30f;
+                mo[hh] = m_s[h];
+            }
+#pragma unroll
+            for (int hh = 0; hh < 8; ++hh) mn[hh] = fmaxf(mo[hh], wave_max(sv[hh]));
+#pragma unroll
+            for (int hh = 0; hh < 8; ++hh) {
+                const float e = valid ? expf(sv[hh] - mn[hh]) : 0.0f;
+                pl[8 * wv + hh][lane] = e;
+                su[hh] = wave_sum(e);
+            }
+            float m_old = mo[0], m_new = mn[0], sum = su[0];
+#pragma unroll
+            for (int hh = 1; hh < 8; ++hh) {
+                m_old = lane == hh ? mo[hh] : m_old;
+                m_new = lane == hh ? mn[hh] : m_new;
+                sum = lane == hh ? su[hh] : sum;
+            }
+            if (lane < 8) {
+                const int h = 8 * wv + lane;
                 const float a = expf(m_old - m_new);
                 alpha_s[h] = a;
                 l_s[h] = l_s[h] * a + sum;
@@ -751,15 +765,22 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p)
     }
 }
 
-// out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12), one
-// work-group per query head.  Thread (d4, g) owns float4 d4 of the head and
-// splits g, g + ng, ...; its first U partial loads are issued before the
-// max / sum pass, so the kernel waits on memory about once.  U is the
-// smallest of 8, 16 and 32 that covers the thread's splits (more loads in
-// flight than needed cost registers and occupancy: 66 splits merge in 3.9 us
-// with U = 16 against 4.3 with 32; 256 splits need 32).
+// out[h] = (sum_j o_j e^(m_j - M)) / (sum_j l_j e^(m_j - M) + 1e-12).  Work-
+// group (h, y) of a (heads, ny) grid writes float4 columns y nd4 .. + nd4 of
+// head h (nd4 = hd / 4 / ny): every work-group forms M and the sum from the
+// (max, sum) pairs of all splits and reads only its columns of the partial
+// o, so a long window's partials are read by ny times as many CUs.  Thread
+// (d4, g) owns column d4 and splits g, g + ng, ...; its first U partial
+// loads are issued before the max / sum pass, so the work-group waits on
+// memory about once.  U is the smallest of 4, 8, 16 and 32 that covers the
+// thread's splits (more loads in flight than needed cost registers and
+// occupancy).  The ng per-thread sums of a column meet in an LDS tree.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxSplit = 4096;
+#ifndef GNCX_MERGE_KB
+#define GNCX_MERGE_KB 32
+#endif
+constexpr size_t kMergeBytesPerGroup = static_cast<size_t>(GNCX_MERGE_KB) * 1024;  // partial o per work-group
 template <int U>
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict part_o,
                                                                    const float* __restrict part_ml, int32_t n_split,
@@ -769,9 +790,9 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
     __shared__ float red[2][kMergeThreads / 64];
     __shared__ float4 accs[kMergeThreads];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nd4 = hd / 4;  // hd in {64, 128, 256}
+    const int nd4 = hd / 4 / static_cast<int>(gridDim.y);  // a power of two from 4 to 64
     const int ng = kMergeThreads / nd4;
-    const int d4 = tid % nd4, g = tid / nd4;
+    const int d4 = static_cast<int>(blockIdx.y) * nd4 + tid % nd4, g = tid / nd4;
     auto po_at = [&](int s) {
         return *reinterpret_cast<const float4*>(part_o + (static_cast<size_t>(s) * n_heads + h) * hd + 4 * d4);
     };
@@ -784,8 +805,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
     float m = -1e30f;
     for (int sp = tid; sp < n_split; sp += kMergeThreads)
         m = fmaxf(m, part_ml[(static_cast<size_t>(sp) * n_heads + h) * 2]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = wave_max(m);
     if (lane == 0) red[0][wv] = m;
     __syncthreads();
     float M = red[0][0];
@@ -823,37 +843,49 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
     }
     accs[tid] = a;
     __syncthreads();
-    if (tid < nd4) {
-        float4 t = accs[tid];
-        for (int gg = 1; gg < ng; ++gg) {
-            const float4 v = accs[gg * nd4 + tid];
-            t.x += v.x;
-            t.y += v.y;
-            t.z += v.z;
-            t.w += v.w;
+    for (int half = ng / 2; half > 0; half /= 2) {
+        if (g < half) {
+            const float4 v = accs[tid + half * nd4];
+            a.x += v.x;
+            a.y += v.y;
+            a.z += v.z;
+            a.w += v.w;
+            accs[tid] = a;
         }
+        __syncthreads();
+    }
+    if (g == 0) {
         float4 r;
-        r.x = t.x * inv;
-        r.y = t.y * inv;
-        r.z = t.z * inv;
-        r.w = t.w * inv;
-        *reinterpret_cast<float4*>(out + static_cast<size_t>(h) * hd + 4 * tid) = r;
+        r.x = a.x * inv;
+        r.y = a.y * inv;
+        r.z = a.z * inv;
+        r.w = a.w * inv;
+        *reinterpret_cast<float4*>(out + static_cast<size_t>(h) * hd + 4 * d4) = r;
     }
 }
 
 hipError_t launch_merge(const float* part_o, const float* part_ml, int32_t n_split, int32_t n_heads, int32_t hd,
                         float* out, hipStream_t stream) {
-    const int32_t ng = kMergeThreads / (hd / 4);  // split groups per head
-    const int32_t per = (n_split + ng - 1) / ng;   // splits per thread
-    if (per <= 8)
-        hipLaunchKernelGGL(attn_merge_kernel<8>, dim3(n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml, n_split,
+    // column slices per head: the smallest count that keeps a work-group's
+    // share of the partial o within kMergeBytesPerGroup (at least 4 columns each)
+    int32_t ny = 1;
+    const size_t head_bytes = sizeof(float) * static_cast<size_t>(n_split) * hd;
+    while (ny < 16 && hd / 4 / ny > 4 && head_bytes / ny > kMergeBytesPerGroup) ny *= 2;
+    const int32_t ng = kMergeThreads / (hd / 4 / ny);  // split groups per column
+    const int32_t per = (n_split + ng - 1) / ng;       // splits per thread
+    const dim3 grid(n_heads, ny);
+    if (per <= 4)
+        hipLaunchKernelGGL(attn_merge_kernel<4>, grid, dim3(kMergeThreads), 0, stream, part_o, part_ml, n_split,
+                           n_heads, hd, out);
+    else if (per <= 8)
+        hipLaunchKernelGGL(attn_merge_kernel<8>, grid, dim3(kMergeThreads), 0, stream, part_o, part_ml, n_split,
                            n_heads, hd, out);
     else if (per <= 16)
-        hipLaunchKernelGGL(attn_merge_kernel<16>, dim3(n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml,
-                           n_split, n_heads, hd, out);
+        hipLaunchKernelGGL(attn_merge_kernel<16>, grid, dim3(kMergeThreads), 0, stream, part_o, part_ml, n_split,
+                           n_heads, hd, out);
     else
-        hipLaunchKernelGGL(attn_merge_kernel<32>, dim3(n_heads), dim3(kMergeThreads), 0, stream, part_o, part_ml,
-                           n_split, n_heads, hd, out);
+        hipLaunchKernelGGL(attn_merge_kernel<32>, grid, dim3(kMergeThreads), 0, stream, part_o, part_ml, n_split,
+                           n_heads, hd, out);
     return hipGetLastError();
 }
 

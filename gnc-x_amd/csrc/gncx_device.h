@@ -80,6 +80,38 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Sum over aligned groups of N = 4, 8 or 16 lanes (the first N / 4 + 1 steps
+// of wave_sum_lane63); every lane of a group ends with the same sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 4 || N == 8 || N == 16, "groups of 4, 8 or 16 lanes");
+    v = dpp_add<0xb1>(v);
+    v = dpp_add<0x4e>(v);
+    if constexpr (N >= 8) v = dpp_add<0x141>(v);
+    if constexpr (N >= 16) v = dpp_add<0x140>(v);
+    return v;
+}
+
+// max(v, v of another lane) through DPP; lanes the masks leave out keep v
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int o = __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -__builtin_inff()), __builtin_bit_cast(int, v),
+                                              CTRL, ROW_MASK, BANK_MASK, false);
+    return fmaxf(v, __builtin_bit_cast(float, o));
+}
+
+// Max over the wave, returned in every lane: the steps of wave_sum_lane63
+// with max for add (no LDS round trips, unlike a shuffle butterfly).
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max<0xb1>(v);
+    v = dpp_max<0x4e>(v);
+    v = dpp_max<0x141>(v);
+    v = dpp_max<0x140>(v);
+    v = dpp_max<0x142, 0xa>(v);
+    v = dpp_max<0x143, 0xc>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // Q4_K 6-bit (scale, min) of sub-block j (reference cpp:1112-1120) from the
 // three little-endian dwords of the 12 scale bytes.
 __device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
