@@ -201,6 +201,12 @@ constexpr int kCtlQuantised = 31;   // index of the count of waves done quantisi
 constexpr int kCtlNormPart = 32;    // [16] per-wave sums of squares of the add+RMSNorm prologue
 constexpr int kCtlNormCount = 48;   // count of waves that stored their sum of squares
 constexpr int kOneMinRowWaves = 8;  // ONE schedule from this many row-waves (16-wave groups only)
+#ifndef GNCX_NORM_WAVES
+#define GNCX_NORM_WAVES 8
+#endif
+constexpr int kNormWaves = GNCX_NORM_WAVES;  // waves forming x in the add+RMSNorm prologue (k <= 4096)
+constexpr int kNormU = 16 / kNormWaves;  // float4 of x per thread of those waves
+constexpr int kNormStride = 64 * kNormWaves;
 
 enum BandSched { kSchedOne = 1, kSchedTwo = 2 };
 
@@ -382,38 +388,71 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
             issue(fa, ja);
             issue(fb, jb);
         };
-        float4 hsum = make_float4(0.f, 0.f, 0.f, 0.f);  // h + r of this thread (kExtNorm)
+        // kExtNorm: h + r of float4 vt = threadIdx.x + 256 u of a quantising thread
+        float4 hsum[kNormU];
         const int32_t n4 = k / 4;
-        const int32_t t4 = static_cast<int32_t>(threadIdx.x) < n4 ? static_cast<int32_t>(threadIdx.x) : n4 - 1;
         if constexpr ((EXT & kExtNorm) != 0) {
 #pragma clang fp contract(off)
-            // h, r and gamma first, so their waitcnt does not wait for the rows
-            const float4 hv = reinterpret_cast<const float4*>(ex.h)[t4];
-            const float4 rv = ex.r ? reinterpret_cast<const float4*>(ex.r)[t4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 gv = reinterpret_cast<const float4*>(ex.gamma)[t4];
-            start();
-            hsum = ex.r ? make_float4(hv.x + rv.x, hv.y + rv.y, hv.z + rv.z, hv.w + rv.w) : hv;
-            const bool mine = static_cast<int32_t>(threadIdx.x) < n4;
-            float ss = mine ? hsum.x * hsum.x + hsum.y * hsum.y + hsum.z * hsum.z + hsum.w * hsum.w : 0.0f;
-            ss = wave_sum(ss);
-            float* npart = reinterpret_cast<float*>(ctl + kCtlNormPart);
-            if (lane == 0) npart[wv] = ss;
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-            asm volatile("" ::: "memory");
-            if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlNormCount], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            while (__hip_atomic_load(&ctl[kCtlNormCount], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < THREADS / 64)
-                __builtin_amdgcn_s_sleep(1);
-            asm volatile("" ::: "memory");
-            float tot = 0.0f;
+            // The first kNormWaves waves form x as 1024 threads of one float4
+            // each would: thread threadIdx.x stands for the threads vt =
+            // threadIdx.x + kNormStride u, of "virtual wave" wv + kNormWaves u,
+            // whose wave sum goes to partial wv + kNormWaves u, and the 16
+            // partials are added in order -- the association of
+            // rmsnorm_kernel<true> -- so x is bit-identical with it.  The
+            // other waves issue their rows at once; h, r and gamma go first,
+            // so their waitcnt does not wait for the rows (the loads are
+            // unconditional, clamped to the last float4 of x: a load behind a
+            // branch made the compiler wait for every row, +2.5 us).
+            if (qwave) {
+                float4 hv[kNormU], rv[kNormU], gv[kNormU];
 #pragma unroll
-            for (int w = 0; w < THREADS / 64; ++w) tot += npart[w];
-            const float inv = 1.0f / sqrtf(tot / static_cast<float>(k) + ex.eps);
-            const float4 xn = make_float4(hsum.x * inv * gv.x, hsum.y * inv * gv.y, hsum.z * inv * gv.z,
-                                          hsum.w * inv * gv.w);
-            if (mine) quantize_task(xn, threadIdx.x >> 3, threadIdx.x & 7, q, meta);
-            __builtin_amdgcn_s_waitcnt(0xc07f);
-            asm volatile("" ::: "memory");
-            if (lane == 0) __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                for (int u = 0; u < kNormU; ++u) {
+                    const int32_t vt = static_cast<int32_t>(threadIdx.x) + kNormStride * u;
+                    const int32_t t4 = vt < n4 ? vt : n4 - 1;
+                    hv[u] = reinterpret_cast<const float4*>(ex.h)[t4];
+                    rv[u] = ex.r ? reinterpret_cast<const float4*>(ex.r)[t4] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    gv[u] = reinterpret_cast<const float4*>(ex.gamma)[t4];
+                }
+                start();
+                float* npart = reinterpret_cast<float*>(ctl + kCtlNormPart);
+#pragma unroll
+                for (int u = 0; u < kNormU; ++u) {
+                    hsum[u] = ex.r ? make_float4(hv[u].x + rv[u].x, hv[u].y + rv[u].y, hv[u].z + rv[u].z,
+                                                 hv[u].w + rv[u].w)
+                                   : hv[u];
+                    const bool mine = static_cast<int32_t>(threadIdx.x) + kNormStride * u < n4;
+                    float ss = mine ? hsum[u].x * hsum[u].x + hsum[u].y * hsum[u].y + hsum[u].z * hsum[u].z +
+                                          hsum[u].w * hsum[u].w
+                                    : 0.0f;
+                    ss = wave_sum(ss);
+                    if (lane == 0) npart[wv + kNormWaves * u] = ss;
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+                asm volatile("" ::: "memory");
+                if (lane == 0)
+                    __hip_atomic_fetch_add(&ctl[kCtlNormCount], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                while (__hip_atomic_load(&ctl[kCtlNormCount], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                       kNormWaves)
+                    __builtin_amdgcn_s_sleep(1);
+                asm volatile("" ::: "memory");
+                float tot = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 16; ++w) tot += npart[w];
+                const float inv = 1.0f / sqrtf(tot / static_cast<float>(k) + ex.eps);
+#pragma unroll
+                for (int u = 0; u < kNormU; ++u) {
+                    const int32_t vt = static_cast<int32_t>(threadIdx.x) + kNormStride * u;
+                    const float4 xn = make_float4(hsum[u].x * inv * gv[u].x, hsum[u].y * inv * gv[u].y,
+                                                  hsum[u].z * inv * gv[u].z, hsum[u].w * inv * gv[u].w);
+                    if (vt < n4) quantize_task(xn, vt >> 3, vt & 7, q, meta);
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                asm volatile("" ::: "memory");
+                if (lane == 0)
+                    __hip_atomic_fetch_add(&ctl[kCtlQuantised], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+                start();
+            }
         } else if (qwave) {
             float4 xv[kU];
             quant_load<kU>(xv, x, k / 32, threadIdx.x, nqw * 64);
@@ -433,8 +472,13 @@ __global__ __launch_bounds__(THREADS) void gemv_band_kernel(BandMats mats, uint3
             }
         }
         if constexpr ((EXT & kExtNorm) != 0) {
-            if (blockIdx.x == 0 && ex.h_out && static_cast<int32_t>(threadIdx.x) < n4)
-                reinterpret_cast<float4*>(ex.h_out)[threadIdx.x] = hsum;
+            if (blockIdx.x == 0 && ex.h_out && qwave) {
+#pragma unroll
+                for (int u = 0; u < kNormU; ++u) {
+                    const int32_t vt = static_cast<int32_t>(threadIdx.x) + kNormStride * u;
+                    if (vt < n4) reinterpret_cast<float4*>(ex.h_out)[vt] = hsum[u];
+                }
+            }
         }
     } else {
         if (qwave) {
@@ -571,7 +615,7 @@ bool try_band_ext(const BandMats& m, const float* x, int32_t k, int32_t n, const
     if (nwk != 1 || nwr < kOneMinRowWaves) return false;
     if constexpr ((EXT & kExtNorm) != 0) {
         if (k % 4 != 0 || k > 4 * 1024) return false;
-        nqw = 16;  // every thread normalises and quantises one float4
+        nqw = kNormWaves;  // kNormU float4 of x per thread of these waves
     }
     if constexpr ((EXT & kExtSwiglu) != 0) {
         if (m.count != 2 || 2 * m.end[0] != n || m.end[0] % groups != 0) return false;
