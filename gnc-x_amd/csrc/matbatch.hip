@@ -490,6 +490,21 @@ constexpr int kXStages = 4;
 // 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
+// vmcnt(N) and lgkmcnt(0), then a work-group barrier with no memory fence.
+// __syncthreads() also waits for the direct-to-LDS loads issued for later
+// steps (its release fence covers every outstanding write, those included),
+// which put a memory round trip on every step.  Here each wave waits only for
+// the loads the next step reads (vmcnt(N)) and for its own LDS writes
+// (lgkmcnt(0)) before the barrier, so after it every wave sees both; the
+// empty asm statements keep the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void step_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int WM, int WN, int MW, int NW>
@@ -514,6 +529,20 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     __shared__ __align__(16) _Float16 sp[2][2][BM * 8];          // [super-block parity][hi, lo] P of 8 blocks
     __shared__ __align__(16) _Float16 smn[2][BN * 8];            // [super-block parity] mins of 8 blocks
     __shared__ __align__(8) float sdm[2][BN][2];                 // [super-block parity] d, dmin
+    // WDMA: the raw weights stream through LDS as well, by direct-to-LDS loads
+    // with no registers in flight (register loads of them put memory waits on
+    // every step): a ring of 4 stages of each row's 32 qs bytes of a step's
+    // sub-block pair, and per super-block parity the rows' 16-byte headers and
+    // the tokens' P pairs, loaded at the 5th step of the super-block before.
+    // Every wave issues the same number of these loads (vmcnt is per wave).
+    constexpr bool WDMA = (BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
+                          (BM * 16) % (THREADS * 4) == 0;
+    constexpr int kWQ = WDMA ? BN * 32 : 16;
+    __shared__ __align__(16) uint8_t wq0[kWQ], wq1[kWQ], wq2[kWQ], wq3[kWQ];
+    __shared__ __align__(16) uint8_t whd[2][WDMA ? BN * 16 : 16];  // [super-block parity] raw headers
+    auto wstage = [&](int stage) -> uint8_t* { return stage == 0 ? wq0 : stage == 1 ? wq1 : stage == 2 ? wq2 : wq3; };
+    constexpr int kWLoads = WDMA ? BN * 32 / (THREADS * 16) : 0;                      // per wave and step
+    constexpr int kHLoads = WDMA ? BN * 16 / (THREADS * 4) + 2 * (BM * 16 / (THREADS * 4)) : 0;  // per super-block
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int li = lane & 31, lh = lane >> 5;
@@ -582,15 +611,73 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
         hdr[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk, 0, 0);
         qv[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk + 16 + 32 * (rr / 64) + 16 * whalf, 0, 0);
     };
-    // weights of the step at k0 from register set `set` into LDS buffer
-    // `buf`; at a super-block's first step also its P, d, dmin and mins
-    // (parity `sbp`)
-    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int sbp) {
+    // WDMA: raw qs of the step at k0 (each row's 32 bytes of its sub-block
+    // pair) into ring stage `stage`, 16 bytes per lane in row order
+    auto dma_w = [&](int stage, int32_t k0) {
+        if constexpr (WDMA) {
+            const int32_t kk = k0 < ke ? k0 : 0;
+            const int32_t koff = (kk / 256) * 144 + 16 + 32 * ((kk % 256) / 64);
+#pragma unroll
+            for (int i = 0; i < kWLoads; ++i) {
+                const int piece = (i * WAVES + wv) * 64 + lane;  // two 16-byte pieces per row
+                const int row = piece >> 1;
+                const int32_t off = k0 < ke && row < wrows_here
+                                        ? row * static_cast<int32_t>(rbytes) + koff + 16 * (piece & 1)
+                                        : kMfOob;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(wstage(stage) + (i * WAVES + wv) * 1024), 16,
+                                                         off, 0, 0, 0);
+            }
+        }
+    };
+    // WDMA: the rows' headers (d, dmin, scales) and the tokens' P pairs of the
+    // super-block at s0 into parity `par`, 4 bytes per lane in row order
+    auto dma_hp = [&](int par, int32_t s0) {
+        if constexpr (WDMA) {
+            const bool in = s0 < ke;
+            constexpr int HL = BN * 16 / (THREADS * 4), PL = BM * 16 / (THREADS * 4);
+#pragma unroll
+            for (int i = 0; i < HL; ++i) {
+                const int dw = (i * WAVES + wv) * 64 + lane;
+                const int row = dw >> 2;
+                const int32_t off = in && row < wrows_here
+                                        ? row * static_cast<int32_t>(rbytes) + (s0 / 256) * 144 + 4 * (dw & 3)
+                                        : kMfOob;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(&whd[par][(i * WAVES + wv) * 256]), 4, off, 0,
+                                                         0, 0);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < PL; ++i) {
+                    const int dw = (i * WAVES + wv) * 64 + lane;
+                    const int row = dw >> 2;
+                    const int32_t off = in && row < rows_here
+                                            ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) *
+                                                      static_cast<int32_t>(sizeof(_Float16)) +
+                                                  4 * (dw & 3)
+                                            : kMfOob;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][(i * WAVES + wv) * 128]), 4,
+                                                             off, 0, 0, 0);
+                }
+        }
+    };
+    // weights of the step at k0 (register set `set`, or ring stage `set` with
+    // WDMA, headers of parity `hpar`) into LDS buffer `buf`; at a super-block's
+    // first step also its d, dmin and mins (and without WDMA its P), parity hpar
+    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int hpar) {
         if (tid < 2 * BN) {
             const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
+            u32x4 hh, qq;
+            if constexpr (WDMA) {
+                hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
+                qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
+            } else {
+                hh = hdr[set & 1];
+                qq = qv[set & 1];
+            }
             int sc, mn;
-            k4_scale_min(j, hdr[set].y, hdr[set].z, hdr[set].w, sc, mn);
-            const uint32_t qw[4] = {qv[set].x, qv[set].y, qv[set].z, qv[set].w};
+            k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
+            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
             uint32_t o[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -604,25 +691,27 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
             *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
             if (sb_first && whalf == 0) {
-                sdm[sbp][wrow][0] = half_bits_to_float(hdr[set].x & 0xffffu);
-                sdm[sbp][wrow][1] = half_bits_to_float(hdr[set].x >> 16);
+                sdm[hpar][wrow][0] = half_bits_to_float(hh.x & 0xffffu);
+                sdm[hpar][wrow][1] = half_bits_to_float(hh.x >> 16);
                 uint32_t m2[4];
 #pragma unroll
                 for (int jj = 0; jj < 8; jj += 2) {
                     int s0, m0, s1, m1;
-                    k4_scale_min(jj, hdr[set].y, hdr[set].z, hdr[set].w, s0, m0);
-                    k4_scale_min(jj + 1, hdr[set].y, hdr[set].z, hdr[set].w, s1, m1);
+                    k4_scale_min(jj, hh.y, hh.z, hh.w, s0, m0);
+                    k4_scale_min(jj + 1, hh.y, hh.z, hh.w, s1, m1);
                     const _Float16 h0 = static_cast<_Float16>(static_cast<float>(m0));
                     const _Float16 h1 = static_cast<_Float16>(static_cast<float>(m1));
                     m2[jj / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
                                  (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
                 }
-                *reinterpret_cast<uint4*>(&smn[sbp][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
+                *reinterpret_cast<uint4*>(&smn[hpar][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
             }
         }
-        if (sb_first && tid < BM) {
-            *reinterpret_cast<uint4*>(&sp[sbp][0][tid * 8]) = pr[0];
-            *reinterpret_cast<uint4*>(&sp[sbp][1][tid * 8]) = pr[1];
+        if constexpr (!WDMA) {
+            if (sb_first && tid < BM) {
+                *reinterpret_cast<uint4*>(&sp[hpar][0][tid * 8]) = pr[0];
+                *reinterpret_cast<uint4*>(&sp[hpar][1][tid * 8]) = pr[1];
+            }
         }
     };
     // two K16 slices of one step (D starts each super-block at 0)
@@ -697,20 +786,34 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     // super-block's constants into LDS, step 1's weights in register set 1.
     // Loads are issued in the order P, x0, w0, x1, w1, x2 so that vmcnt(8)
     // covers the first ring stage.
-    gload_p(kb);
-    dma_x(0, kb);
-    gload_w(0, kb);
-    dma_x(1, kb + 32);
-    gload_w(1, kb + 32);
-    dma_x(2, kb + 64);
-    lstore(0, 0, kb, true, 0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXLoads + 2));
-    __syncthreads();
-    // Per step: (P at the 7th step of a super-block), the ring load 3 steps
-    // ahead, the weights 2 steps ahead; compute; the next step's weights into
-    // LDS; then a wait for the ring stage the next step reads, whose load was
-    // issued two steps ago: the loads issued since then are at most
-    // 2 + 2 (w) + 2 kXLoads (ring) + 2 (P).
+    if constexpr (WDMA) {
+        // headers and P of super-block 0, then steps 0-2 of activations and
+        // raw weights; step 0's weights are dequantised once the first three
+        // groups of loads are in LDS for every wave
+        dma_hp(0, kb);
+        dma_x(0, kb);
+        dma_w(0, kb);
+        dma_x(1, kb + 32);
+        dma_w(1, kb + 32);
+        dma_x(2, kb + 64);
+        dma_w(2, kb + 64);
+        step_barrier<2 * (kXLoads + kWLoads)>();
+        lstore(0, 0, kb, true, 0);
+        step_barrier<kXLoads + kWLoads>();
+    } else {
+        gload_p(kb);
+        dma_x(0, kb);
+        gload_w(0, kb);
+        dma_x(1, kb + 32);
+        gload_w(1, kb + 32);
+        dma_x(2, kb + 64);
+        lstore(0, 0, kb, true, 0);
+        step_barrier<2 * kXLoads + 2>();
+    }
+    // Per step: the activation ring load 3 steps ahead, the weights 3 steps
+    // ahead (WDMA, plus the next super-block's headers and P at its 5th step)
+    // or 2 steps ahead into registers (P at the 7th step); compute; the next
+    // step's weights dequantised into LDS; then the barrier (below).
     for (int32_t sb = 0; sb < nsb; ++sb) {
         const int32_t s0 = kb + sb * 256;
         const int sbp = sb & 1;
@@ -718,23 +821,49 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
         for (int st = 0; st < 8; ++st) {
             const int32_t k0 = s0 + 32 * st;
             const int buf = st & 1;  // 8 steps per super-block keep every parity static
-            if (st == 6) gload_p(s0 + 256);
-            dma_x((st + 3) & 3, k0 + 96);
-            gload_w(buf, k0 + 64);
-            // the two waves on each SIMD take the step's MFMA and VALU phases
-            // in opposite orders (staging writes the other weight buffer), so
-            // the barrier does not line up both waves' matrix-core work
+            auto issue_loads = [&]() {
+                dma_x((st + 3) & 3, k0 + 96);
+                if constexpr (WDMA) {
+                    dma_w((st + 3) & 3, k0 + 96);
+                    if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
+                } else {
+                    if (st == 6) gload_p(s0 + 256);
+                    gload_w(buf, k0 + 64);
+                }
+            };
+            // the step dequantised here is k0 + 32: its raw weights (ring
+            // stage or register set) and its super-block's parity
+            const int wset = WDMA ? ((st + 1) & 3) : (buf ^ 1);
+            const int hpar = st == 7 ? (sbp ^ 1) : sbp;
+            // the two waves on each SIMD (waves w and w + WAVES / 2) take the
+            // step's MFMA and VALU phases in opposite orders (staging writes
+            // the other weight buffer), so the barrier does not line up both
+            // waves' matrix-core work; each issues its loads as its MFMA phase
+            // starts, so the CU's memory pipeline takes half of the step's
+            // requests at a time (all of them right after the barrier stalled
+            // the issuing waves for about 400 clocks)
             if (wv < WAVES / 2) {
+                issue_loads();
                 compute(st & 3, buf);
                 if (st == 7) fold(sbp);
-                if (k0 + 32 < ke) lstore(buf ^ 1, buf ^ 1, k0 + 32, st == 7, sbp ^ 1);
+                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
             } else {
-                if (k0 + 32 < ke) lstore(buf ^ 1, buf ^ 1, k0 + 32, st == 7, sbp ^ 1);
+                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
+                issue_loads();
                 compute(st & 3, buf);
                 if (st == 7) fold(sbp);
             }
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kXLoads + 4));
-            __syncthreads();
+            // WDMA: the next step reads loads issued one and two steps ago;
+            // only this step's may still run (and at the 5th step its
+            // headers and P).  Otherwise: the ring stage the next step reads
+            // was issued two steps ago; the loads issued since then are at
+            // most 2 + 2 (w) + 2 kXLoads (ring) + 2 (P).
+            if constexpr (WDMA) {
+                if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
+                else step_barrier<kXLoads + kWLoads>();
+            } else {
+                step_barrier<2 * kXLoads + 4>();
+            }
         }
     }
     float* dst = gridDim.z > 1 ? part + static_cast<size_t>(blockIdx.z) * b * n : y;
