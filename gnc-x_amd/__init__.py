@@ -123,6 +123,8 @@ SIGNATURES = {
     "gncx_hip_quantize_act": (None, [_fp, _i32, _i32, _vp, _vp]),
     "gncx_hip_vec_add": (None, [_fp, _fp, _i32]),
     "gncx_hip_matvec_multi": (None, [_i32, _vp, _vp, _i32, _fp, _i32, _vp]),
+    "gncx_hip_matbatch_multi": (None, [_i32, _vp, _vp, _i32, _fp, _i32, _i32, _vp]),
+    "gncx_hip_fetch_token_embeddings": (None, [_i32, _vp, _sz, _vp, _i32, _i32, _i32, _f32, _fp]),
     "gncx_hip_add_rmsnorm": (None, [_fp, _fp, _vp, _sz, _i32, _f32, _fp]),
     "gncx_hip_attention_prefill": (
         None,

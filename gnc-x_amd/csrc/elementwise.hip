@@ -323,6 +323,16 @@ __global__ void fetch_embedding_dev_kernel(int32_t type, const uint8_t* __restri
         out[e] = decode_elem(type, row, e, scale);
 }
 
+// Rows of `count` tokens (ids already checked against the table's rows), one
+// y-block of the grid per token.
+__global__ void fetch_embedding_rows_kernel(int32_t type, const uint8_t* __restrict table, const int32_t* tokens,
+                                            size_t rbytes, int32_t dim, float scale, float* __restrict out) {
+    const uint8_t* row = table + static_cast<size_t>(tokens[blockIdx.y]) * rbytes;
+    float* o = out + static_cast<size_t>(blockIdx.y) * dim;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < dim; e += gridDim.x * blockDim.x)
+        o[e] = decode_elem(type, row, e, scale);
+}
+
 // Index of the largest value (the first one among equal maxima; NaN never
 // wins), as torch.argmax and the greedy pick of the streamer's sampler take
 // it.  Two launches: argmax_part_kernel reduces contiguous chunks of
@@ -512,6 +522,16 @@ hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t to
     const uint8_t* row = table + static_cast<size_t>(token) * row_bytes(type, dim);
     hipLaunchKernelGGL(fetch_embedding_kernel, dim3(grid_for(dim, 256)), dim3(256), 0, stream, type, row, dim,
                        scale, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fetch_embedding_rows(int32_t type, const uint8_t* table, const int32_t* tokens, int32_t count,
+                                       int32_t dim, float scale, float* out, hipStream_t stream) {
+    if (type != kQ8_0 && type != kQ6_K && type != kBF16) return hipErrorInvalidValue;
+    if (dim <= 0 || count <= 0) return hipSuccess;
+    if (count > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fetch_embedding_rows_kernel, dim3(grid_for(dim, 256), count), dim3(256), 0, stream, type,
+                       table, tokens, row_bytes(type, dim), dim, scale, out);
     return hipGetLastError();
 }
 

@@ -63,6 +63,14 @@ size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n);
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k,
                            int32_t n, float* y, void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
+// ys[i][b x ns[i]] = Q8(X) . W_i^T for count (1..4) matrices of one type
+// sharing X: the activations are quantised once, and Q4_K matrices whose rows
+// are whole tiles of the summed plan run as one launch.  Each output equals
+// launch_matbatch's for that matrix.
+size_t matbatch_multi_workspace_bytes(int32_t type, int32_t count, const int32_t* ns, int32_t b, int32_t k);
+hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                                 const float* x, int32_t b, int32_t k, float* const* ys, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream);
 
 // cos/sin of one RoPE position, computed on the host with the C library's
 // powf/cosf/sinf exactly as the reference does (cpp:1779-1796), passed to
@@ -158,6 +166,10 @@ hipError_t launch_fetch_embedding(int32_t type, const uint8_t* table, int32_t to
                                   float scale, float* out, hipStream_t stream);
 // The same with the token read from device memory (tokens outside [0, vocab)
 // leave out untouched).
+// Rows of count tokens of a device table (ids checked by the caller) into
+// out[count][dim], one launch.
+hipError_t launch_fetch_embedding_rows(int32_t type, const uint8_t* table, const int32_t* tokens, int32_t count,
+                                       int32_t dim, float scale, float* out, hipStream_t stream);
 hipError_t launch_fetch_embedding_dev(int32_t type, const uint8_t* table, const int32_t* token, int32_t vocab,
                                       int32_t dim, float scale, float* out, hipStream_t stream);
 // *out = index of the first largest of x[0..n) (NaN never wins); also *log when

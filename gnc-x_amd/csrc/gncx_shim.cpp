@@ -1269,6 +1269,61 @@ GNCX_API void gncx_xfold_q4_0_matbatch(const uint8_t* mmap_base, size_t weight_a
                                   out_batch, telemetry);
 }
 
+// Several matrices of one type and in_dim applied to the same batch: the
+// batch is quantised once, and Q4_K matrices that are whole tiles of one
+// plan go through one launch.
+GNCX_API void gncx_hip_matbatch_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
+                                      int32_t ggml_type, const float* in_batch, int32_t batch_size, int32_t in_dim,
+                                      float* const* out_arg) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_matbatch_multi";
+    if (count <= 0 || count > 4 || !weights || !out_dims || !out_arg || !in_batch || in_dim <= 0 ||
+        batch_size <= 0) {
+        set_error(where, "count must be 1..4, with weights, out_dims, in_batch and out_batches given", -1);
+        return;
+    }
+    if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    bool ok = true;
+    float* outs[4];
+    in_batch = lazy_ptr(in_batch, dim_count(batch_size) * dim_count(in_dim), kRd, ok, where);
+    for (int32_t i = 0; i < count; ++i)
+        outs[i] = lazy_ptr(out_arg[i], dim_count(batch_size) * dim_count(out_dims[i]), kWr, ok, where);
+    if (!ok) return;
+    const uint8_t* ws[4];
+    float* ys[4];
+    bool host[4];
+    size_t host_total = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (out_dims[i] <= 0 || !weights[i] || !outs[i]) {
+            set_error(where, "every matrix needs weights, out_dims > 0 and an output", -1);
+            return;
+        }
+        ws[i] = device_weights(weights[i], row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dims[i]), where);
+        if (!ws[i]) return;
+        host[i] = !is_device_ptr(outs[i]);
+        if (host[i]) host_total += static_cast<size_t>(batch_size) * static_cast<size_t>(out_dims[i]);
+    }
+    const float* x = stage_in(in_batch, static_cast<size_t>(batch_size) * in_dim, g_rt.aux, where);
+    if (!x) return;
+    if (host_total && !g_rt.y.ensure(sizeof(float) * host_total, where)) return;
+    size_t off = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        ys[i] = host[i] ? g_rt.y.as<float>() + off : outs[i];
+        if (host[i]) off += static_cast<size_t>(batch_size) * static_cast<size_t>(out_dims[i]);
+    }
+    const size_t wsb = matbatch_multi_workspace_bytes(ggml_type, count, out_dims, batch_size, in_dim);
+    if (!g_rt.ws.ensure(wsb, where)) return;
+    if (!check(launch_matbatch_multi(ggml_type, count, ws, out_dims, x, batch_size, in_dim, ys, g_rt.ws.p,
+                                     g_rt.ws.cap, g_rt.stream),
+               where))
+        return;
+    for (int32_t i = 0; i < count; ++i)
+        if (host[i] &&
+            !finish_out(outs[i], ys[i], static_cast<size_t>(batch_size) * static_cast<size_t>(out_dims[i]), true,
+                        where))
+            return;
+}
+
 // cpp:1713-1732
 GNCX_API void gncx_universal_lm_head_logits(const uint8_t* mmap_base, size_t embd_abs_offset, int32_t ggml_type,
                                             const float* final_hidden, int32_t embed_dim, int32_t vocab_size,
@@ -1650,6 +1705,52 @@ void fetch_embedding(int32_t type, const uint8_t* base, size_t off, int32_t toke
     finish_out(out, o, dim, host, where);
 }
 }  // namespace
+
+// The rows of count tokens (host token ids, checked against vocab_size) of an
+// embedding table in one launch: the values of one gncx_fetch_token_embedding_*
+// call per token (the streamer's prefill loop, lua/gncx_streamer.lua:1001-1003).
+GNCX_API void gncx_hip_fetch_token_embeddings(int32_t ggml_type, const uint8_t* mmap_base, size_t tensor_abs_offset,
+                                              const int32_t* token_ids, int32_t count, int32_t vocab_size,
+                                              int32_t embed_dim, float scale_factor, float* out_rows) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_fetch_token_embeddings";
+    if (ggml_type != kQ8_0 && ggml_type != kQ6_K && ggml_type != kBF16) {
+        set_error(where, "the embedding table must be Q8_0, Q6_K or BF16", -1);
+        return;
+    }
+    if (!token_ids || !out_rows || count <= 0 || count > 65535 || vocab_size <= 0 || embed_dim <= 0) {
+        set_error(where, "token_ids, out_rows, count 1..65535, vocab_size > 0 and embed_dim > 0 are required", -1);
+        return;
+    }
+    if (is_device_ptr(token_ids)) {
+        set_error(where, "token_ids must be host memory (they are checked against vocab_size first)", -1);
+        return;
+    }
+    for (int32_t i = 0; i < count; ++i) {
+        if (token_ids[i] < 0 || token_ids[i] >= vocab_size) {
+            set_error(where, "a token id is outside [0, vocab_size)", -1);
+            return;
+        }
+    }
+    if (!ensure_runtime(where)) return;
+    bool ok = true;
+    const size_t n = static_cast<size_t>(count) * static_cast<size_t>(embed_dim);
+    out_rows = lazy_ptr(out_rows, n, kWr, ok, where);
+    if (!ok) return;
+    const size_t rb = row_bytes(ggml_type, embed_dim);
+    const uint8_t* table = device_weights(mmap_base + tensor_abs_offset, rb * static_cast<size_t>(vocab_size), where);
+    if (!table) return;
+    if (!g_rt.v.ensure(round_up(sizeof(int32_t) * static_cast<size_t>(count), 16), where)) return;
+    if (!h2d(g_rt.v.p, token_ids, sizeof(int32_t) * static_cast<size_t>(count), where)) return;
+    bool host = false;
+    float* o = out_target(out_rows, n, g_rt.o, host, where);
+    if (!o) return;
+    if (!check(launch_fetch_embedding_rows(ggml_type, table, g_rt.v.as<int32_t>(), count, embed_dim, scale_factor, o,
+                                           g_rt.stream),
+               where))
+        return;
+    finish_out(out_rows, o, n, host, where);
+}
 
 // cpp:693-715
 GNCX_API void gncx_fetch_token_embedding_q8_0(const uint8_t* mmap_base, size_t tensor_abs_offset, int32_t token_id,

@@ -29,6 +29,8 @@
 // wave per (row, token).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "gncx_device.h"
 #include "gncx_launch.h"
 #include "gncx_slots.h"
@@ -507,12 +509,36 @@ __device__ __forceinline__ void step_barrier() {
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// The matrices of one Q4_K launch (one activation batch, the same K): x-tiles
+// [tile0[i], tile0[i + 1]) are matrix i, n[i] rows, output y[i] [b x n[i]].
+// A work-group picks its matrix with scalar compares and selects over the
+// kernel arguments.
+constexpr int kMaxMbMats = 4;
+struct MbMats {
+    const uint8_t* w[kMaxMbMats];
+    float* y[kMaxMbMats];
+    int32_t n[kMaxMbMats];
+    int32_t tile0[kMaxMbMats];
+    int32_t count;
+};
+
 template <int WM, int WN, int MW, int NW>
 __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1) void matbatch_q4k_kernel(
-    const uint8_t* __restrict w, size_t rbytes, const _Float16* __restrict xhl, const _Float16* __restrict pq,
-    const float* __restrict rscale, int32_t b, int32_t k, int32_t n, float* __restrict y, int32_t kchunk,
-    float* __restrict part) {
+    MbMats mats, size_t rbytes, const _Float16* __restrict xhl, const _Float16* __restrict pq,
+    const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk, float* __restrict part) {
     constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
+    const uint8_t* __restrict w = mats.w[0];
+    float* __restrict y = mats.y[0];
+    int32_t n = mats.n[0], tile0 = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxMbMats; ++i) {
+        if (mats.count > i && static_cast<int32_t>(blockIdx.x) >= mats.tile0[i]) {
+            w = mats.w[i];
+            y = mats.y[i];
+            n = mats.n[i];
+            tile0 = mats.tile0[i];
+        }
+    }
     constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
     constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage and half; whole blocks per wave
     static_assert(XBLK % WAVES == 0, "whole activation blocks per wave");
@@ -546,7 +572,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int li = lane & 31, lh = lane >> 5;
-    const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int32_t t0 = blockIdx.y * BM, n0 = (static_cast<int32_t>(blockIdx.x) - tile0) * BN;
     const int32_t kb = blockIdx.z * kchunk;
     const int32_t ke = min(k, kb + kchunk);
     const int32_t nsb = (ke - kb) / 256;
@@ -987,14 +1013,33 @@ Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
     return {3, (k + kchunk - 1) / kchunk, kchunk};
 }
 
+// rows per x-tile of each Q4_K configuration
+int32_t q4k_tile_rows(int cfg) { return cfg == 0 ? 256 : cfg == 2 ? 128 : 64; }
+
 template <int WM, int WN, int MW, int NW>
-hipError_t launch_q4k_t(const uint8_t* w, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
-                        int32_t k, int32_t n, float* y, const Q4kPlan& p, float* part, hipStream_t stream) {
+hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
+                        int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
     constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    const dim3 grid((n + BN - 1) / BN, (b + BM - 1) / BM, p.splits);
-    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, w,
-                       row_bytes(kQ4_K, k), xhl, pq, rscale, b, k, n, y, p.kchunk, part);
+    const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
+    const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
+    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, m,
+                       row_bytes(kQ4_K, k), xhl, pq, rscale, b, k, p.kchunk, part);
     return hipGetLastError();
+}
+
+hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
+                           int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
+    const int32_t bn = q4k_tile_rows(p.cfg);
+    int32_t t = 0;
+    for (int32_t i = 0; i < m.count; ++i) {
+        m.tile0[i] = t;
+        t += (m.n[i] + bn - 1) / bn;
+    }
+    switch (p.cfg) {
+    case 0: return launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
+    case 2: return launch_q4k_t<2, 2, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
+    default: return launch_q4k_t<1, 1, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
+    }
 }
 
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
@@ -1004,11 +1049,12 @@ hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, in
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const Q4kPlan p = q4k_plan(b, k, n);
-    switch (p.cfg) {
-    case 0: e = launch_q4k_t<2, 2, 2, 4>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
-    case 2: e = launch_q4k_t<2, 2, 2, 2>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
-    default: e = launch_q4k_t<1, 1, 2, 2>(w, xhl, pq, rscale, b, k, n, y, p, part, stream); break;
-    }
+    MbMats m{};
+    m.w[0] = w;
+    m.y[0] = y;
+    m.n[0] = n;
+    m.count = 1;
+    e = launch_q4k_mats(m, xhl, pq, rscale, b, k, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     const size_t count = static_cast<size_t>(b) * n;
     size_t g = (count + kThreads - 1) / kThreads;
@@ -1081,6 +1127,75 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+
+namespace {
+
+// One launch over count Q4_K matrices sharing the activation batch: when the
+// plan for the summed rows needs no K split and every matrix is whole x-tiles
+// of it (false otherwise, and the matrices go one launch each).
+bool multi_fused(int32_t type, int32_t count, const int32_t* ns, int32_t b, int32_t k, Q4kPlan& p) {
+    if (type != kQ4_K || count < 2 || count > kMaxMbMats || b <= 0 || k <= 0 || (k % 256) != 0) return false;
+    int64_t total = 0;
+    for (int32_t i = 0; i < count; ++i) total += ns[i];
+    if (total > INT32_MAX) return false;
+    p = q4k_plan(b, k, static_cast<int32_t>(total));
+    if (p.splits != 1) return false;
+    const int32_t bn = q4k_tile_rows(p.cfg);
+    for (int32_t i = 0; i < count; ++i)
+        if (ns[i] % bn != 0) return false;
+    return true;
+}
+
+}  // namespace
+
+size_t matbatch_multi_workspace_bytes(int32_t type, int32_t count, const int32_t* ns, int32_t b, int32_t k) {
+    size_t need = 256;
+    for (int32_t i = 0; i < count; ++i) need = std::max(need, matbatch_workspace_bytes(type, b, k, ns[i]));
+    Q4kPlan p;
+    if (multi_fused(type, count, ns, b, k, p))
+        need = std::max(need, xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b) + 256);
+    return need;
+}
+
+hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                                 const float* x, int32_t b, int32_t k, float* const* ys, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
+    if (count <= 0 || count > kMaxMbMats || !ws || !ns || !ys) return hipErrorInvalidValue;
+    for (int32_t i = 0; i < count; ++i)
+        if (ns[i] <= 0 || !ws[i] || !ys[i]) return hipErrorInvalidValue;
+    if (workspace_bytes < matbatch_multi_workspace_bytes(type, count, ns, b, k)) return hipErrorInvalidValue;
+    Q4kPlan p;
+    if (!multi_fused(type, count, ns, b, k, p)) {
+        for (int32_t i = 0; i < count; ++i) {
+            const hipError_t e = launch_matbatch(type, ws[i], x, b, k, ns[i], ys[i], workspace, workspace_bytes, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    // the checks of launch_matbatch for Q4_K
+    if (k > (1 << 20) || b > 65535) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (row_bytes(kQ4_K, k) & 15u) != 0) return hipErrorInvalidValue;
+    for (int32_t i = 0; i < count; ++i)
+        if ((reinterpret_cast<uintptr_t>(ws[i]) & 15u) != 0) return hipErrorInvalidValue;
+    char* wsp = static_cast<char*>(workspace);
+    _Float16* xhl = reinterpret_cast<_Float16*>(wsp);
+    _Float16* pq = reinterpret_cast<_Float16*>(wsp + xh_bytes(b, k));
+    float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
+    if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
+                       rscale, pq);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    MbMats m{};
+    for (int32_t i = 0; i < count; ++i) {
+        m.w[i] = ws[i];
+        m.y[i] = ys[i];
+        m.n[i] = ns[i];
+    }
+    m.count = count;
+    return launch_q4k_mats(m, xhl, pq, rscale, b, k, p, nullptr, stream);
 }
 
 }  // namespace gncx

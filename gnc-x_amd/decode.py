@@ -34,8 +34,10 @@ differences are where the streamer works on host memory:
   prologue+attention calls, gncx_hip_matvec_multi for Q/K/V and for gate/up
   (one launch each) and gncx_hip_add_rmsnorm for each residual add and the
   RMSNorm after it; in prefill, gncx_hip_rmsnorm_rows for the per-token
-  RMSNorm loops and gncx_hip_attention_prefill for the per-token prologue +
-  attention loop (one causal batch).
+  RMSNorm loops, gncx_hip_fetch_token_embeddings for the embedding rows,
+  gncx_hip_matbatch_multi for Q/K/V and for gate/up, and
+  gncx_hip_attention_prefill for the per-token prologue + attention loop
+  (one causal batch).
 
 Weights are random-init with the block statistics of the synthetic
 benchmark inputs: fp16 scales |N(0, 0.02)|, uniform random code bytes,
@@ -542,10 +544,13 @@ class Decoder:
         bu = torch.zeros(B, s.ffn, **f32)
         bf = torch.zeros(B, s.ffn, **f32)
         rowp = lambda t, i: t.data_ptr() + 4 * i * t.shape[1]  # noqa: E731
+        if self.fused:
+            ids = (C.c_int32 * B)(*(int(t) for t in token_ids))
+            L.gncx_hip_fetch_token_embeddings(s.embd_type, self.m.base, self.m.off("token_embd.weight"), ids, B,
+                                              s.vocab, s.embed, 1.0, bh.data_ptr())
+            return self._prefill_fused(B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf)
         for i, tok in enumerate(token_ids):
             self._embed(tok, rowp(bh, i))
-        if self.fused:
-            return self._prefill_fused(B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf)
         for l in range(s.n_layers):
             p = f"blk.{l}"
             for i in range(B):
@@ -576,9 +581,8 @@ class Decoder:
             p = f"blk.{l}"
             L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"), s.embed, s.eps,
                                     bn.data_ptr())
-            self._matbatch(f"{p}.attn_q.weight", bn.data_ptr(), B, s.embed, s.q_dim, bq.data_ptr())
-            self._matbatch(f"{p}.attn_k.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bk.data_ptr())
-            self._matbatch(f"{p}.attn_v.weight", bn.data_ptr(), B, s.embed, s.kv_dim, bv.data_ptr())
+            self._matbatch_multi(p, "qkv", bn.data_ptr(), B, s.embed, (s.q_dim, s.kv_dim, s.kv_dim),
+                                 (bq, bk, bv))
             L.gncx_hip_attention_prefill(bq.data_ptr(), bk.data_ptr(), bv.data_ptr(), self.kc[l].data_ptr(),
                                          self.vc[l].data_ptr(), 0, B, s.n_heads, s.n_kv, s.head_dim, self.scale, 0,
                                          m.base, m.off(f"{p}.attn_q_norm.weight"), m.off(f"{p}.attn_k_norm.weight"),
@@ -587,13 +591,23 @@ class Decoder:
             self._add(bh, bp)
             L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"), s.embed, s.eps,
                                     bn.data_ptr())
-            self._matbatch(f"{p}.ffn_gate.weight", bn.data_ptr(), B, s.embed, s.ffn, bg.data_ptr())
-            self._matbatch(f"{p}.ffn_up.weight", bn.data_ptr(), B, s.embed, s.ffn, bu.data_ptr())
+            self._matbatch_multi(p, ("ffn_gate", "ffn_up"), bn.data_ptr(), B, s.embed, (s.ffn, s.ffn), (bg, bu))
             L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
             self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
             self._add(bh, bp)
         self.hidden.copy_(bh[B - 1])
         return self._lm_head()
+
+    def _matbatch_multi(self, p, names, x, b, in_dim, out_dims, outs):
+        """gncx_hip_matbatch_multi over tensors {p}.{name}.weight (names "qkv"
+        stands for attn_q, attn_k, attn_v)."""
+        P, I = C.c_void_p, C.c_int32
+        if names == "qkv":
+            names = ("attn_q", "attn_k", "attn_v")
+        n = len(names)
+        w = (P * n)(*(self.m.base + self.m.off(f"{p}.{nm}.weight") for nm in names))
+        y = (P * n)(*(t.data_ptr() for t in outs))
+        self.lib.gncx_hip_matbatch_multi(n, w, (I * n)(*out_dims), self.s.layer_type, x, b, in_dim, y)
 
     def greedy(self, logits) -> int:
         return int(self.torch.argmax(logits).item())

@@ -280,6 +280,24 @@ void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_ve
  * output equals what gncx_xfold_universal_matvec gives for that matrix. */
 void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
                            int32_t ggml_type, const float* in_vec, int32_t in_dim, float* const* out_vecs);
+/* out_batches[i][batch][out_dims[i]] = the gncx_xfold_universal_matbatch
+ * product of W_i and in_batch [batch][in_dim] for count (1..4) matrices of
+ * one ggml_type, e.g. Q/K/V or gate/up of a prefill (lua/gncx_streamer.lua
+ * 1068-1071 and 1135-1136 issue them one call each); the batch is quantised once,
+ * and Q4_K matrices whose rows are whole tiles of one launch plan share one
+ * launch.  Each output is the single call's result to within fp32 summation
+ * order (a single call may split K for a small matrix). */
+void gncx_hip_matbatch_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
+                             int32_t ggml_type, const float* in_batch, int32_t batch_size, int32_t in_dim,
+                             float* const* out_batches);
+/* out_rows[count][embed_dim] = the rows of token_ids[0..count) (host memory,
+ * each in [0, vocab_size)) of the embedding table at mmap_base +
+ * tensor_abs_offset (Q8_0, Q6_K or BF16) times scale_factor, in one launch:
+ * the values of gncx_fetch_token_embedding_* per token (the streamer's prefill
+ * fetches one row per call, lua/gncx_streamer.lua:1001-1003). */
+void gncx_hip_fetch_token_embeddings(int32_t ggml_type, const uint8_t* mmap_base, size_t tensor_abs_offset,
+                                     const int32_t* token_ids, int32_t count, int32_t vocab_size, int32_t embed_dim,
+                                     float scale_factor, float* out_rows);
 /* gncx_hip_attention_step_fused (write_kv = 1) for tokens pos0 .. pos0 +
  * batch - 1 in turn, as one causal batch: q_batch [batch][n_heads*head_dim],
  * k_batch / v_batch [batch][n_kv_heads*head_dim] (q and k receive the

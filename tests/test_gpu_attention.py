@@ -262,6 +262,33 @@ def test_rmsnorm_swiglu_embeddings(lib, golden, oracle):
         assert np.array_equal(e, golden[f"emb_{name}_y11s"])
 
 
+@pytest.mark.parametrize("name,t", [("q8_0", 8), ("q6_k", 14), ("bf16", 30)])
+def test_fetch_token_embeddings_rows(lib, golden, name, t):
+    """gncx_hip_fetch_token_embeddings equals one per-token fetch per row, bit
+    for bit (and the golden rows); an id outside the table is refused on the
+    host, before anything is launched."""
+    fn = {8: lib.gncx_fetch_token_embedding_q8_0, 14: lib.gncx_fetch_token_embedding_q6_k,
+          30: lib.gncx_fetch_token_embedding_bf16}[t]
+    tab, dim = golden[f"emb_{name}_tab"].copy(), 512
+    vocab = tab.nbytes // gncx.row_bytes(t, dim)
+    ids = np.array([5, 0, vocab - 1, 11, 5, 3], np.int32)
+    out = np.full((len(ids), dim), np.nan, np.float32)
+    lib.gncx_hip_fetch_token_embeddings(t, ptr(tab), 0, ptr(ids), len(ids), vocab, dim, 0.37, ptr(out))
+    gncx.check(lib)
+    for i, tok in enumerate(ids):
+        e = np.zeros(dim, np.float32)
+        fn(ptr(tab), 0, int(tok), dim, 0.37, ptr(e))
+        gncx.check(lib)
+        assert np.array_equal(out[i], e)
+    assert np.array_equal(out[3], golden[f"emb_{name}_y11s"])
+    bad = np.array([1, vocab], np.int32)
+    before = out.copy()
+    lib.gncx_hip_fetch_token_embeddings(t, ptr(tab), 0, ptr(bad), 2, vocab, dim, 1.0, ptr(out))
+    assert lib.gncx_hip_last_status() != 0
+    assert np.array_equal(out, before)
+    lib.gncx_hip_weight_forget(ptr(tab))
+
+
 @pytest.mark.parametrize("lk", [0, 2, 3, 9, 17])
 def test_rmsnorm_encode_tokens_bitexact(lib, golden, lk):
     """The 4-phase encode runs on the device: its tokens and quant scale equal

@@ -251,6 +251,42 @@ def test_matbatch_prefill_shapes(lib, oracle, t, k, n, b):
     assert err < TOL_MATBATCH
 
 
+# Q/K/V- and gate/up-like groups through gncx_hip_matbatch_multi: the batch is
+# quantised once, and the matrices share one launch when the plan for their
+# summed rows needs no K split and each is whole tiles of it (B = 512: 128-row
+# tiles; B = 2048: 256-row tiles); otherwise one launch per matrix (B = 64 and
+# 300: split K; 1000 rows: not whole tiles).
+MULTI_CASES = [((4096, 1024, 1024), 4096, b) for b in (64, 512, 2048)] + [
+    ((1536, 1536), 1024, 300), ((4096, 1000), 2048, 2048)]
+
+
+@pytest.mark.parametrize("ns,k,b", MULTI_CASES)
+def test_matbatch_multi_matches_single_calls(lib, oracle, ns, k, b):
+    ws = [synth.make_weights(Q4_K, n, k, seed=7000 + 7 * i + n) for i, n in enumerate(ns)]
+    x = synth.make_activations(b, k, seed=7100 + b + k).reshape(b, k)
+    ys = [np.full((b, n), np.nan, np.float32) for n in ns]
+    P, I = C.c_void_p * len(ns), C.c_int32 * len(ns)
+    try:
+        lib.gncx_hip_matbatch_multi(len(ns), P(*(w.ctypes.data for w in ws)), I(*ns), Q4_K, ptr(x), b, k,
+                                    P(*(y.ctypes.data for y in ys)))
+        gncx.check(lib)
+        for i, (w, n, y) in enumerate(zip(ws, ns, ys)):
+            single = np.full((b, n), np.nan, np.float32)
+            lib.gncx_xfold_universal_matbatch(ptr(w), 0, Q4_K, ptr(x), b, k, n, ptr(single), None)
+            gncx.check(lib)
+            # the same tile arithmetic; a single call that splits K adds its
+            # ranges in another order
+            assert rel_l2(y, single) < 1e-6
+            if b == 2048 and i == 0 and ns[1] % 256 == 0:
+                assert np.array_equal(y, single)  # both unsplit 256-row tiles: bit for bit
+            err = rel_l2(y, oracle.matbatch(Q4_K, w, x, b, k, n))
+            print(f"matbatch multi {ns} k={k} b={b} matrix {i}: rel_l2 {err:.3e}", flush=True)
+            assert err < TOL_MATBATCH
+    finally:
+        for w in ws:
+            lib.gncx_hip_weight_forget(ptr(w))
+
+
 def test_lm_head_and_softcap(lib, golden):
     w, x = golden["lm_w"].copy(), golden["lm_x"].copy()
     v, k = int(golden["lm_vocab"]), int(golden["lm_k"])
