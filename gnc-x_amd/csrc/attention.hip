@@ -710,25 +710,40 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p)
             for (int r = 0; r < 16; ++r) spart[dh][8 * (r >> 2) + 4 * g + (r & 3)][32 * tt + li] = sacc[r];
         }
         __syncthreads();
-        // online softmax: wave w updates rows 8 w .. 8 w + 7, lane = key
+        // online softmax: wave w updates rows 8 w .. 8 w + 7, lane = key; the
+        // eight rows go through each step together (independent DPP max / sum
+        // reductions), then lane i < 8 updates the running max / sum of row 8 w + i
+        {
+            float sv[8], mo[8], mn[8], su[8];
+            bool valid[8];
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const int r = 8 * wv + rr;
-            const int qt = r / G;
-            const int hi = p.pos0 + q0 + qt;
-            const int lo = p.sw > 0 ? max(0, hi - p.sw + 1) : 0;
-            const int key = sa + lane;
-            const bool valid = qt < nq && key >= lo && key <= hi;
-            const float sv = valid ? (spart[0][r][lane] + spart[1][r][lane]) * p.scale : -1e30f;
-            float mx = sv;
+            for (int rr = 0; rr < 8; ++rr) {
+                const int r = 8 * wv + rr;
+                const int qt = r / G;
+                const int hi = p.pos0 + q0 + qt;
+                const int lo = p.sw > 0 ? max(0, hi - p.sw + 1) : 0;
+                const int key = sa + lane;
+                valid[rr] = qt < nq && key >= lo && key <= hi;
+                sv[rr] = valid[rr] ? (spart[0][r][lane] + spart[1][r][lane]) * p.scale : -1e30f;
+                mo[rr] = m_s[r];
+            }
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float m_old = m_s[r];
-            const float m_new = fmaxf(m_old, mx);
-            const float e = valid ? expf(sv - m_new) : 0.0f;
-            const float sum = wave_sum(e);
-            pl[r][lane] = e;
-            if (lane == 0) {
+            for (int rr = 0; rr < 8; ++rr) mn[rr] = fmaxf(mo[rr], wave_max(sv[rr]));
+#pragma unroll
+            for (int rr = 0; rr < 8; ++rr) {
+                const float e = valid[rr] ? expf(sv[rr] - mn[rr]) : 0.0f;
+                pl[8 * wv + rr][lane] = e;
+                su[rr] = wave_sum(e);
+            }
+            float m_old = mo[0], m_new = mn[0], sum = su[0];
+#pragma unroll
+            for (int rr = 1; rr < 8; ++rr) {
+                m_old = lane == rr ? mo[rr] : m_old;
+                m_new = lane == rr ? mn[rr] : m_new;
+                sum = lane == rr ? su[rr] : sum;
+            }
+            if (lane < 8) {
+                const int r = 8 * wv + lane;
                 const float a = expf(m_old - m_new);
                 alpha_s[r] = a;
                 l_s[r] = l_s[r] * a + sum;
