@@ -512,13 +512,25 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 // The matrices of one Q4_K launch (one activation batch, the same K): x-tiles
 // [tile0[i], tile0[i + 1]) are matrix i, n[i] rows, output y[i] [b x n[i]].
 // A work-group picks its matrix with scalar compares and selects over the
-// kernel arguments.
+// kernel arguments.  With split K the partials of range z are one [b x ntot]
+// block, matrix i's [b x n[i]] part at b npre[i] in it (npre: rows of the
+// matrices before i).
 constexpr int kMaxMbMats = 4;
 struct MbMats {
     const uint8_t* w[kMaxMbMats];
     float* y[kMaxMbMats];
     int32_t n[kMaxMbMats];
     int32_t tile0[kMaxMbMats];
+    int32_t npre[kMaxMbMats];
+    int32_t ntot;
+    int32_t count;
+};
+
+// The outputs of a split-K reduce: flat partial indices [end[i - 1], end[i])
+// go to y[i] (end[-1] = 0), each y[i] one contiguous [b x n] block.
+struct RedMats {
+    float* y[kMaxMbMats];
+    size_t end[kMaxMbMats];
     int32_t count;
 };
 
@@ -529,7 +541,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
     const uint8_t* __restrict w = mats.w[0];
     float* __restrict y = mats.y[0];
-    int32_t n = mats.n[0], tile0 = 0;
+    int32_t n = mats.n[0], tile0 = 0, npre = 0;
 #pragma unroll
     for (int i = 1; i < kMaxMbMats; ++i) {
         if (mats.count > i && static_cast<int32_t>(blockIdx.x) >= mats.tile0[i]) {
@@ -537,6 +549,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             y = mats.y[i];
             n = mats.n[i];
             tile0 = mats.tile0[i];
+            npre = mats.npre[i];
         }
     }
     constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
@@ -892,7 +905,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             }
         }
     }
-    float* dst = gridDim.z > 1 ? part + static_cast<size_t>(blockIdx.z) * b * n : y;
+    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -906,15 +919,34 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
         }
 }
 
-// y = sum over the split K ranges, added in range order (deterministic)
+// y = sum over the split K ranges, added in range order (deterministic);
+// range z's partials are the flat block [z count, (z + 1) count)
 __global__ __launch_bounds__(kThreads) void matbatch_reduce_kernel(const float* __restrict part, int32_t splits,
-                                                                   size_t count, float* __restrict y) {
+                                                                   RedMats r) {
+    const size_t count = r.end[r.count - 1];
     for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
          i += static_cast<size_t>(gridDim.x) * kThreads) {
         float acc = part[i];
         for (int32_t z = 1; z < splits; ++z) acc += part[static_cast<size_t>(z) * count + i];
-        y[i] = acc;
+        float* y = r.y[0];
+        size_t first = 0;
+#pragma unroll
+        for (int m = 1; m < kMaxMbMats; ++m) {
+            if (r.count > m && i >= r.end[m - 1]) {
+                y = r.y[m];
+                first = r.end[m - 1];
+            }
+        }
+        y[i - first] = acc;
     }
+}
+
+hipError_t launch_reduce(const float* part, int32_t splits, const RedMats& r, hipStream_t stream) {
+    size_t g = (r.end[r.count - 1] + kThreads - 1) / kThreads;
+    if (g > 4096) g = 4096;
+    hipLaunchKernelGGL(matbatch_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(kThreads), 0, stream, part,
+                       splits, r);
+    return hipGetLastError();
 }
 
 struct MfmaPlan {
@@ -925,11 +957,13 @@ struct MfmaPlan {
 
 // From 256 tokens, 256-token tiles of 8 waves (one work-group per CU, 111 KB
 // of LDS): 256 x 128 when that gives at least 192 tiles, else 256 x 64 when
-// that does (with fewer, split K on 64 x 64 tiles measured faster).  Twice the tokens per dequantised weight step, with the
-// dequantising waves and MFMA-only waves sharing each SIMD, measured 1.1-1.4x
-// the 128 x 128 tile (Q4_K 4096 x 14336 at B = 512: 111 vs 141 us; 4096 x 4096
-// at B = 2048: 116 vs 149 us) and bit-identical results (same K order).
-// Otherwise the largest tile whose grid fills every CU with as many
+// that does, else 256 x 128 with K split until about 256 work-groups run
+// (Q6_K 14336 -> 4096 at B = 256 / 512: 144 / 258 us against 268 / 480 us
+// for the 64 x 64 tiles with K split used before).  Twice the tokens per
+// dequantised weight step, with the dequantising waves and MFMA-only waves
+// sharing each SIMD, measured 1.1-1.4x the 128 x 128 tile (Q4_K 4096 x 14336
+// at B = 512: 111 vs 141 us; 4096 x 4096 at B = 2048: 116 vs 149 us) and
+// bit-identical results (same K order).  Below 256 tokens, the largest tile whose grid fills every CU with as many
 // work-groups as its LDS lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for
 // 64 x 64), else 64 x 64 tiles with K split until it does (ranges of at
 // least 256).
@@ -939,8 +973,16 @@ MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
     };
     if (b >= 256) {
         const int64_t mt = (b + 255) / 256;
-        if (static_cast<int64_t>((n + 127) / 128) * mt >= 192) return {2, 2, 1, k, 4};
+        const int64_t t = static_cast<int64_t>((n + 127) / 128) * mt;
+        if (t >= 192) return {2, 2, 1, k, 4};
         if (static_cast<int64_t>((n + 63) / 64) * mt >= 192) return {2, 1, 1, k, 4};
+        // fewer tiles: 256 x 128 with K split (ranges of whole 256-value
+        // blocks) until about 256 work-groups run
+        int32_t splits = static_cast<int32_t>(256 / t);
+        if (splits > k / 256) splits = k / 256;
+        if (splits <= 1) return {2, 2, 1, k, 4};
+        const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
+        return {2, 2, (k + kchunk - 1) / kchunk, kchunk, 4};
     }
     const int cand[3][3] = {{2, 2, 2}, {2, 1, 2}, {1, 1, 4}};
     for (const auto& c : cand)
@@ -979,42 +1021,46 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
     else if (p.wm == 2) e = launch_mfma_t<TYPE, 2, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
     else e = launch_mfma_t<TYPE, 1, 1>(w, xhl, rscale, b, k, n, y, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
-    const size_t count = static_cast<size_t>(b) * n;
-    size_t g = (count + kThreads - 1) / kThreads;
-    if (g > 4096) g = 4096;
-    hipLaunchKernelGGL(matbatch_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(kThreads), 0, stream, part,
-                       p.splits, count, y);
-    return hipGetLastError();
+    RedMats r{};
+    r.y[0] = y;
+    r.end[0] = static_cast<size_t>(b) * n;
+    r.count = 1;
+    return launch_reduce(part, p.splits, r, stream);
 }
 
 // Q4_K tiles: (waves along tokens, along rows, tiles per wave along each)
 struct Q4kPlan {
-    int cfg;  // 0: 128 x 256 (8 waves); 2: 128 x 128 (4 waves, one work-group per CU); 3: 64 x 64 (4 waves)
+    int cfg;  // 0: 128 tokens x 256 rows (8 waves, one work-group per CU); 3: 64 x 64 (4 waves)
     int32_t splits, kchunk;
 };
 
-// Measured on Q4_K 4096 x 4096, 4096 -> 14336 (B = 64, 256, 512) and the
-// B = 2048 prefill matrices: 128 x 256 tiles once they fill three quarters of
-// the CUs (B = 512 on the gate/up shape, every B = 2048 shape); 128 x 128 at
-// one work-group per CU when those do (B = 256 on 4096 -> 14336: 147 against
-// 181 us); otherwise 64 x 64 tiles with K split until about 512 work-groups
-// run (ranges of whole super-blocks).
+// Past 64 tokens, 128 x 256 tiles with K split into ranges of whole
+// super-blocks until about 256 work-groups run (one per CU).  Measured full
+// calls (quantisation, product, reduce) against the tile choice before it
+// (128 x 256 only from 192 tiles, else 128 x 128 from 192 tiles, else 64 x 64
+// with K split to about 512 work-groups): Q4_K 4096 x 4096 at B = 128 / 256 /
+// 512 / 1024: 38 / 48 / 68 / 115 against 41 / 66 / 108 / 140 us; 4096 -> 14336
+// at B = 128 / 256 / 384: 65 / 103 / 157 against 108 / 130 / 235 us; 12288 ->
+// 4096 at B = 256 / 512: 93 / 158 against 170 / 305 us; B = 2048 unchanged (no
+// split).  Up to 64 tokens, 64 x 64 tiles with K split until about 512
+// work-groups run (B = 64: 30 us on 4096 x 4096, against 35 us for the
+// 128 x 256 tiles).
 Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
     auto tiles = [&](int bm, int bn) {
         return static_cast<int64_t>((n + bn - 1) / bn) * ((b + bm - 1) / bm);
     };
-    if (b >= 512 && tiles(128, 256) >= 192) return {0, 1, k};
-    if (b >= 128 && tiles(128, 128) >= 192) return {2, 1, k};
-    const int64_t t = tiles(64, 64);
-    int32_t splits = static_cast<int32_t>((512 + t - 1) / t);
+    const bool big = b > 64;
+    const int64_t t = big ? tiles(128, 256) : tiles(64, 64);
+    const int64_t want = big ? 256 : 512;
+    int32_t splits = static_cast<int32_t>(big ? want / t : (want + t - 1) / t);
     if (splits > k / 256) splits = k / 256;
     if (splits < 1) splits = 1;
     const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
-    return {3, (k + kchunk - 1) / kchunk, kchunk};
+    return {big ? 0 : 3, (k + kchunk - 1) / kchunk, kchunk};
 }
 
 // rows per x-tile of each Q4_K configuration
-int32_t q4k_tile_rows(int cfg) { return cfg == 0 ? 256 : cfg == 2 ? 128 : 64; }
+int32_t q4k_tile_rows(int cfg) { return cfg == 0 ? 256 : 64; }
 
 template <int WM, int WN, int MW, int NW>
 hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
@@ -1027,19 +1073,27 @@ hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq
     return hipGetLastError();
 }
 
+// The product of plan p over the matrices of m (w, y, n and count set), then
+// with split K the reduce of the partials into each y
 hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
                            int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
     const int32_t bn = q4k_tile_rows(p.cfg);
-    int32_t t = 0;
+    int32_t t = 0, rows = 0;
+    RedMats r{};
     for (int32_t i = 0; i < m.count; ++i) {
         m.tile0[i] = t;
+        m.npre[i] = rows;
         t += (m.n[i] + bn - 1) / bn;
+        rows += m.n[i];
+        r.y[i] = m.y[i];
+        r.end[i] = static_cast<size_t>(b) * rows;
     }
-    switch (p.cfg) {
-    case 0: return launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
-    case 2: return launch_q4k_t<2, 2, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
-    default: return launch_q4k_t<1, 1, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
-    }
+    m.ntot = rows;
+    r.count = m.count;
+    const hipError_t e = p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
+                                    : launch_q4k_t<1, 1, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
+    if (e != hipSuccess || p.splits == 1) return e;
+    return launch_reduce(part, p.splits, r, stream);
 }
 
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
@@ -1048,20 +1102,12 @@ hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, in
                        rscale, pq);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const Q4kPlan p = q4k_plan(b, k, n);
     MbMats m{};
     m.w[0] = w;
     m.y[0] = y;
     m.n[0] = n;
     m.count = 1;
-    e = launch_q4k_mats(m, xhl, pq, rscale, b, k, p, part, stream);
-    if (e != hipSuccess || p.splits == 1) return e;
-    const size_t count = static_cast<size_t>(b) * n;
-    size_t g = (count + kThreads - 1) / kThreads;
-    if (g > 4096) g = 4096;
-    hipLaunchKernelGGL(matbatch_reduce_kernel, dim3(static_cast<unsigned>(g)), dim3(kThreads), 0, stream, part,
-                       p.splits, count, y);
-    return hipGetLastError();
+    return launch_q4k_mats(m, xhl, pq, rscale, b, k, q4k_plan(b, k, n), part, stream);
 }
 
 template <int TYPE>
@@ -1132,16 +1178,16 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
 
 namespace {
 
-// One launch over count Q4_K matrices sharing the activation batch: when the
-// plan for the summed rows needs no K split and every matrix is whole x-tiles
-// of it (false otherwise, and the matrices go one launch each).
-bool multi_fused(int32_t type, int32_t count, const int32_t* ns, int32_t b, int32_t k, Q4kPlan& p) {
+// One launch over count Q4_K matrices sharing the activation batch (and with
+// split K one reduce over all of them): when every matrix is whole x-tiles of
+// the plan for the summed rows (false otherwise, and the matrices go one call
+// each).
+bool multi_fused(int32_t type, int32_t count, const int32_t* ns, int32_t b, int32_t k, Q4kPlan& p, int64_t& total) {
     if (type != kQ4_K || count < 2 || count > kMaxMbMats || b <= 0 || k <= 0 || (k % 256) != 0) return false;
-    int64_t total = 0;
+    total = 0;
     for (int32_t i = 0; i < count; ++i) total += ns[i];
     if (total > INT32_MAX) return false;
     p = q4k_plan(b, k, static_cast<int32_t>(total));
-    if (p.splits != 1) return false;
     const int32_t bn = q4k_tile_rows(p.cfg);
     for (int32_t i = 0; i < count; ++i)
         if (ns[i] % bn != 0) return false;
@@ -1154,8 +1200,11 @@ size_t matbatch_multi_workspace_bytes(int32_t type, int32_t count, const int32_t
     size_t need = 256;
     for (int32_t i = 0; i < count; ++i) need = std::max(need, matbatch_workspace_bytes(type, b, k, ns[i]));
     Q4kPlan p;
-    if (multi_fused(type, count, ns, b, k, p))
-        need = std::max(need, xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b) + 256);
+    int64_t total;
+    if (multi_fused(type, count, ns, b, k, p, total)) {
+        const size_t parts = p.splits > 1 ? static_cast<size_t>(p.splits) * b * total * sizeof(float) : 0;
+        need = std::max(need, xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b) + parts + 256);
+    }
     return need;
 }
 
@@ -1167,7 +1216,8 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
         if (ns[i] <= 0 || !ws[i] || !ys[i]) return hipErrorInvalidValue;
     if (workspace_bytes < matbatch_multi_workspace_bytes(type, count, ns, b, k)) return hipErrorInvalidValue;
     Q4kPlan p;
-    if (!multi_fused(type, count, ns, b, k, p)) {
+    int64_t total;
+    if (!multi_fused(type, count, ns, b, k, p, total)) {
         for (int32_t i = 0; i < count; ++i) {
             const hipError_t e = launch_matbatch(type, ws[i], x, b, k, ns[i], ys[i], workspace, workspace_bytes, stream);
             if (e != hipSuccess) return e;
@@ -1183,6 +1233,7 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
     _Float16* xhl = reinterpret_cast<_Float16*>(wsp);
     _Float16* pq = reinterpret_cast<_Float16*>(wsp + xh_bytes(b, k));
     float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
+    float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
                        rscale, pq);
@@ -1195,7 +1246,7 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
         m.n[i] = ns[i];
     }
     m.count = count;
-    return launch_q4k_mats(m, xhl, pq, rscale, b, k, p, nullptr, stream);
+    return launch_q4k_mats(m, xhl, pq, rscale, b, k, p, part, stream);
 }
 
 }  // namespace gncx
