@@ -955,23 +955,25 @@ struct MfmaPlan {
     int mw = 2;  // waves along the tokens (4: 512-thread work-groups)
 };
 
-// From 256 tokens, 256-token tiles of 8 waves (one work-group per CU, 111 KB
+// From 129 tokens, 256-token tiles of 8 waves (one work-group per CU, 111 KB
 // of LDS): 256 x 128 when that gives at least 192 tiles, else 256 x 64 when
-// that does, else 256 x 128 with K split until about 256 work-groups run
-// (Q6_K 14336 -> 4096 at B = 256 / 512: 144 / 258 us against 268 / 480 us
-// for the 64 x 64 tiles with K split used before).  Twice the tokens per
-// dequantised weight step, with the dequantising waves and MFMA-only waves
-// sharing each SIMD, measured 1.1-1.4x the 128 x 128 tile (Q4_K 4096 x 14336
-// at B = 512: 111 vs 141 us; 4096 x 4096 at B = 2048: 116 vs 149 us) and
-// bit-identical results (same K order).  Below 256 tokens, the largest tile whose grid fills every CU with as many
-// work-groups as its LDS lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for
-// 64 x 64), else 64 x 64 tiles with K split until it does (ranges of at
-// least 256).
+// that does, else 256 x 128 with K split until about 256 work-groups run.
+// Twice the tokens per dequantised weight step, with the dequantising waves
+// and MFMA-only waves sharing each SIMD, measured 1.1-1.4x the 128 x 128 tile
+// (Q4_K 4096 x 14336 at B = 512: 111 vs 141 us; 4096 x 4096 at B = 2048: 116
+// vs 149 us) with bit-identical results (same K order); with K split, Q6_K
+// 14336 -> 4096 at B = 200 / 256 / 512 took 139 / 144 / 258 us against 266 /
+// 268 / 480 us for 64 x 64 tiles with K split.  From 65 to 128 tokens,
+// 128 x 128 tiles of 4 waves with K split until about 512 work-groups run
+// (Q6_K 14336 -> 4096 at B = 128: 108 against 157 us).  Up to 64 tokens, the
+// largest tile whose grid fills every CU with as many work-groups as its LDS
+// lets one CU hold (2 for 128 x 128 and 128 x 64, 4 for 64 x 64), else 64 x 64
+// tiles with K split until it does (ranges of at least 256).
 MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
     auto tiles = [&](int wm, int wn) {
         return static_cast<int64_t>((n + 64 * wn - 1) / (64 * wn)) * ((b + 64 * wm - 1) / (64 * wm));
     };
-    if (b >= 256) {
+    if (b > 128) {
         const int64_t mt = (b + 255) / 256;
         const int64_t t = static_cast<int64_t>((n + 127) / 128) * mt;
         if (t >= 192) return {2, 2, 1, k, 4};
@@ -983,6 +985,15 @@ MfmaPlan mfma_plan(int32_t b, int32_t k, int32_t n) {
         if (splits <= 1) return {2, 2, 1, k, 4};
         const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
         return {2, 2, (k + kchunk - 1) / kchunk, kchunk, 4};
+    }
+    if (b > 64) {
+        // 128 x 128 tiles of 4 waves, with K split until about 512 work-groups run
+        const int64_t t = tiles(2, 2);
+        int32_t splits = static_cast<int32_t>(512 / t);
+        if (splits > k / 256) splits = k / 256;
+        if (splits <= 1) return {2, 2, 1, k};
+        const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
+        return {2, 2, (k + kchunk - 1) / kchunk, kchunk};
     }
     const int cand[3][3] = {{2, 2, 2}, {2, 1, 2}, {1, 1, 4}};
     for (const auto& c : cand)

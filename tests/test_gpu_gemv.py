@@ -213,8 +213,10 @@ MATBATCH_CASES = [
     # the 256-token tiles of 8 waves (256 x 128 and 256 x 64), ragged B and N
     (Q6_K, 256, 24576, 260), (Q4_K, 256, 8192, 300), (Q8_0, 512, 6000, 257),
     # the 8-wave tiles with K split (Q4_K 128 x 256 from 65 tokens; 256 x 128
-    # from 256 tokens for the other types), ragged B and N
+    # from 129 tokens for the other types), ragged B and N
     (Q4_K, 2048, 1000, 100), (Q4_K, 4096, 3000, 65), (Q6_K, 4096, 1000, 300), (Q8_0, 2080, 700, 400),
+    # 128 x 128 tiles of 4 waves with K split (65 to 128 tokens, types other than Q4_K)
+    (Q8_0, 1024, 640, 128), (Q6_K, 14336, 512, 77),
 ]
 
 
