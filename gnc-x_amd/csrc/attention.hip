@@ -34,7 +34,15 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHeadBlock = 4;     // query heads handled per pass (one wave each in the softmax)
 constexpr int kMaxChunk = 1024;   // tokens per work-group
+// Work-groups a call aims for: windows that fit 32-token chunks at kTargetGroups
+// keep those (one pass per work-group, K/V loaded up front); longer windows
+// take about half as many, longer chunks.  Measured per call, GQA 32/8 x 128
+// (chunk + merge), 1024 / 512 target work-groups: ctx 2100: 13.8 / 18.0 us;
+// ctx 4096: 16.1 / 17.3; ctx 8192: 27.6 / 26.5; ctx 16384: 42.5 / 34.5;
+// ctx 32768: 63.2 / 56.4; ctx 65536: 110 / 101; GQA 32/4 ctx 32768: 60.7 /
+// 52.6 us.
 constexpr int kTargetGroups = 1024;
+constexpr int kTargetGroupsLong = 512;
 
 struct AttnParams {
     const float* q;
@@ -932,12 +940,16 @@ Plan make_plan(int32_t pos, int32_t sw, int32_t n_kv, int32_t G, int32_t hd) {
     pl.t0 = sw > 0 ? (pos - sw + 1 > 0 ? pos - sw + 1 : 0) : 0;
     pl.t1 = pos + 1;
     const int32_t win = pl.t1 - pl.t0;
-    int32_t want = kTargetGroups / (n_kv > 0 ? n_kv : 1);
-    if (want < 1) want = 1;
-    int32_t chunk = (win + want - 1) / want;
-    chunk = ((chunk + 31) / 32) * 32;
-    if (chunk < 32) chunk = 32;
-    if (chunk > kMaxChunk) chunk = kMaxChunk;
+    auto chunk_for = [&](int32_t groups) {
+        int32_t want = groups / (n_kv > 0 ? n_kv : 1);
+        if (want < 1) want = 1;
+        int32_t c = (win + want - 1) / want;
+        c = ((c + 31) / 32) * 32;
+        if (c < 32) c = 32;
+        return c > kMaxChunk ? kMaxChunk : c;
+    };
+    int32_t chunk = chunk_for(kTargetGroups);
+    if (chunk > 32) chunk = chunk_for(kTargetGroupsLong);
     while (chunk > 32 && lds_bytes(chunk, G, hd) > kLdsBudget) chunk -= 32;
     // the merge weighs at most kMergeMaxSplit chunks
     while ((win + chunk - 1) / chunk > kMergeMaxSplit) chunk += 32;
