@@ -70,6 +70,7 @@ __global__ __launch_bounds__(kThreads) void matbatch_rowtok_kernel(const uint8_t
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // fp16 pair (hi, lo) of a float: hi = fp16(v) and lo = fp16(v - hi), with
@@ -717,15 +718,21 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             int sc, mn;
             k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
             const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
+            // sc q as fp16, two codes per instruction: a byte permute puts
+            // codes a and c under the exponent of 1024 (fp16 bits 0x6400 | a
+            // are 1024 + a), and one packed fma gives (1024 + a) sc - 1024 sc
+            // = a sc with a single rounding of an exact value (a sc <= 945)
+            const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
+            const _Float16 off = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
+            const half2 s2 = {scf, scf}, m2 = {off, off};
             uint32_t o[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t a = (qw[e >> 1] >> (sh + 16 * (e & 1))) & 15u;
-                const uint32_t c = (qw[e >> 1] >> (sh + 16 * (e & 1) + 8)) & 15u;
-                const _Float16 ha = static_cast<_Float16>(static_cast<float>(static_cast<int>(a) * sc));
-                const _Float16 hc = static_cast<_Float16>(static_cast<float>(static_cast<int>(c) * sc));
-                o[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
-                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hc)) << 16);
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t x = (qw[d] >> sh) & 0x0f0f0f0fu;
+                const half2 p0 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
+                const half2 p1 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
+                o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p0, s2, m2));
+                o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p1, s2, m2));
             }
             *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
             *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
