@@ -494,7 +494,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     args = ap.parse_args()
     if args.traffic_json:
-        cmd = "rocprofv3 --pmc {c} --output-format csv -d gpurun_out/traffic -o {o} -- python3 bench.py " \
+        cmd = "rocprofv3 --pmc {c} --output-format csv -d rocprof_out/traffic -o {o} -- python3 bench.py " \
               "--steps 200 --warmup 20 --no-extra --no-cpu --no-decode"
         print(json.dumps(write_traffic_json(*args.traffic_json, [cmd.format(c="FETCH_SIZE", o="fetch"),
                                                                  cmd.format(c="WRITE_SIZE", o="write")])))
