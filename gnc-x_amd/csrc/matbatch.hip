@@ -554,8 +554,8 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
         }
     }
     constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage and half; whole blocks per wave
-    static_assert(XBLK % WAVES == 0, "whole activation blocks per wave");
+    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage and half
+    static_assert((2 * XBLK) % WAVES == 0, "the same number of activation loads for every wave");
     static_assert(2 * BN <= THREADS && BM <= THREADS, "one weight piece and one P row per thread at most");
     // ring stages as separate arrays: the compiler then sees that a
     // direct-to-LDS load into one stage does not alias reads of another and
@@ -569,20 +569,20 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     __shared__ __align__(16) _Float16 sp[2][2][BM * 8];          // [super-block parity][hi, lo] P of 8 blocks
     __shared__ __align__(16) _Float16 smn[2][BN * 8];            // [super-block parity] mins of 8 blocks
     __shared__ __align__(8) float sdm[2][BN][2];                 // [super-block parity] d, dmin
-    // WDMA: the raw weights stream through LDS as well, by direct-to-LDS loads
+    // The raw weights stream through LDS as well, by direct-to-LDS loads
     // with no registers in flight (register loads of them put memory waits on
     // every step): a ring of 4 stages of each row's 32 qs bytes of a step's
     // sub-block pair, and per super-block parity the rows' 16-byte headers and
     // the tokens' P pairs, loaded at the 5th step of the super-block before.
     // Every wave issues the same number of these loads (vmcnt is per wave).
-    constexpr bool WDMA = (BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
-                          (BM * 16) % (THREADS * 4) == 0;
-    constexpr int kWQ = WDMA ? BN * 32 : 16;
-    __shared__ __align__(16) uint8_t wq0[kWQ], wq1[kWQ], wq2[kWQ], wq3[kWQ];
-    __shared__ __align__(16) uint8_t whd[2][WDMA ? BN * 16 : 16];  // [super-block parity] raw headers
+    static_assert((BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
+                      (2 * BM * 16) % (THREADS * 4) == 0,
+                  "the same number of weight, header and P loads for every wave");
+    __shared__ __align__(16) uint8_t wq0[BN * 32], wq1[BN * 32], wq2[BN * 32], wq3[BN * 32];
+    __shared__ __align__(16) uint8_t whd[2][BN * 16];  // [super-block parity] raw headers
     auto wstage = [&](int stage) -> uint8_t* { return stage == 0 ? wq0 : stage == 1 ? wq1 : stage == 2 ? wq2 : wq3; };
-    constexpr int kWLoads = WDMA ? BN * 32 / (THREADS * 16) : 0;                      // per wave and step
-    constexpr int kHLoads = WDMA ? BN * 16 / (THREADS * 4) + 2 * (BM * 16 / (THREADS * 4)) : 0;  // per super-block
+    constexpr int kWLoads = BN * 32 / (THREADS * 16);                                  // per wave and step
+    constexpr int kHLoads = BN * 16 / (THREADS * 4) + 2 * BM * 16 / (THREADS * 4);   // per super-block
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int li = lane & 31, lh = lane >> 5;
@@ -604,7 +604,6 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
         wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
-    const int32_t wbase = tid < 2 * BN && wrow < wrows_here ? wrow * static_cast<int32_t>(rbytes) : kMfOob / 2;
 
     floatx16 acc[WM][WN], D[WM][WN];
 #pragma unroll
@@ -614,47 +613,29 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = D[i][j][r] = 0.0f;
 
-    uint4 pr[2];
-    u32x4 hdr[2], qv[2];
-    // activations of the step at k0 into ring stage `stage`: block blk (token
-    // rows 16 blk .. + 16) is 64 lanes x 16 B; lane L lands at segment
-    // position L % 4 of row L / 4, which holds logical segment
-    // (L % 4) ^ ((row / 4) % 4).  Past the range: zeros.
+    // activations of the step at k0 into ring stage `stage`: load q of the
+    // step is block q % XBLK (token rows 16 blk .. + 16) of half q / XBLK,
+    // 64 lanes x 16 B; lane L lands at segment position L % 4 of row L / 4,
+    // which holds logical segment (L % 4) ^ ((row / 4) % 4).  Past the
+    // range: zeros.
+    constexpr int kXLoads = 2 * XBLK / WAVES;  // ring loads per wave and step
     auto dma_x = [&](int stage, int32_t k0) {
 #pragma unroll
-        for (int blk = wv; blk < XBLK; blk += WAVES) {
+        for (int i = 0; i < kXLoads; ++i) {
+            const int q = i * WAVES + wv, blk = q % XBLK, half = q / XBLK;
             const int row = 16 * blk + (lane >> 2);
             const int lseg = (lane & 3) ^ ((row >> 2) & 3);
             const int32_t off = k0 < ke ? (row * k + k0 + 8 * lseg) * 2 * static_cast<int32_t>(sizeof(_Float16))
                                         : kMfOob;
             _Float16(*xs)[BM * 32] = xstage(stage);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[0][blk * 16 * 32], 16, off, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[1][blk * 16 * 32], 16, off + 16, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[half][blk * 16 * 32], 16, off + 16 * half, 0,
+                                                     0, 0);
         }
     };
-    constexpr int kXLoads = 2 * (XBLK / WAVES);  // ring loads per wave and step
-    auto gload_p = [&](int32_t k0) {  // P of the super-block starting at k0
-        const int32_t off = k0 < ke && tid < BM
-                                ? (tid * sbs_row + k0 / 256) * 16 * static_cast<int32_t>(sizeof(_Float16))
-                                : kMfOob;
-        const u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 0);
-        const u32x4 l = __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16, 0, 0);
-        pr[0] = make_uint4(h.x, h.y, h.z, h.w);
-        pr[1] = make_uint4(l.x, l.y, l.z, l.w);
-    };
-    // header and the 16 code bytes of piece (wrow, whalf) of the 32-block at
-    // k0; past the range the base moves past the resource (reads zeros)
-    auto gload_w = [&](int set, int32_t k0) {
-        const int32_t base = k0 < ke ? wbase : kMfOob / 2;
-        const int32_t kk = k0 < ke ? k0 : 0;
-        const int32_t blk = (kk / 256) * 144, rr = kk % 256;
-        hdr[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk, 0, 0);
-        qv[set] = __builtin_amdgcn_raw_buffer_load_b128(wrs, base + blk + 16 + 32 * (rr / 64) + 16 * whalf, 0, 0);
-    };
-    // WDMA: raw qs of the step at k0 (each row's 32 bytes of its sub-block
+    // raw qs of the step at k0 (each row's 32 bytes of its sub-block
     // pair) into ring stage `stage`, 16 bytes per lane in row order
     auto dma_w = [&](int stage, int32_t k0) {
-        if constexpr (WDMA) {
+        {
             const int32_t kk = k0 < ke ? k0 : 0;
             const int32_t koff = (kk / 256) * 144 + 16 + 32 * ((kk % 256) / 64);
 #pragma unroll
@@ -669,12 +650,13 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             }
         }
     };
-    // WDMA: the rows' headers (d, dmin, scales) and the tokens' P pairs of the
+    // the rows' headers (d, dmin, scales) and the tokens' P pairs of the
     // super-block at s0 into parity `par`, 4 bytes per lane in row order
     auto dma_hp = [&](int par, int32_t s0) {
-        if constexpr (WDMA) {
+        {
             const bool in = s0 < ke;
-            constexpr int HL = BN * 16 / (THREADS * 4), PL = BM * 16 / (THREADS * 4);
+            // P: load q is dwords (q % PH) 64 .. + 64 of half q / PH
+            constexpr int HL = BN * 16 / (THREADS * 4), PH = BM * 16 / (64 * 4), PL = 2 * PH / WAVES;
 #pragma unroll
             for (int i = 0; i < HL; ++i) {
                 const int dw = (i * WAVES + wv) * 64 + lane;
@@ -686,35 +668,27 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
                                                          0, 0);
             }
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int i = 0; i < PL; ++i) {
-                    const int dw = (i * WAVES + wv) * 64 + lane;
-                    const int row = dw >> 2;
-                    const int32_t off = in && row < rows_here
-                                            ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) *
-                                                      static_cast<int32_t>(sizeof(_Float16)) +
-                                                  4 * (dw & 3)
-                                            : kMfOob;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][(i * WAVES + wv) * 128]), 4,
-                                                             off, 0, 0, 0);
-                }
+            for (int i = 0; i < PL; ++i) {
+                const int q = i * WAVES + wv, h = q / PH, qq = q % PH;
+                const int dw = qq * 64 + lane;
+                const int row = dw >> 2;
+                const int32_t off = in && row < rows_here
+                                        ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) *
+                                                  static_cast<int32_t>(sizeof(_Float16)) +
+                                              4 * (dw & 3)
+                                        : kMfOob;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][qq * 128]), 4, off, 0, 0, 0);
+            }
         }
     };
-    // weights of the step at k0 (register set `set`, or ring stage `set` with
-    // WDMA, headers of parity `hpar`) into LDS buffer `buf`; at a super-block's
-    // first step also its d, dmin and mins (and without WDMA its P), parity hpar
+    // weights of the step at k0 (ring stage `set`, headers of parity `hpar`)
+    // into LDS buffer `buf`; at a super-block's first step also its d, dmin
+    // and mins, parity hpar
     auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int hpar) {
         if (tid < 2 * BN) {
             const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
-            u32x4 hh, qq;
-            if constexpr (WDMA) {
-                hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
-                qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
-            } else {
-                hh = hdr[set & 1];
-                qq = qv[set & 1];
-            }
+            const u32x4 hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
+            const u32x4 qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
             int sc, mn;
             k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
             const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
@@ -751,12 +725,6 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
                                  (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
                 }
                 *reinterpret_cast<uint4*>(&smn[hpar][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
-            }
-        }
-        if constexpr (!WDMA) {
-            if (sb_first && tid < BM) {
-                *reinterpret_cast<uint4*>(&sp[hpar][0][tid * 8]) = pr[0];
-                *reinterpret_cast<uint4*>(&sp[hpar][1][tid * 8]) = pr[1];
             }
         }
     };
@@ -828,38 +796,23 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
                 }
     };
 
-    // Prologue: steps 0-2 into ring stages 0-2, step 0's weights and its
-    // super-block's constants into LDS, step 1's weights in register set 1.
-    // Loads are issued in the order P, x0, w0, x1, w1, x2 so that vmcnt(8)
-    // covers the first ring stage.
-    if constexpr (WDMA) {
-        // headers and P of super-block 0, then steps 0-2 of activations and
-        // raw weights; step 0's weights are dequantised once the first three
-        // groups of loads are in LDS for every wave
-        dma_hp(0, kb);
-        dma_x(0, kb);
-        dma_w(0, kb);
-        dma_x(1, kb + 32);
-        dma_w(1, kb + 32);
-        dma_x(2, kb + 64);
-        dma_w(2, kb + 64);
-        step_barrier<2 * (kXLoads + kWLoads)>();
-        lstore(0, 0, kb, true, 0);
-        step_barrier<kXLoads + kWLoads>();
-    } else {
-        gload_p(kb);
-        dma_x(0, kb);
-        gload_w(0, kb);
-        dma_x(1, kb + 32);
-        gload_w(1, kb + 32);
-        dma_x(2, kb + 64);
-        lstore(0, 0, kb, true, 0);
-        step_barrier<2 * kXLoads + 2>();
-    }
-    // Per step: the activation ring load 3 steps ahead, the weights 3 steps
-    // ahead (WDMA, plus the next super-block's headers and P at its 5th step)
-    // or 2 steps ahead into registers (P at the 7th step); compute; the next
-    // step's weights dequantised into LDS; then the barrier (below).
+    // Prologue: the headers and P of super-block 0, then steps 0-2 of
+    // activations and raw weights into ring stages 0-2; step 0's weights are
+    // dequantised once the first three groups of loads are in LDS for every
+    // wave.
+    dma_hp(0, kb);
+    dma_x(0, kb);
+    dma_w(0, kb);
+    dma_x(1, kb + 32);
+    dma_w(1, kb + 32);
+    dma_x(2, kb + 64);
+    dma_w(2, kb + 64);
+    step_barrier<2 * (kXLoads + kWLoads)>();
+    lstore(0, 0, kb, true, 0);
+    step_barrier<kXLoads + kWLoads>();
+    // Per step: the activation and raw-weight ring loads 3 steps ahead (plus
+    // the next super-block's headers and P at its 5th step); compute; the
+    // next step's weights dequantised into LDS; then the barrier (below).
     for (int32_t sb = 0; sb < nsb; ++sb) {
         const int32_t s0 = kb + sb * 256;
         const int sbp = sb & 1;
@@ -869,17 +822,12 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
             const int buf = st & 1;  // 8 steps per super-block keep every parity static
             auto issue_loads = [&]() {
                 dma_x((st + 3) & 3, k0 + 96);
-                if constexpr (WDMA) {
-                    dma_w((st + 3) & 3, k0 + 96);
-                    if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
-                } else {
-                    if (st == 6) gload_p(s0 + 256);
-                    gload_w(buf, k0 + 64);
-                }
+                dma_w((st + 3) & 3, k0 + 96);
+                if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
             };
-            // the step dequantised here is k0 + 32: its raw weights (ring
-            // stage or register set) and its super-block's parity
-            const int wset = WDMA ? ((st + 1) & 3) : (buf ^ 1);
+            // the step dequantised here is k0 + 32: its raw weights' ring
+            // stage and its super-block's parity
+            const int wset = (st + 1) & 3;
             const int hpar = st == 7 ? (sbp ^ 1) : sbp;
             // the two waves on each SIMD (waves w and w + WAVES / 2) take the
             // step's MFMA and VALU phases in opposite orders (staging writes
@@ -899,17 +847,10 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
                 compute(st & 3, buf);
                 if (st == 7) fold(sbp);
             }
-            // WDMA: the next step reads loads issued one and two steps ago;
-            // only this step's may still run (and at the 5th step its
-            // headers and P).  Otherwise: the ring stage the next step reads
-            // was issued two steps ago; the loads issued since then are at
-            // most 2 + 2 (w) + 2 kXLoads (ring) + 2 (P).
-            if constexpr (WDMA) {
-                if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
-                else step_barrier<kXLoads + kWLoads>();
-            } else {
-                step_barrier<2 * kXLoads + 4>();
-            }
+            // the next step reads loads issued one and two steps ago; only
+            // this step's may still run (and at the 5th step its headers and P)
+            if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
+            else step_barrier<kXLoads + kWLoads>();
         }
     }
     float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
@@ -1048,37 +989,34 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
 
 // Q4_K tiles: (waves along tokens, along rows, tiles per wave along each)
 struct Q4kPlan {
-    int cfg;  // 0: 128 tokens x 256 rows (8 waves, one work-group per CU); 3: 64 x 64 (4 waves)
+    int cfg;  // 0: 128 tokens x 256 rows, 4: 64 x 256 (8 waves, one work-group per CU)
     int32_t splits, kchunk;
 };
 
-// Past 64 tokens, 128 x 256 tiles with K split into ranges of whole
-// super-blocks until about 256 work-groups run (one per CU).  Measured full
-// calls (quantisation, product, reduce) against the tile choice before it
-// (128 x 256 only from 192 tiles, else 128 x 128 from 192 tiles, else 64 x 64
-// with K split to about 512 work-groups): Q4_K 4096 x 4096 at B = 128 / 256 /
-// 512 / 1024: 38 / 48 / 68 / 115 against 41 / 66 / 108 / 140 us; 4096 -> 14336
-// at B = 128 / 256 / 384: 65 / 103 / 157 against 108 / 130 / 235 us; 12288 ->
-// 4096 at B = 256 / 512: 93 / 158 against 170 / 305 us; B = 2048 unchanged (no
-// split).  Up to 64 tokens, 64 x 64 tiles with K split until about 512
-// work-groups run (B = 64: 30 us on 4096 x 4096, against 35 us for the
-// 128 x 256 tiles).
+// Tiles of 256 rows with K split into ranges of whole super-blocks until
+// about 256 work-groups run (one per CU): 64 tokens up to B = 128, 128 tokens
+// above.  Measured full calls (quantisation, product, reduce) against the
+// plans before them (128 x 256 only from 192 tiles, else 128 x 128 from 192
+// tiles, else 64 x 64 with K split to about 512 work-groups): Q4_K 4096 x 4096
+// at B = 256 / 512 / 1024: 48 / 68 / 115 against 66 / 108 / 140 us; 4096 ->
+// 14336 at B = 256 / 384: 103 / 157 against 130 / 235 us; 12288 -> 4096 at
+// B = 256 / 512: 93 / 158 against 170 / 305 us; B = 2048 unchanged (no split).
+// The 64-token tiles against 64 x 64 tiles with K split (B <= 64) or 128 x 256
+// (B = 100, 128): 4096 -> 14336 at B = 64: 46 against 54 us; 12288 -> 4096 at
+// B = 64: 49 against 58; 4096 x 4096 at B = 32 / 64 / 100 / 128: 23.6 / 28.9 /
+// 32.9 / 34.3 against 25.7 / 29.1 / 36.6 / 37.8 us.
 Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
-    auto tiles = [&](int bm, int bn) {
-        return static_cast<int64_t>((n + bn - 1) / bn) * ((b + bm - 1) / bm);
-    };
-    const bool big = b > 64;
-    const int64_t t = big ? tiles(128, 256) : tiles(64, 64);
-    const int64_t want = big ? 256 : 512;
-    int32_t splits = static_cast<int32_t>(big ? want / t : (want + t - 1) / t);
+    const int bm = b > 128 ? 128 : 64;
+    const int64_t t = static_cast<int64_t>((n + 255) / 256) * ((b + bm - 1) / bm);
+    int32_t splits = static_cast<int32_t>(256 / t);
     if (splits > k / 256) splits = k / 256;
     if (splits < 1) splits = 1;
     const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
-    return {big ? 0 : 3, (k + kchunk - 1) / kchunk, kchunk};
+    return {b > 128 ? 0 : 4, (k + kchunk - 1) / kchunk, kchunk};
 }
 
-// rows per x-tile of each Q4_K configuration
-int32_t q4k_tile_rows(int cfg) { return cfg == 0 ? 256 : 64; }
+// rows per x-tile of both Q4_K configurations
+constexpr int32_t kQ4kTileRows = 256;
 
 template <int WM, int WN, int MW, int NW>
 hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
@@ -1095,7 +1033,7 @@ hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq
 // with split K the reduce of the partials into each y
 hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
                            int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
-    const int32_t bn = q4k_tile_rows(p.cfg);
+    const int32_t bn = kQ4kTileRows;
     int32_t t = 0, rows = 0;
     RedMats r{};
     for (int32_t i = 0; i < m.count; ++i) {
@@ -1109,7 +1047,7 @@ hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, c
     m.ntot = rows;
     r.count = m.count;
     const hipError_t e = p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
-                                    : launch_q4k_t<1, 1, 2, 2>(m, xhl, pq, rscale, b, k, p, part, stream);
+                                    : launch_q4k_t<1, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     return launch_reduce(part, p.splits, r, stream);
 }
@@ -1206,7 +1144,7 @@ bool multi_fused(int32_t type, int32_t count, const int32_t* ns, int32_t b, int3
     for (int32_t i = 0; i < count; ++i) total += ns[i];
     if (total > INT32_MAX) return false;
     p = q4k_plan(b, k, static_cast<int32_t>(total));
-    const int32_t bn = q4k_tile_rows(p.cfg);
+    const int32_t bn = kQ4kTileRows;
     for (int32_t i = 0; i < count; ++i)
         if (ns[i] % bn != 0) return false;
     return true;

@@ -212,9 +212,10 @@ MATBATCH_CASES = [
     (Q4_K, 256, 8192, 500), (Q6_K, 256, 16384, 128), (Q4_K, 256, 16384, 512), (Q6_K, 512, 8192, 520),
     # the 256-token tiles of 8 waves (256 x 128 and 256 x 64), ragged B and N
     (Q6_K, 256, 24576, 260), (Q4_K, 256, 8192, 300), (Q8_0, 512, 6000, 257),
-    # the 8-wave tiles with K split (Q4_K 128 x 256 from 65 tokens; 256 x 128
-    # from 129 tokens for the other types), ragged B and N
+    # the 8-wave tiles with K split (Q4_K 64 x 256 up to 128 tokens, 128 x 256
+    # above; 256 x 128 from 129 tokens for the other types), ragged B and N
     (Q4_K, 2048, 1000, 100), (Q4_K, 4096, 3000, 65), (Q6_K, 4096, 1000, 300), (Q8_0, 2080, 700, 400),
+    (Q4_K, 4096, 3000, 200), (Q4_K, 2048, 700, 33),
     # 128 x 128 tiles of 4 waves with K split (65 to 128 tokens, types other than Q4_K)
     (Q8_0, 1024, 640, 128), (Q6_K, 14336, 512, 77),
 ]
@@ -258,10 +259,10 @@ def test_matbatch_prefill_shapes(lib, oracle, t, k, n, b):
 
 # Q/K/V- and gate/up-like groups through gncx_hip_matbatch_multi: the batch is
 # quantised once, and the matrices share one launch (and, with split K, one
-# reduce) when each is whole tiles of the plan for their summed rows (B = 64:
-# 64-row tiles, K in 6 ranges; B = 300 and 512: 256-row tiles, K in 4 and 2
-# ranges; B = 2048: 256-row tiles, no split); otherwise one call per matrix
-# (1000 rows: not whole tiles).
+# reduce) when each is whole 256-row tiles of the plan for their summed rows
+# (B = 64 and 100: 64-token tiles, K in 8 ranges; B = 300 and 512:
+# 128-token tiles, K in 4 and 2 ranges; B = 2048: no split); otherwise one
+# call per matrix (1000 rows: not whole tiles).
 MULTI_CASES = [((4096, 1024, 1024), 4096, b) for b in (64, 512, 2048)] + [
     ((1536, 1536), 1024, 300), ((4096, 1000), 2048, 2048), ((256, 512, 256, 1024), 2048, 100)]
 
