@@ -46,7 +46,10 @@ CASES = [(32, 8, 128, 512, 0), (32, 8, 128, 4096, 0), (32, 8, 128, 32768, 0), (3
          # query-head groups of 16..32 (matrix-core kernel): one token, ragged
          # sliding window, 16 heads padded to 32, two KV heads, partial sub-chunk
          (32, 1, 128, 1, 0), (32, 1, 128, 100, 50), (16, 1, 128, 333, 0), (64, 2, 128, 2000, 0),
-         (32, 2, 128, 129, 0)]
+         (32, 2, 128, 129, 0),
+         # windows past 32-token chunks at 1024 work-groups: longer chunks,
+         # ragged (the last chunk partial), 4 KV heads, a sliding window
+         (32, 8, 128, 8193, 0), (32, 4, 128, 20000, 0), (32, 8, 128, 20000, 6000)]
 
 
 @pytest.mark.parametrize("H,KV,hd,ctx,sw", CASES)
