@@ -304,6 +304,14 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
     static_assert(mfma_lds_bytes<WM, WN, MW>() <= 160 * 1024, "LDS of one CU");
     __shared__ __align__(16) _Float16 xs[2][2][BM * kMfLd];  // [buffer][hi, lo]
     __shared__ __align__(16) _Float16 ws[2][2][BN * kMfLd];
+    // The tile's token scales sit in the padding of the activation rows of
+    // buffer 1 (halves kMfKs .. kMfLd of row r, which no load, store or
+    // product touches), so they cost no LDS: 64x64 tiles fill the CU's LDS
+    // with four work-groups at exactly 40 KB each.  Read from memory at the
+    // output, they were a dependent load of every wave at the moment all
+    // work-groups store.
+    static_assert(kMfLd - kMfKs >= 2 && BM <= THREADS, "a float of padding per row, one scale per thread");
+    auto rs_at = [&](int r) -> float& { return *reinterpret_cast<float*>(&xs[1][0][r * kMfLd + kMfKs]); };
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int32_t t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -425,10 +433,13 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
     // writing step s + 1 to LDS does not cover step s + 2's weights.  Steps go
     // in pairs so that register-set and buffer indices are compile-time
     // constants; loads past the range read nothing.
+    // the scale load goes first: the wait for step 0's loads covers it
+    const float rsv = tid < rows_here ? rscale[t0 + tid] : 1.0f;
     gload_x(kb);
     gload_w(0, kb);
     gload_w(1, kb + kMfKs);
     lstore(0, 0, kb);
+    if (tid < BM) rs_at(tid) = rsv;
     __syncthreads();
     for (int32_t s = 0; s < nsteps; s += 2) {
         const int32_t k0 = kb + s * kMfKs;
@@ -453,7 +464,7 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rscale[t];
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rs_at(t - t0);
             }
         }
 }
@@ -569,6 +580,11 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     __shared__ __align__(16) _Float16 sp[2][2][BM * 8];          // [super-block parity][hi, lo] P of 8 blocks
     __shared__ __align__(16) _Float16 smn[2][BN * 8];            // [super-block parity] mins of 8 blocks
     __shared__ __align__(8) float sdm[2][BN][2];                 // [super-block parity] d, dmin
+    // the tile's token scales, loaded with the first loads: read from memory
+    // at the output they were one dependent load of every wave at the moment
+    // all work-groups store (2.5 us at B = 64, 5 us at B = 512); one dword per
+    // lane of every wave, entries from BM on unused
+    __shared__ __align__(16) float srs[THREADS];
     // The raw weights stream through LDS as well, by direct-to-LDS loads
     // with no registers in flight (register loads of them put memory waits on
     // every step): a ring of 4 stages of each row's 32 qs bytes of a step's
@@ -800,6 +816,13 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     // activations and raw weights into ring stages 0-2; step 0's weights are
     // dequantised once the first three groups of loads are in LDS for every
     // wave.
+    {
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(rscale + t0), static_cast<short>(0), rows_here * static_cast<int32_t>(sizeof(float)),
+            0x00020000);
+        const int32_t off = tid < rows_here ? tid * static_cast<int32_t>(sizeof(float)) : kMfOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (lds_ptr)&srs[64 * wv], 4, off, 0, 0, 0);
+    }
     dma_hp(0, kb);
     dma_x(0, kb);
     dma_w(0, kb);
@@ -862,7 +885,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rscale[t];
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * srs[t - t0];
             }
         }
 }
