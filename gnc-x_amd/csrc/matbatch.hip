@@ -85,6 +85,12 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lb)) << 16);
 }
 
+// act_hilo_kernel<U> holds U float4 of x per thread in registers from the
+// max pass to the quantising pass (rows up to 4 kThreads U values): the
+// loads of a row are issued together, and a longer row reads its tail again.
+// U = 4 covers 4096-wide rows at 40-odd registers; wider rows take U = 16
+// (130-odd registers, 3 waves per SIMD).
+
 // The reference's per-32 quantisation of row blockIdx.x of x (cpp:955-995),
 // each quantised value a = q * d (one fp32 rounding) scaled by 1 / s, where
 // s is the power of two above the row's largest |x| (stored in rscale; the
@@ -98,17 +104,24 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // quantised activations, P = (sum q) * d / s, as an fp16 pair: per token row
 // and 256-value super-block, 8 hi then 8 lo values (the Q4_K kernel's min
 // term, cpp:1177-1178).
+template <int kHiloU>
 __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
                                                             uint2* __restrict xhl, float* __restrict rscale,
                                                             _Float16* __restrict pq) {
     __shared__ float red[kThreads / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
-    float m = 0.0f;
-    for (int32_t t = threadIdx.x; t < tasks; t += kThreads) {
-        const float4 v = xr[t];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    auto amax4 = [](const float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+    float4 xv[kHiloU];
+#pragma unroll
+    for (int u = 0; u < kHiloU; ++u) {
+        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * kThreads;
+        xv[u] = t < tasks ? xr[t] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    float m = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kHiloU; ++u) m = fmaxf(m, amax4(xv[u]));
+    for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) m = fmaxf(m, amax4(xr[t]));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
@@ -120,11 +133,10 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
     const float inv = 1.0f / sc;                                       // exact
     if (threadIdx.x == 0) rscale[row] = sc;
     uint2* out = xhl + static_cast<size_t>(row) * tasks * 2;
-    // whole 8-lane groups take the same trip count (tasks and kThreads are multiples of 8)
-    for (int32_t t = threadIdx.x; t < tasks; t += kThreads) {
+    auto emit = [&](const float4 v, int32_t t) {
         int q0, q1, q2, q3;
         float d;
-        quantize_values(xr[t], q0, q1, q2, q3, d);
+        quantize_values(v, q0, q1, q2, q3, d);
         uint2 hi, lo;
         split2((static_cast<float>(q0) * d) * inv, (static_cast<float>(q1) * d) * inv, hi.x, lo.x);
         split2((static_cast<float>(q2) * d) * inv, (static_cast<float>(q3) * d) * inv, hi.y, lo.y);
@@ -146,7 +158,25 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
                 pr[8] = pl;
             }
         }
+    };
+    // whole 8-lane groups take the same branches and trip counts (tasks and
+    // kThreads are multiples of 8), as the group operations need
+#pragma unroll
+    for (int u = 0; u < kHiloU; ++u) {
+        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * kThreads;
+        if (t < tasks) emit(xv[u], t);
     }
+    for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) emit(xr[t], t);
+}
+
+void launch_act_hilo(const float* x, int32_t b, int32_t k, _Float16* xhl, float* rscale, _Float16* pq,
+                     hipStream_t stream) {
+    if (k <= 4 * 4 * kThreads)
+        hipLaunchKernelGGL((act_hilo_kernel<4>), dim3(b), dim3(kThreads), 0, stream, x, k,
+                           reinterpret_cast<uint2*>(xhl), rscale, pq);
+    else
+        hipLaunchKernelGGL((act_hilo_kernel<16>), dim3(b), dim3(kThreads), 0, stream, x, k,
+                           reinterpret_cast<uint2*>(xhl), rscale, pq);
 }
 
 // Weights e0 .. e0 + 15 (e0 a multiple of 16) of one row: raw block bytes
@@ -992,8 +1022,7 @@ hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xhl, const float* rsc
 template <int TYPE>
 hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                        float* rscale, float* part, hipStream_t stream) {
-    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
-                       rscale, static_cast<_Float16*>(nullptr));
+    launch_act_hilo(x, b, k, xhl, rscale, nullptr, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
@@ -1077,8 +1106,7 @@ hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, c
 
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                       _Float16* pq, float* rscale, float* part, hipStream_t stream) {
-    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
-                       rscale, pq);
+    launch_act_hilo(x, b, k, xhl, rscale, pq, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
@@ -1214,8 +1242,7 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
     float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
     float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(act_hilo_kernel, dim3(b), dim3(kThreads), 0, stream, x, k, reinterpret_cast<uint2*>(xhl),
-                       rscale, pq);
+    launch_act_hilo(x, b, k, xhl, rscale, pq, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
