@@ -921,14 +921,24 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
 }
 
 // y = sum over the split K ranges, added in range order (deterministic);
-// range z's partials are the flat block [z count, (z + 1) count)
+// range z's partials are the flat block [z count, (z + 1) count).  The
+// first kRedU ranges are loaded together before the adds (a loop of
+// load-then-add waited on memory once per range).
+constexpr int kRedU = 16;
+
 __global__ __launch_bounds__(kThreads) void matbatch_reduce_kernel(const float* __restrict part, int32_t splits,
                                                                    RedMats r) {
     const size_t count = r.end[r.count - 1];
     for (size_t i = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; i < count;
          i += static_cast<size_t>(gridDim.x) * kThreads) {
-        float acc = part[i];
-        for (int32_t z = 1; z < splits; ++z) acc += part[static_cast<size_t>(z) * count + i];
+        float v[kRedU];
+#pragma unroll
+        for (int u = 0; u < kRedU; ++u) v[u] = u < splits ? part[static_cast<size_t>(u) * count + i] : 0.0f;
+        float acc = v[0];
+#pragma unroll
+        for (int u = 1; u < kRedU; ++u)
+            if (u < splits) acc += v[u];
+        for (int32_t z = kRedU; z < splits; ++z) acc += part[static_cast<size_t>(z) * count + i];
         float* y = r.y[0];
         size_t first = 0;
 #pragma unroll
