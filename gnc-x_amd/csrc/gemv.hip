@@ -661,10 +661,10 @@ template <int TYPE>
 hipError_t launch_band(const BandMats& m, const float* x, int32_t k, int32_t n, hipStream_t stream, bool& used) {
     const int32_t groups = n < kBandGroups ? n : kBandGroups;
     const size_t per_group = row_bytes(TYPE, k) * static_cast<size_t>(n) / static_cast<size_t>(groups);
-    // Q6_K rows of three or more K-slices also stream best with 8 waves
-    // (14336 x 4096: 13.5 vs 14.3 us; 12288 x 4096: 11.9 vs 12.8 us)
-    const bool q6_long = TYPE == kQ6_K && (Slot<TYPE>::slots(k) + 63) / 64 >= 3;
-    used = ((per_group > kBandStreamBytes || q6_long) && try_band<TYPE, kBandThreadsStream>(m, x, k, n, stream)) ||
+    // Long-K Q6_K (three or more K-slices) also streams best with 16 waves:
+    // 14336 x 4096 12.5-12.7 us against 13.3-13.7 with 8, 12288 x 4096 11.1
+    // against 12.0-12.3 (the same boxes, back-to-back calls on 16 copies)
+    used = (per_group > kBandStreamBytes && try_band<TYPE, kBandThreadsStream>(m, x, k, n, stream)) ||
            try_band<TYPE, kBandThreads>(m, x, k, n, stream);
     return used ? hipGetLastError() : hipSuccess;
 }

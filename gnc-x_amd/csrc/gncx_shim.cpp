@@ -213,9 +213,13 @@ uint64_t host_signature(const uint8_t* p, size_t bytes) {
     return h;
 }
 
+// A deferred matvec or attention prologue may still point at the copy (its
+// weights or gamma): recorded work is issued before the copy is freed, and
+// hipFree waits for the device, so it never reads freed or re-uploaded bytes.
 void forget_weight(uintptr_t key) {
     auto it = g_rt.weights.find(key);
     if (it == g_rt.weights.end()) return;
+    (void)flush_pending("weight copy release");
     (void)hipFree(it->second.d);
     g_rt.weights.erase(it);
 }
@@ -772,12 +776,17 @@ void on_segv(int sig, siginfo_t* si, void* uc);
 // call, makes the buffer's pages current (which may wait on the device, copy
 // and change protections), and wakes the faulting thread, which then retries
 // its access or, for a fault that is not a lazy buffer's, chains to the
-// handler installed before.  So the faulting thread may hold any lock (a
-// libc or HIP-runtime lock included) when it faults: the work that needs
-// locks runs in another thread.  Only a fault taken by the library itself
-// while it holds the call lock is resolved in the handler, as the resolver
-// could never get that lock; the library touches lazy buffers' host pages
-// only through their device copies, so that case is not expected.
+// handler installed before.  So the faulting thread may hold a lock that the
+// resolver never takes (a stdio FILE lock, the caller's own locks) when it
+// faults.  The resolver does call the HIP runtime (event and stream waits,
+// copies), so a lazy buffer handed straight to a HIP API (a copy from it, for
+// instance) can deadlock: such use is not supported.  Only a fault taken by
+// the library itself while it holds the call lock is resolved in the handler,
+// as the resolver could never get that lock, and then without issuing any
+// recorded work; the library touches lazy buffers' host pages only through
+// their device copies, so that case is not expected.  A fork() child inherits
+// the handler but not the resolver thread: its faults go straight to the
+// handler installed before.
 struct FaultRequest {
     uintptr_t addr;
     int write;
@@ -785,9 +794,10 @@ struct FaultRequest {
     int handled;
 };
 int g_fault_pipe[2] = {-1, -1};
+pid_t g_fault_pid = 0;  // the process whose resolver thread reads the pipe
 ssize_t write_fd(int fd, const void* p, size_t n) { return ::write(fd, p, n); }
 
-bool resolve_fault(uintptr_t a, bool write);
+bool resolve_fault(uintptr_t a, bool write, bool may_issue);
 
 void fault_resolver() {
     for (;;) {
@@ -800,7 +810,7 @@ void fault_resolver() {
         bool handled;
         {
             std::lock_guard<CallLock> lk(g_mu);
-            handled = resolve_fault(r->addr, r->write != 0);
+            handled = resolve_fault(r->addr, r->write != 0, true);
         }
         r->handled = handled ? 1 : 0;
         r->done.store(1, std::memory_order_release);
@@ -814,6 +824,7 @@ void ensure_segv_handler() {
             g_fault_pipe[0] = g_fault_pipe[1] = -1;
             return;  // no resolver: lazy_ptr reports the failure
         }
+        g_fault_pid = getpid();
         std::thread(fault_resolver).detach();
     }
     struct sigaction cur;
@@ -827,12 +838,13 @@ void ensure_segv_handler() {
     sigaction(SIGSEGV, &sa, &g_prev_segv);
 }
 
-// A host access to a lazy buffer's protected page (runs in normal thread
-// context, with the call lock held): make the host copy current and
-// read-only, or read-write for a write to a read-only page.  False when the
-// address is not a protected page of a lazy buffer.
-bool resolve_fault(uintptr_t a, bool write) {
-    (void)flush_pending("lazy host buffer access");
+// A host access to a lazy buffer's protected page (with the call lock
+// held): make the host copy current and read-only, or read-write for a write
+// to a read-only page.  False when the address is not a protected page of a
+// lazy buffer.  The address is classified first; recorded work (deferred
+// matvecs, an attention prologue) is issued only for a lazy buffer's page and
+// only when may_issue (the resolver thread, never the signal handler).
+bool resolve_fault(uintptr_t a, bool write, bool may_issue) {
     HostBuffer* b = buffer_at(a);
     if (!b || b->pinned || !b->twin || b->home == Home::kHost) return false;
     const uintptr_t pg = page_bytes();
@@ -840,6 +852,7 @@ bool resolve_fault(uintptr_t a, bool write) {
     const uintptr_t hi = (reinterpret_cast<uintptr_t>(b->ptr) + b->bytes + pg - 1) & ~(pg - 1);
     if (a < lo || a >= hi) return false;
     const char* where = "lazy host buffer access";
+    if (may_issue) (void)flush_pending(where);
     if (b->home == Home::kDevice && b->stage && b->staged == b->writes) {
         // the copy queued when the last writer returned
         if (check(hipEventSynchronize(b->staged_ev), where) && protect(*b, PROT_READ | PROT_WRITE)) {
@@ -877,8 +890,11 @@ void on_segv(int sig, siginfo_t* si, void* uc) {
     // x86-64 page-fault error code: bit 1 set for a write
     const bool write = (static_cast<ucontext_t*>(uc)->uc_mcontext.gregs[REG_ERR] & 2) != 0;
     bool handled = false;
-    if (t_in_call) {
-        handled = resolve_fault(a, write);  // the library itself holds the call lock
+    if (g_fault_pid != 0 && getpid() != g_fault_pid) {
+        // a fork() child: no resolver reads the pipe here, and the parent's
+        // resolver would act on the parent's memory
+    } else if (t_in_call) {
+        handled = resolve_fault(a, write, false);  // the library itself holds the call lock
     } else if (g_fault_pipe[1] >= 0) {
         const int saved_errno = errno;
         FaultRequest req;
@@ -1874,6 +1890,7 @@ GNCX_API void gncx_hip_weight_forget(const void* p) {
         forget_weight(reinterpret_cast<uintptr_t>(p));
         return;
     }
+    (void)flush_pending("weight copy release");
     for (auto& kv : g_rt.weights) (void)hipFree(kv.second.d);
     g_rt.weights.clear();
 }

@@ -283,10 +283,11 @@ void gncx_hip_matvec_multi(int32_t count, const uint8_t* const* weights, const i
 /* out_batches[i][batch][out_dims[i]] = the gncx_xfold_universal_matbatch
  * product of W_i and in_batch [batch][in_dim] for count (1..4) matrices of
  * one ggml_type, e.g. Q/K/V or gate/up of a prefill (lua/gncx_streamer.lua
- * 1068-1071 and 1135-1136 issue them one call each); the batch is quantised once,
- * and Q4_K matrices whose rows are whole tiles of one launch plan share one
- * launch.  Each output is the single call's result to within fp32 summation
- * order (a single call may split K for a small matrix). */
+ * 1068-1071 and 1135-1136 issue them one call each).  Q4_K matrices whose rows
+ * are whole tiles of one launch plan share one launch, and the batch is then
+ * quantised once; otherwise each matrix is a call of its own, which quantises
+ * the batch again.  Each output is the single call's result to within fp32
+ * summation order (a single call may split K for a small matrix). */
 void gncx_hip_matbatch_multi(int32_t count, const uint8_t* const* weights, const int32_t* out_dims,
                              int32_t ggml_type, const float* in_batch, int32_t batch_size, int32_t in_dim,
                              float* const* out_batches);

@@ -594,6 +594,39 @@ static float qk_dot_ref(const float* q, const float* k, int32_t hd) {
 
 /* cpp:1887-1994: write K/V at pos, then per head a two-pass softmax over
  * the window [max(0, pos-sw+1), pos]; kv head = h / (n_heads/n_kv_heads). */
+/* One query head of one position: scores over the window [t0, pos], the
+ * max-shifted exponentials, and V weighted by exp / (sum + 1e-12).  sc holds
+ * at least pos - t0 + 1 floats.  Shared by the single step and the batched
+ * prefill below, so both give the same bits. */
+static void attn_head(const float* qh, const float* k_cache, const float* v_cache, int32_t kvh, int32_t t0,
+                      int32_t t1, int32_t kv_dim, int32_t head_dim, float scale, float* sc, float* oh) {
+    const int32_t win = t1 - t0;
+    float mx = -1e30f;
+    for (int32_t t = t0; t < t1; ++t) {
+        const float* kt = k_cache + (size_t)t * kv_dim + (size_t)kvh * head_dim;
+        const float s = qk_dot_ref(qh, kt, head_dim) * scale;
+        sc[t - t0] = s;
+        if (s > mx) mx = s;
+    }
+    float sum = 0.0f;
+    for (int32_t i = 0; i < win; ++i) {
+        const float e = expf(sc[i] - mx);
+        sc[i] = e;
+        sum += e;
+    }
+    const float inv = 1.0f / (sum + 1e-12f);
+    for (int32_t d = 0; d < head_dim; ++d) oh[d] = 0.0f;
+    for (int32_t t = t0; t < t1; ++t) {
+        const float w = sc[t - t0] * inv;
+        const float* vt = v_cache + (size_t)t * kv_dim + (size_t)kvh * head_dim;
+        for (int32_t d = 0; d < head_dim; ++d) oh[d] += w * vt[d];
+    }
+}
+
+static int32_t attn_window_start(int32_t pos, int32_t sliding_window) {
+    return sliding_window > 0 ? (pos - sliding_window + 1 > 0 ? pos - sliding_window + 1 : 0) : 0;
+}
+
 void orc_attention_step(const float* q, const float* k_new, const float* v_new, float* k_cache,
                         float* v_cache, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
                         int32_t head_dim, float scale, int32_t sliding_window, int32_t write_kv,
@@ -604,36 +637,48 @@ void orc_attention_step(const float* q, const float* k_new, const float* v_new, 
         memcpy(v_cache + (size_t)pos * kv_dim, v_new, sizeof(float) * (size_t)kv_dim);
     }
     const int32_t group = n_heads / n_kv_heads;
-    const int32_t t0 = sliding_window > 0 ? (pos - sliding_window + 1 > 0 ? pos - sliding_window + 1 : 0) : 0;
+    const int32_t t0 = attn_window_start(pos, sliding_window);
     const int32_t t1 = pos + 1;
     const int32_t win = t1 - t0;
     float* sc = (float*)malloc(sizeof(float) * (size_t)(win > 0 ? win : 1));
-    for (int32_t h = 0; h < n_heads; ++h) {
-        const int32_t kvh = h / group;
-        const float* qh = q + (size_t)h * head_dim;
-        float* oh = out + (size_t)h * head_dim;
-        float mx = -1e30f;
-        for (int32_t t = t0; t < t1; ++t) {
-            const float* kt = k_cache + (size_t)t * kv_dim + (size_t)kvh * head_dim;
-            const float s = qk_dot_ref(qh, kt, head_dim) * scale;
-            sc[t - t0] = s;
-            if (s > mx) mx = s;
-        }
-        float sum = 0.0f;
-        for (int32_t i = 0; i < win; ++i) {
-            const float e = expf(sc[i] - mx);
-            sc[i] = e;
-            sum += e;
-        }
-        const float inv = 1.0f / (sum + 1e-12f);
-        for (int32_t d = 0; d < head_dim; ++d) oh[d] = 0.0f;
-        for (int32_t t = t0; t < t1; ++t) {
-            const float w = sc[t - t0] * inv;
-            const float* vt = v_cache + (size_t)t * kv_dim + (size_t)kvh * head_dim;
-            for (int32_t d = 0; d < head_dim; ++d) oh[d] += w * vt[d];
-        }
+    for (int32_t h = 0; h < n_heads; ++h)
+        attn_head(q + (size_t)h * head_dim, k_cache, v_cache, h / group, t0, t1, kv_dim, head_dim, scale, sc,
+                  out + (size_t)h * head_dim);
+    free(sc);
+}
+
+/* The streamer's prefill attention loop (lua/gncx_streamer.lua:1079-1109):
+ * token i of the batch attends at position pos0 + i over K/V rows that are
+ * already in the caches (rows pos0 .. pos0 + b - 1 written by the caller).
+ * Each (token, head) is attn_head, as in b consecutive orc_attention_step
+ * calls with write_kv; the (token, head) pairs run in parallel. */
+typedef struct {
+    const float *q, *k_cache, *v_cache;
+    float* out;
+    int32_t pos0, n_heads, group, kv_dim, head_dim, window;
+    float scale;
+} attn_pf_ctx;
+
+static void attn_pf_rows(void* p, int32_t m0, int32_t m1) {
+    const attn_pf_ctx* c = (const attn_pf_ctx*)p;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(c->pos0 + m1 / c->n_heads + 1));
+    for (int32_t m = m0; m < m1; ++m) {
+        const int32_t i = m / c->n_heads, h = m % c->n_heads;
+        const int32_t pos = c->pos0 + i;
+        const size_t row = (size_t)i * c->n_heads * c->head_dim + (size_t)h * c->head_dim;
+        attn_head(c->q + row, c->k_cache, c->v_cache, h / c->group, attn_window_start(pos, c->window), pos + 1,
+                  c->kv_dim, c->head_dim, c->scale, sc, c->out + row);
     }
     free(sc);
+}
+
+void orc_attention_prefill(const float* q, const float* k_cache, const float* v_cache, int32_t pos0, int32_t b,
+                           int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                           int32_t sliding_window, float* out) {
+    if (b <= 0) return;
+    attn_pf_ctx c = {q, k_cache, v_cache, out, pos0, n_heads, n_heads / n_kv_heads, n_kv_heads * head_dim,
+                     head_dim, sliding_window, scale};
+    orc_parallel_rows(b * n_heads, 8, attn_pf_rows, &c);
 }
 
 /* cpp:2038-2052 */

@@ -69,6 +69,11 @@ void     orc_attention_step(const float* q, const float* k_new, const float* v_n
                             float* v_cache, int32_t pos, int32_t n_heads, int32_t n_kv_heads,
                             int32_t head_dim, float scale, int32_t sliding_window,
                             int32_t write_kv, float* out);
+/* b consecutive attention steps at pos0 .. pos0 + b - 1 over caches that
+ * already hold those rows; q and out are [b][n_heads * head_dim]. */
+void     orc_attention_prefill(const float* q, const float* k_cache, const float* v_cache, int32_t pos0,
+                               int32_t b, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float scale,
+                               int32_t sliding_window, float* out);
 void     orc_swiglu(const float* gate, const float* up, int32_t n, float* out);
 void     orc_geglu(const float* gate, const float* up, int32_t n, float* out);
 float    orc_encode_4phase(const float* v, int32_t dim, int32_t layer_k, uint32_t* tokens);

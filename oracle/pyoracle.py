@@ -57,6 +57,7 @@ class Oracle:
             "orc_rope_table": (None, [_i32, _i32, _f32, _vp, _vp, _vp]),
             "orc_rope": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32]),
             "orc_attention_step": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _vp]),
+            "orc_attention_prefill": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp]),
             "orc_swiglu": (None, [_vp, _vp, _i32, _vp]),
             "orc_geglu": (None, [_vp, _vp, _i32, _vp]),
             "orc_encode_4phase": (_f32, [_vp, _i32, _i32, _vp]),
@@ -147,6 +148,18 @@ class Oracle:
         self.lib.orc_attention_step(_ptr(np.ascontiguousarray(q, dtype=np.float32)), _ptr(kn), _ptr(vn), _ptr(kc),
                                     _ptr(vc), pos, n_heads, n_kv, head_dim, scale, window, write_kv, _ptr(out))
         return out, kc, vc
+
+    def attention_prefill(self, q, k_cache, v_cache, pos0, b, n_heads, n_kv, head_dim, scale, window):
+        """out[b][n_heads*head_dim]: b consecutive attention steps at positions
+        pos0 .. pos0+b-1 over caches that already hold those K/V rows."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        kc = np.ascontiguousarray(k_cache, dtype=np.float32)
+        vc = np.ascontiguousarray(v_cache, dtype=np.float32)
+        assert q.size == b * n_heads * head_dim and kc.shape[0] >= pos0 + b and vc.shape[0] >= pos0 + b
+        out = np.zeros((b, n_heads * head_dim), dtype=np.float32)
+        self.lib.orc_attention_prefill(_ptr(q), _ptr(kc), _ptr(vc), pos0, b, n_heads, n_kv, head_dim, scale, window,
+                                       _ptr(out))
+        return out
 
     def swiglu(self, g, u):
         g = np.ascontiguousarray(g, dtype=np.float32)

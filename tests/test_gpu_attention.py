@@ -41,7 +41,8 @@ def test_attention_reference_vectors(lib, golden, tag):
 
 # config 4: 32 Q / 8 KV heads x 128, ctx 512 / 4096 / 32768, SWA 1024, MQA
 CASES = [(32, 8, 128, 512, 0), (32, 8, 128, 4096, 0), (32, 8, 128, 32768, 0), (32, 8, 128, 4096, 1024),
-         (32, 8, 128, 32768, 1024), (32, 1, 128, 4096, 0), (32, 1, 128, 32768, 0), (16, 16, 64, 300, 0),
+         (32, 8, 128, 32768, 1024), (32, 1, 128, 512, 0), (32, 1, 128, 4096, 0), (32, 1, 128, 32768, 0),
+         (16, 16, 64, 300, 0),
          (8, 2, 256, 700, 100), (4, 4, 128, 1, 0),
          # query-head groups of 16..32 (matrix-core kernel): one token, ragged
          # sliding window, 16 heads padded to 32, two KV heads, partial sub-chunk

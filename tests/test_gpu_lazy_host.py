@@ -138,6 +138,33 @@ def test_lazy_deferred_matvecs_issue_before_every_consumer(lib, oracle, lazy):
     assert rel_l2(z, oracle.matvec(Q4_K, wc, y2, 256, 64)) < 1e-3
 
 
+def test_lazy_weight_rewritten_between_gathered_matvecs(lib, oracle, lazy):
+    """A host weight array rewritten in place between two matvecs of one
+    gathered group: the second call finds the cached device copy stale and
+    replaces it, and the first (still recorded) matvec must have read the old
+    weights, not freed memory or the new upload at the same address."""
+    k, n = 512, 192
+    w = synth.make_weights(Q4_K, n, k, seed=121)
+    w_old = w.copy()
+    w_new = synth.make_weights(Q4_K, n, k, seed=122)
+    _, x = lazy(k, 1)
+    _, xn = lazy(k, 2)
+    _, y1 = lazy(n, 3)
+    _, y2 = lazy(n, 4)
+    x[:] = synth.make_activations(1, k, seed=123)
+    lib.gncx_hip_vec_add(xn.ctypes.data, x.ctypes.data, k)  # a device-held input
+    for rnd in range(2):
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, xn.ctypes.data, None, k, n, y1.ctypes.data, None)
+        w[:] = w_new if rnd == 0 else w_old  # same address, other contents
+        lib.gncx_xfold_universal_matvec(ptr(w), 0, Q4_K, xn.ctypes.data, None, k, n, y2.ctypes.data, None)
+        gncx.check(lib)
+        xs = xn.copy()
+        first, second = (w_old, w_new) if rnd == 0 else (w_new, w_old)
+        assert rel_l2(y1, oracle.matvec(Q4_K, first, xs, k, n)) < 1e-3, rnd
+        assert rel_l2(y2, oracle.matvec(Q4_K, second, xs, k, n)) < 1e-3, rnd
+    lib.gncx_hip_weight_forget(ptr(w))
+
+
 @pytest.mark.parametrize("interrupt", [False, True])
 def test_lazy_deferred_attention_prologue(lib, lazy, interrupt):
     """heads-RMSNorm of q and of k, RoPE of both and the attention step on

@@ -14,7 +14,10 @@ and attention calls) and the library's fused extensions (batched norms, one
 causal attention pass) run over the same model and are held to the same bar.
 All 36 layers run with a short prompt; a 300-token prompt, which takes the
 256-token matbatch tiles and several causal attention blocks, runs 4 layers
-at the full widths.
+at the full widths; and the decode workload's own 2048-token prompt (the
+B = 2048 matbatch plans, causal attention over 2048 positions, then decode
+steps at positions 2048-2050 whose attention spans the whole prefilled cache)
+runs 4 layers at the full widths against the oracle's batched prefill.
 """
 from __future__ import annotations
 
@@ -28,13 +31,16 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _teacher_forced(lib, torch, oracle, model, prompt, n_decode, max_seq):
+def _teacher_forced(lib, torch, oracle, model, prompt, n_decode, max_seq, batched_oracle=False):
     import gncx_amd.decode as dec
 
     ref = OracleModel(oracle, model, max_seq=max_seq)
-    for pos, tok in enumerate(prompt[:-1]):
-        ref.step(tok, pos, logits=False)
-    want = [ref.step(prompt[-1], len(prompt) - 1)]
+    if batched_oracle:
+        want = [ref.prefill(prompt, progress=lambda m: print(m, flush=True))]
+    else:
+        for pos, tok in enumerate(prompt[:-1]):
+            ref.step(tok, pos, logits=False)
+        want = [ref.step(prompt[-1], len(prompt) - 1)]
     toks = []
     for i in range(n_decode):
         toks.append(int(np.argmax(want[-1])))
@@ -82,6 +88,29 @@ def test_qwen3_8b_widths_300_token_prompt(lib, oracle, torch_mod):
         rng = np.random.default_rng(12)
         prompt = [int(t) for t in rng.integers(0, shape.vocab, 300)]
         _teacher_forced(lib, torch, oracle, model, prompt, n_decode=2, max_seq=320)
+    finally:
+        lib.gncx_hip_weight_forget(None)
+        del model
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_8b_widths_2048_token_prompt(lib, oracle, torch_mod):
+    """The decode workload's prompt length at the full widths (4 layers): the
+    library's prefill through the streamer's call sequence and through the
+    fused extensions (B = 2048 multi-matrix matbatch, one causal attention
+    pass over 2048 positions), then 3 decode steps at positions 2048-2050,
+    against the oracle's prefill (matbatch projections and the streamer's
+    attention loop, lua/gncx_streamer.lua:968-1208) and its decode steps."""
+    import gncx_amd.decode as dec
+
+    torch = torch_mod
+    shape = dec.Qwen3Shape(n_layers=4)
+    model = dec.build_model(torch, shape, seed=2048)
+    try:
+        rng = np.random.default_rng(13)
+        prompt = [int(t) for t in rng.integers(0, shape.vocab, 2048)]
+        _teacher_forced(lib, torch, oracle, model, prompt, n_decode=3, max_seq=2048 + 4, batched_oracle=True)
     finally:
         lib.gncx_hip_weight_forget(None)
         del model

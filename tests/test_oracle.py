@@ -336,6 +336,47 @@ def test_attention_window_is_a_shorter_cache(oracle):
     assert np.array_equal(o1, o2)
 
 
+@pytest.mark.parametrize("H,KV,W,pos0", [(8, 2, 0, 0), (8, 2, 7, 0), (8, 1, 0, 5), (4, 4, 16, 3)])
+def test_attention_prefill_is_consecutive_steps(oracle, H, KV, W, pos0):
+    """The batched causal pass (the streamer's prefill loop, lua/gncx_streamer.lua
+    1079-1109) equals b consecutive single steps that each write their K/V row,
+    bit for bit: GQA, a sliding window shorter than the batch, MQA after a
+    cached prefix, and one KV head per query head."""
+    rng = np.random.default_rng(31 + H + KV + W)
+    hd, b = 64, 37
+    rows = pos0 + b
+    kc = np.zeros((rows, KV * hd), np.float32)
+    vc = np.zeros((rows, KV * hd), np.float32)
+    kc[:pos0] = rng.standard_normal((pos0, KV * hd), dtype=np.float32)
+    vc[:pos0] = rng.standard_normal((pos0, KV * hd), dtype=np.float32)
+    q = rng.standard_normal((b, H * hd), dtype=np.float32)
+    kn = rng.standard_normal((b, KV * hd), dtype=np.float32)
+    vn = rng.standard_normal((b, KV * hd), dtype=np.float32)
+    sc = 1 / np.sqrt(hd)
+    want = np.zeros((b, H * hd), np.float32)
+    kcs, vcs = kc.copy(), vc.copy()
+    for i in range(b):
+        want[i], kcs, vcs = oracle.attention(q[i], kn[i], vn[i], kcs, vcs, pos0 + i, H, KV, hd, sc, W, 1)
+    got = oracle.attention_prefill(q, kcs, vcs, pos0, b, H, KV, hd, sc, W)
+    assert np.array_equal(got, want)
+
+
+def test_attention_prefill_matches_reference_steps(oracle, ref):
+    """Against the reference's own step, called once per position."""
+    rng = np.random.default_rng(44)
+    H, KV, hd, b = 8, 2, 128, 40
+    kc = np.zeros((b, KV * hd), np.float32)
+    vc = np.zeros((b, KV * hd), np.float32)
+    q = rng.standard_normal((b, H * hd), dtype=np.float32)
+    kn = rng.standard_normal((b, KV * hd), dtype=np.float32)
+    vn = rng.standard_normal((b, KV * hd), dtype=np.float32)
+    want = np.zeros((b, H * hd), np.float32)
+    for i in range(b):
+        want[i], kc, vc = ref.attention(q[i], kn[i], vn[i], kc, vc, i, H, KV, hd, 1 / np.sqrt(hd), 0, 1)
+    got = oracle.attention_prefill(q, kc, vc, 0, b, H, KV, hd, 1 / np.sqrt(hd), 0)
+    assert rel_l2(got, want) < 1e-6
+
+
 @pytest.mark.parametrize("tag", ["gqa", "swa", "mqa"])
 def test_attention_matches_reference(oracle, golden, tag):
     g = golden
@@ -401,3 +442,30 @@ def test_oracle_against_live_reference(oracle, ref):
         w = synth.make_weights(t, n, k, seed=900 + t)
         x = synth.make_activations(1, k, seed=901 + t)
         assert rel_l2(oracle.matvec(t, w, x, k, n), ref.matvec(t, w, x, k, n)) < 1e-6
+
+
+def test_oracle_model_prefill_equals_token_steps(oracle):
+    """The oracle's batched prefill (matbatch projections, the batched causal
+    attention pass) against the same model stepped token by token (matvec
+    projections, one attention step each): logits after the prompt and after
+    a decode step that reads the prefilled caches agree to matbatch-versus-
+    matvec summation order."""
+    import torch
+
+    import gncx_amd.decode as dec
+    from oracle_model import OracleModel
+
+    shape = dec.Qwen3Shape(n_layers=2, embed=256, n_heads=4, n_kv=2, head_dim=64, ffn=512, vocab=600)
+    model = dec.build_model(torch, shape, seed=17, device="cpu")
+    prompt = [5, 17, 599, 0, 311, 42, 7, 128, 64, 1]
+    a, b = OracleModel(oracle, model, max_seq=16), OracleModel(oracle, model, max_seq=16)
+    for pos, tok in enumerate(prompt[:-1]):
+        a.step(tok, pos, logits=False)
+    want = a.step(prompt[-1], len(prompt) - 1)
+    got = b.prefill(prompt)
+    assert rel_l2(got, want) < 1e-5
+    for l in range(shape.n_layers):  # every layer's K/V rows, the last layer's included
+        assert rel_l2(b.kc[l][:len(prompt)], a.kc[l][:len(prompt)]) < 1e-5
+        assert rel_l2(b.vc[l][:len(prompt)], a.vc[l][:len(prompt)]) < 1e-5
+    tok = int(np.argmax(want))
+    assert rel_l2(b.step(tok, len(prompt)), a.step(tok, len(prompt))) < 1e-5
