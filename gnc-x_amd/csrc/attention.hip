@@ -93,12 +93,18 @@ struct ProRegs {
     static constexpr int NE = HD / 64 > 0 ? HD / 64 : 1;  // elements per lane
     static constexpr int NR = (HD / 2 + 63) / 64;         // rotated pairs per lane
     float gq[NE], gk[NE], c[NR], s[NR];
+    // unconditional loads (a missing weight reads q, whose first HD values
+    // exist, and is never used: prologue_head_r takes has_gamma): with no load
+    // behind a branch the compiler counts them exactly and waits for these
+    // alone, not for the K/V rows issued after them
     __device__ __forceinline__ void load(const AttnParams& p, int lane) {
+        const float* gqp = p.q_gamma ? p.q_gamma : p.q;
+        const float* gkp = p.k_gamma ? p.k_gamma : p.q;
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             const int i = lane + 64 * e < HD ? lane + 64 * e : 0;
-            gq[e] = p.q_gamma ? p.q_gamma[i] : 1.0f;
-            gk[e] = p.k_gamma ? p.k_gamma[i] : 1.0f;
+            gq[e] = gqp[i];
+            gk[e] = gkp[i];
         }
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
@@ -166,43 +172,48 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     const bool have_new = p.use_new != 0;
 
     // q rows of this KV head's query heads, k_new and the prologue operands
-    // first: the prologue then runs while the K/V rows are still in flight
+    // first: the prologue then runs while the K/V rows are still in flight.
+    // Every early load is unconditional (indices clamped, pointers selected,
+    // unused values replaced afterwards), so the compiler counts them exactly
+    // and the prologue waits for these loads alone: a load behind a branch made
+    // it wait for every load issued so far, the K/V rows included.
     constexpr int kQRegs = 8;  // q values per thread held across the K/V issue
+    const int gq_n = G * HD;
     const float* qg = p.q + static_cast<size_t>(hk) * G * HD;
     float qreg[kQRegs];
 #pragma unroll
     for (int u = 0; u < kQRegs; ++u) {
         const int i = tid + u * kThreads;
-        qreg[u] = i < G * HD ? qg[i] : 0.0f;
+        qreg[u] = qg[i < gq_n ? i : gq_n - 1];
     }
-    const float kreg = (have_new && tid < HD) ? p.k_new[static_cast<size_t>(hk) * HD + tid] : 0.0f;
+    // without a new row, q (at least n_kv HD values) stands in for k_new
+    const float* knp = have_new ? p.k_new : p.q;
+    const float kreg = knp[static_cast<size_t>(hk) * HD + (tid < HD ? tid : 0)];  // used where have_new && tid < HD
     const bool pro = p.norm_qk || p.has_rope;
     ProRegs<HD> pr;
     if (pro) pr.load(p, lane);
 
     // SHORT: this thread's token is ta + ts; its K / V slices are loaded now
-    // (the new token's K comes from LDS after the prologue, its V from v_new)
-    float4 kpre[4], vpre[4];
+    // (the new token's K comes from LDS after the prologue, its V from v_new);
+    // a slot past the chunk reads row ta, and neither its score nor its V row
+    // is used
+    // (native vectors: float4 copies are memcpys, and a V slice copied that
+    // way went through scratch memory on its way to LDS)
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    float4 kpre[4];
+    f32x4 vpre[4];
     const int tok0 = ta + ts;
     const bool valid0 = tok0 < tb;
     const bool new0 = have_new && tok0 == p.pos;
     if constexpr (SHORT) {
+        const int tokc = valid0 ? tok0 : ta;
+        const float* ksrc = p.k_cache + static_cast<size_t>(tokc) * kv_dim + static_cast<size_t>(hk) * HD;
+        const float* vsrc = new0 ? p.v_new + static_cast<size_t>(hk) * HD
+                                 : p.v_cache + static_cast<size_t>(tokc) * kv_dim + static_cast<size_t>(hk) * HD;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            kpre[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-            vpre[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        if (valid0) {
-            const float* vsrc = new0 ? p.v_new + static_cast<size_t>(hk) * HD
-                                     : p.v_cache + static_cast<size_t>(tok0) * kv_dim + static_cast<size_t>(hk) * HD;
-            if (!new0) {
-                const float* ksrc = p.k_cache + static_cast<size_t>(tok0) * kv_dim + static_cast<size_t>(hk) * HD;
+        for (int c = 0; c < 4; ++c) kpre[c] = *reinterpret_cast<const float4*>(ksrc + 4 * (j + LPT * c));
 #pragma unroll
-                for (int c = 0; c < 4; ++c) kpre[c] = *reinterpret_cast<const float4*>(ksrc + 4 * (j + LPT * c));
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vpre[c] = *reinterpret_cast<const float4*>(vsrc + 4 * (j + LPT * c));
-        }
+        for (int c = 0; c < 4; ++c) vpre[c] = *reinterpret_cast<const f32x4*>(vsrc + 4 * (j + LPT * c));
     }
 
     // ---- q (and k_new) into LDS, with the optional prologue ----
@@ -214,13 +225,17 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
     for (int i = tid + kQRegs * kThreads; i < G * HD; i += kThreads) qs[i] = qg[i];
     if (have_new && tid < HD) ks[tid] = kreg;
     __syncthreads();
+    // The work-group whose chunk holds `pos` (the last one) is the only one
+    // that reads the new k: it alone runs k's prologue and writes the
+    // prologue results back to q_out / k_out.
+    const bool owner = p.pos >= ta && p.pos < tb;
     if (pro) {
-        for (int h = wv; h < G + (have_new ? 1 : 0); h += kWaves) {
+        for (int h = wv; h < G + (have_new && owner ? 1 : 0); h += kWaves) {
             if (h < G) prologue_head_r<HD>(qs + h * HD, pr.gq, p.q_gamma != nullptr, p.norm_qk, p.has_rope, p.eps, pr, lane);
             else prologue_head_r<HD>(ks, pr.gk, p.k_gamma != nullptr, p.norm_qk, p.has_rope, p.eps, pr, lane);
         }
         __syncthreads();
-        if (split == 0) {
+        if (owner) {
             if (p.q_out)
                 for (int i = tid; i < G * HD; i += kThreads) p.q_out[static_cast<size_t>(hk) * G * HD + i] = qs[i];
             if (p.k_out && have_new)
@@ -238,16 +253,27 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
         }
     }
 
+    // SHORT: the chunk's V rows into LDS for pass 2 (their last use of
+    // registers: held across the head-block loop they went to scratch memory)
+    if constexpr (SHORT) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) *reinterpret_cast<f32x4*>(vs + ts * HD + 4 * (j + LPT * c)) = vpre[c];
+    }
+
     for (int hb = 0; hb < G; hb += kHeadBlock) {
         const int nh = min(kHeadBlock, G - hb);
-        // q slices of this lane
-        float4 qf[kHeadBlock][4];
+        // q slices of this lane: kept in registers across the token passes of
+        // a long chunk; a one-pass chunk reads each head's slices from LDS where
+        // it uses them (64 registers fewer: four work-groups per CU)
+        float4 qf[SHORT ? 1 : kHeadBlock][4];
+        if constexpr (!SHORT) {
 #pragma unroll
-        for (int h = 0; h < kHeadBlock; ++h)
+            for (int h = 0; h < kHeadBlock; ++h)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                qf[h][c] = h < nh ? *reinterpret_cast<const float4*>(qs + (hb + h) * HD + 4 * (j + LPT * c))
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int c = 0; c < 4; ++c)
+                    qf[h][c] = h < nh ? *reinterpret_cast<const float4*>(qs + (hb + h) * HD + 4 * (j + LPT * c))
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
 
         // ---- pass 1: scores ----
         for (int t = ta; t < tb; t += TPP) {
@@ -272,15 +298,18 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
             for (int h = 0; h < kHeadBlock; ++h) {
                 float s = 0.0f;
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    s += qf[h][c].x * kf[c].x + qf[h][c].y * kf[c].y + qf[h][c].z * kf[c].z + qf[h][c].w * kf[c].w;
+                for (int c = 0; c < 4; ++c) {
+                    float4 qv;
+                    if constexpr (SHORT)
+                        qv = h < nh ? *reinterpret_cast<const float4*>(qs + (hb + h) * HD + 4 * (j + LPT * c))
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    else
+                        qv = qf[h][c];
+                    s += qv.x * kf[c].x + qv.y * kf[c].y + qv.z * kf[c].z + qv.w * kf[c].w;
+                }
                 s = group_sum<LPT>(s);
                 if (valid && j == 0 && h < nh) sc[h * p.chunk + (tok - ta)] = s * p.scale;
             }
-        }
-        if (SHORT && hb == 0) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) *reinterpret_cast<float4*>(vs + ts * HD + 4 * (j + LPT * c)) = vpre[c];
         }
         __syncthreads();
 
@@ -355,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(AttnParams p) {
                 float4 vf[4];
                 if (SHORT) {
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) vf[c] = vpre[c];
+                    for (int c = 0; c < 4; ++c) vf[c] = make_float4(vpre[c].x, vpre[c].y, vpre[c].z, vpre[c].w);
                 } else {
                     const float* src = (have_new && tok == p.pos)
                                            ? p.v_new + static_cast<size_t>(hk) * HD
@@ -819,27 +848,43 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
     auto po_at = [&](int s) {
         return *reinterpret_cast<const float4*>(part_o + (static_cast<size_t>(s) * n_heads + h) * hd + 4 * d4);
     };
+    // Every load a thread needs is issued here, unconditionally (split
+    // indices clamped to the last split, whose weight is then not used), so
+    // the kernel waits on memory once: this thread's (max, sum) pair of split
+    // tid and its U partial-o float4.
+    // (more than kMergeThreads splits: the pairs are read again where used)
+    const bool one_ml = n_split <= kMergeThreads;
+    auto ml_at = [&](int sp) {
+        return *reinterpret_cast<const float2*>(part_ml + (static_cast<size_t>(sp) * n_heads + h) * 2);
+    };
+    const float2 ml0 = ml_at(tid < n_split ? tid : n_split - 1);
     float4 po[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int sp = g + u * ng;
-        po[u] = sp < n_split ? po_at(sp) : make_float4(0.f, 0.f, 0.f, 0.f);
+        po[u] = po_at(sp < n_split ? sp : n_split - 1);
     }
-    float m = -1e30f;
-    for (int sp = tid; sp < n_split; sp += kMergeThreads)
-        m = fmaxf(m, part_ml[(static_cast<size_t>(sp) * n_heads + h) * 2]);
+    float m = tid < n_split ? ml0.x : -1e30f;
+    if (!one_ml)
+        for (int sp = tid + kMergeThreads; sp < n_split; sp += kMergeThreads) m = fmaxf(m, ml_at(sp).x);
     m = wave_max(m);
     if (lane == 0) red[0][wv] = m;
     __syncthreads();
     float M = red[0][0];
     for (int w = 1; w < kMergeThreads / 64; ++w) M = fmaxf(M, red[0][w]);
     float l = 0.0f;
-    for (int sp = tid; sp < n_split; sp += kMergeThreads) {
-        const float* ml = part_ml + (static_cast<size_t>(sp) * n_heads + h) * 2;
-        const float e = expf(ml[0] - M);
-        wgt[sp] = e;
-        l += ml[1] * e;
+    if (tid < n_split) {
+        const float e = expf(ml0.x - M);
+        wgt[tid] = e;
+        l += ml0.y * e;
     }
+    if (!one_ml)
+        for (int sp = tid + kMergeThreads; sp < n_split; sp += kMergeThreads) {
+            const float2 v = ml_at(sp);
+            const float e = expf(v.x - M);
+            wgt[sp] = e;
+            l += v.y * e;
+        }
     l = wave_sum(l);
     if (lane == 0) red[1][wv] = l;
     __syncthreads();

@@ -136,8 +136,16 @@ __device__ __forceinline__ float head_inv_rms(const float* v, int hd, float eps,
     const int full = hd & ~3;
     float part = 0.0f;
     if (lane < 4) {
-        // eight loads in flight ahead of the ordered adds (the order is the sum's)
+        // 32 loads in flight ahead of the ordered adds (the order is the sum's):
+        // a 128-wide head waits for LDS once
         int i = lane;
+        for (; i + 124 < full; i += 128) {
+            float a[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) a[u] = v[i + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) part += a[u] * a[u];
+        }
         for (; i + 28 < full; i += 32) {
             float a[8];
 #pragma unroll
@@ -147,8 +155,11 @@ __device__ __forceinline__ float head_inv_rms(const float* v, int hd, float eps,
         }
         for (; i < full; i += 4) part += v[i] * v[i];
     }
-    const float p0 = __shfl(part, 0, 64), p1 = __shfl(part, 1, 64);
-    const float p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
+    auto lane_val = [](float v, int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+    };
+    const float p0 = lane_val(part, 0), p1 = lane_val(part, 1);
+    const float p2 = lane_val(part, 2), p3 = lane_val(part, 3);
     double s = static_cast<double>(p0) + static_cast<double>(p1) + static_cast<double>(p2) + static_cast<double>(p3);
     for (int i = full; i < hd; ++i) s += static_cast<double>(v[i]) * static_cast<double>(v[i]);
     const float mean = static_cast<float>(s / static_cast<double>(hd));
