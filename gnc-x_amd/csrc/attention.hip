@@ -624,12 +624,12 @@ __global__ __launch_bounds__(kThreads) void attn_mq_kernel(AttnParams p) {
 //   attn_prefill_prologue_kernel: per token, the heads-RMSNorm + RoPE
 //     prologue of q and k in LDS (the decode prologue's arithmetic, with the
 //     token's own host-made cos/sin row), q written back, K/V rows stored;
-//   attn_prefill_kernel (head_dim 128, G = n_heads / n_kv dividing 32): the
-//     32 M-rows of the MFMA tiles are TQ = 32 / G query tokens x G heads of
-//     one KV head; the work-group walks the block's whole key range in
-//     64-token sub-chunks with the MQA kernel's S = Q K^T, online softmax and
-//     O += P V (fp32 MFMA), masking each row to its own causal window, and
-//     writes out = O / (l + 1e-12) directly (no split, no merge).
+//   attn_prefill_kernel (head_dim 128, G = n_heads / n_kv dividing 32): a
+//     work-group owns 128 query rows, 128 / G tokens x the G heads of one KV
+//     head, and walks the block's whole key range in 32-key sub-chunks with
+//     S^T = K Q^T, online softmax and O += P V (fp16 matrix cores, fp16-pair
+//     operands), masking each row to its own causal window, and writes
+//     out = O / (l + 1e-12) directly (no split, no merge).
 struct PrefillParams {
     float* q;             // [B][n_heads * HD], prologue result in place
     float* k;             // [B][n_kv * HD], prologue result in place
@@ -678,15 +678,57 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_prologue_kernel(Prefill
     }
 }
 
-__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p) {
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+// 8 floats as an fp16 pair: hi = fp16(v), lo = fp16(v - hi) (v - hi is exact
+// in fp32), so hi + lo carries about 22 significant bits of v.  Below fp16's
+// normal range lo keeps an absolute step of 2^-24, far below what these
+// attention sums resolve.
+__device__ __forceinline__ void split8(const float (&v)[8], half8_t& hi, half8_t& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const _Float16 h = static_cast<_Float16>(v[i]);
+        hi[i] = h;
+        lo[i] = static_cast<_Float16>(v[i] - static_cast<float>(h));
+    }
+}
+
+// The causal batch on the fp16 matrix cores.  A work-group owns 128 query rows
+// (128 / G tokens x the G heads of one KV head), a wave 32 of them, and walks
+// the rows' key range in 32-key sub-chunks:
+//   stage   the sub-chunk's K and V rows are loaded once per work-group (the
+//           next sub-chunk's loads are in flight during this one's products),
+//           split into fp16 pairs (hi = fp16(v), lo = fp16(v - hi): about 22
+//           significant bits) and written to LDS in MFMA operand order;
+//   S^T     = K Q^T on v_mfma_f32_32x32x16_f16, three products per K16 slice
+//           (hi hi, hi lo, lo hi; the lo lo term is below 2^-22 of the
+//           product), Q split once at the start: lane (i, g) ends up holding
+//           the scores of query row i (of its wave) for the 16 keys
+//           8 a + 4 g + b (a, b = 0..3) of the sub-chunk;
+//   softmax the online update of each row's max and sum in registers (the two
+//           lane halves of a row meet with one exchange each);
+//   O += P V with P straight from those registers as the MFMA's A operand:
+//           its K16 slice c holds keys 16 c + 4 g + {0..3, 8..11} in lane half
+//           g, and the staged V fragments take the same key order.  O rows
+//           are rescaled by the rows' factors through a 32-float LDS array.
+// A 64-key sub-chunk of 32 rows with operands from registers and S transposed
+// through LDS (the fp32-MFMA form before this) read each K/V row once per 32
+// rows instead of once per 128.
+// Operands hold |values| < 65504 (fp16's range): q and k after the
+// heads-RMSNorm, v and the probabilities in [0, 1].
+constexpr int kPfRows = 128;  // query rows (token, head) per work-group
+constexpr int kPfKeys = 32;   // keys per sub-chunk
+
+__global__ __launch_bounds__(kThreads, 2) void attn_prefill_kernel(PrefillParams p) {
     constexpr int HD = 128;
-    constexpr int R = 32;  // MFMA M-rows: (query token, head) pairs
-    __shared__ __align__(16) float spart[2][R][kMqLd];
-    __shared__ __align__(16) float pl[R][kMqLd];
-    __shared__ float alpha_s[R], m_s[R], l_s[R];
+    // operand fragments: 8 halves per lane, [slice][lane] for K (A of S^T),
+    // [N tile][slice][lane] for V (B of P V)
+    __shared__ __align__(16) half8_t khi[HD / 16][64], klo[HD / 16][64];
+    __shared__ __align__(16) half8_t vhi[HD / 32][kPfKeys / 16][64], vlo[HD / 32][kPfKeys / 16][64];
+    __shared__ __align__(16) float rowf[kWaves][32];  // per-row factors on their way to the O layout
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int li = lane & 31, g = lane >> 5;
-    const int G = p.n_heads / p.n_kv, TQ = R / G;
+    const int G = p.n_heads / p.n_kv, TQ = kPfRows / G;
     const int hk = blockIdx.x;
     const int blk = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);  // longest key ranges first
     const int q0 = blk * TQ;
@@ -695,125 +737,180 @@ __global__ __launch_bounds__(kThreads) void attn_prefill_kernel(PrefillParams p)
     const int lo_first = p.sw > 0 ? max(0, p.pos0 + q0 - p.sw + 1) : 0;
     const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
     const size_t q_dim = static_cast<size_t>(p.n_heads) * HD;
-    auto krow = [&](int t) { return p.k_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD; };
-    auto vrow = [&](int t) { return p.v_cache + static_cast<size_t>(t) * kv_dim + static_cast<size_t>(hk) * HD; };
+    const float* kbase = p.k_cache + static_cast<size_t>(hk) * HD;
+    const float* vbase = p.v_cache + static_cast<size_t>(hk) * HD;
 
-    const int tt = wv & 1, dh = wv >> 1;
-    const int dq = 64 * dh + 32 * g;
-    float qa[32];
+    // this lane's query row: row 32 wv + li of the work-group, token
+    // (32 wv + li) / G of the block, head (32 wv + li) % G of KV head hk
+    const int qrow = 32 * wv + li;
+    const int qt = qrow / G;
+    const bool qvalid = qt < nq;
+    const int q_hi = p.pos0 + q0 + qt;                          // last key of its window
+    const int q_lo = p.sw > 0 ? max(0, q_hi - p.sw + 1) : 0;    // first key
+    half8_t qh[HD / 16], ql[HD / 16];
     {
-        const int qt = li / G, h = li % G;
-        if (qt < nq) {
-            const float* qr = p.q + static_cast<size_t>(q0 + qt) * q_dim + (static_cast<size_t>(hk) * G + h) * HD + dq;
+        const float* qr = p.q + static_cast<size_t>(q0 + (qvalid ? qt : 0)) * q_dim +
+                          (static_cast<size_t>(hk) * G + qrow % G) * HD + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 v = *reinterpret_cast<const float4*>(qr + 4 * i);
-                qa[4 * i] = v.x; qa[4 * i + 1] = v.y; qa[4 * i + 2] = v.z; qa[4 * i + 3] = v.w;
-            }
-        } else {
+        for (int c = 0; c < HD / 16; ++c) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 16 * c);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 16 * c + 4);
+            float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            if (!qvalid)
 #pragma unroll
-            for (int i = 0; i < 32; ++i) qa[i] = 0.0f;
+                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+            split8(v, qh[c], ql[c]);
         }
     }
-    if (tid < R) {
-        m_s[tid] = -1e30f;
-        l_s[tid] = 0.0f;
-    }
-    floatx16 o;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[r] = 0.0f;
-    __syncthreads();
 
-    // (the V-before-S and next-K prefetch of attn_mq_kernel measured slower
-    // here, 614 against 544 us per layer at 2048 tokens: it takes 194 VGPRs
-    // against 121, half the waves per SIMD, and this loop has no other work
-    // to hide its loads behind)
-    for (int sa = lo_first; sa <= hi_last; sa += kMqSub) {
-        {
-            const int tok = sa + 32 * tt + li;
-            const float* kr = krow(tok <= hi_last ? tok : hi_last) + dq;
-            float kb[32];
+    // staging slots of this thread: K slots tid, tid + 256 (slot s: slice
+    // s / 64, lane s % 64 -> key s % 32, dims 16 slice + 8 ((s % 64) / 32));
+    // V slots tid, tid + 256 (slot s: N tile s / 128, slice (s / 64) % 2,
+    // lane s % 64 -> dim 32 tile + s % 32, keys 16 slice + 4 half + {0..3, 8..11})
+    float4 kst[2][2];
+    float vst[2][8];
+    auto prefetch = [&](int sa) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int sl = tid + 256 * u;
+            const int c = sl >> 6, L = sl & 63;
+            int key = sa + (L & 31);
+            key = key <= hi_last ? key : hi_last;
+            const float* kr = kbase + static_cast<size_t>(key) * kv_dim + 16 * c + 8 * (L >> 5);
+            kst[u][0] = *reinterpret_cast<const float4*>(kr);
+            kst[u][1] = *reinterpret_cast<const float4*>(kr + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int sl = tid + 256 * u;
+            const int n = sl >> 7, c = (sl >> 6) & 1, L = sl & 63;
+            const int d = 32 * n + (L & 31);
+            const int k0 = sa + 16 * c + 4 * (L >> 5);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float4 v = *reinterpret_cast<const float4*>(kr + 4 * i);
-                kb[4 * i] = v.x; kb[4 * i + 1] = v.y; kb[4 * i + 2] = v.z; kb[4 * i + 3] = v.w;
-            }
-            floatx16 sacc;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-#pragma unroll
-            for (int kk = 0; kk < 32; ++kk) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[kk], kb[kk], sacc, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) spart[dh][8 * (r >> 2) + 4 * g + (r & 3)][32 * tt + li] = sacc[r];
-        }
-        __syncthreads();
-        // online softmax: wave w updates rows 8 w .. 8 w + 7, lane = key; the
-        // eight rows go through each step together (independent DPP max / sum
-        // reductions), then lane i < 8 updates the running max / sum of row 8 w + i
-        {
-            float sv[8], mo[8], mn[8], su[8];
-            bool valid[8];
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int r = 8 * wv + rr;
-                const int qt = r / G;
-                const int hi = p.pos0 + q0 + qt;
-                const int lo = p.sw > 0 ? max(0, hi - p.sw + 1) : 0;
-                const int key = sa + lane;
-                valid[rr] = qt < nq && key >= lo && key <= hi;
-                sv[rr] = valid[rr] ? (spart[0][r][lane] + spart[1][r][lane]) * p.scale : -1e30f;
-                mo[rr] = m_s[r];
-            }
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) mn[rr] = fmaxf(mo[rr], wave_max(sv[rr]));
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const float e = valid[rr] ? expf(sv[rr] - mn[rr]) : 0.0f;
-                pl[8 * wv + rr][lane] = e;
-                su[rr] = wave_sum(e);
-            }
-            float m_old = mo[0], m_new = mn[0], sum = su[0];
-#pragma unroll
-            for (int rr = 1; rr < 8; ++rr) {
-                m_old = lane == rr ? mo[rr] : m_old;
-                m_new = lane == rr ? mn[rr] : m_new;
-                sum = lane == rr ? su[rr] : sum;
-            }
-            if (lane < 8) {
-                const int r = 8 * wv + lane;
-                const float a = expf(m_old - m_new);
-                alpha_s[r] = a;
-                l_s[r] = l_s[r] * a + sum;
-                m_s[r] = m_new;
+                int key = k0 + (i & 3) + 8 * (i >> 2);
+                key = key <= hi_last ? key : hi_last;
+                vst[u][i] = vbase[static_cast<size_t>(key) * kv_dim + d];
             }
         }
-        __syncthreads();
-        {
+    };
+    auto stage = [&]() {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[r] *= alpha_s[8 * (r >> 2) + 4 * g + (r & 3)];
-            float pa[32], vb[32];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 v = *reinterpret_cast<const float4*>(&pl[li][32 * g + 4 * i]);
-                pa[4 * i] = v.x; pa[4 * i + 1] = v.y; pa[4 * i + 2] = v.z; pa[4 * i + 3] = v.w;
-            }
-#pragma unroll
-            for (int kk = 0; kk < 32; ++kk) {
-                const int t = sa + 32 * g + kk;
-                vb[kk] = vrow(t <= hi_last ? t : hi_last)[32 * wv + li];
-            }
-#pragma unroll
-            for (int kk = 0; kk < 32; ++kk) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[kk], vb[kk], o, 0, 0, 0);
+        for (int u = 0; u < 2; ++u) {
+            const int sl = tid + 256 * u;
+            const float kv[8] = {kst[u][0].x, kst[u][0].y, kst[u][0].z, kst[u][0].w,
+                                 kst[u][1].x, kst[u][1].y, kst[u][1].z, kst[u][1].w};
+            half8_t h, l;
+            split8(kv, h, l);
+            khi[sl >> 6][sl & 63] = h;
+            klo[sl >> 6][sl & 63] = l;
         }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int sl = tid + 256 * u;
+            half8_t h, l;
+            split8(vst[u], h, l);
+            vhi[sl >> 7][(sl >> 6) & 1][sl & 63] = h;
+            vlo[sl >> 7][(sl >> 6) & 1][sl & 63] = l;
+        }
+    };
+
+    float m_run = -1e30f, l_run = 0.0f;  // row qrow's running max and sum
+    floatx16 o[HD / 32];
+#pragma unroll
+    for (int n = 0; n < HD / 32; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[n][r] = 0.0f;
+
+    prefetch(lo_first);
+    for (int sa = lo_first; sa <= hi_last; sa += kPfKeys) {
+        stage();
         __syncthreads();
+        if (sa + kPfKeys <= hi_last) prefetch(sa + kPfKeys);
+        // S^T for the sub-chunk: rows = keys, columns = this wave's query rows
+        floatx16 st;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HD / 16; ++c) {
+            const half8_t kh = khi[c][lane], kl = klo[c][lane];
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], st, 0, 0, 0);
+        }
+        // online softmax of row qrow over keys sa + 8 a + 4 g + b (r = 4 a + b)
+        float mx = -1e30f;
+        bool valid[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = sa + 8 * (r >> 2) + 4 * g + (r & 3);
+            valid[r] = qvalid && key >= q_lo && key <= q_hi;
+            st[r] = valid[r] ? st[r] * p.scale : -1e30f;
+            mx = fmaxf(mx, st[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        float e[16], sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            e[r] = valid[r] ? expf(st[r] - m_new) : 0.0f;
+            sum += e[r];
+        }
+        sum += __shfl_xor(sum, 32, 64);
+        const float alpha = expf(m_run - m_new);
+        l_run = l_run * alpha + sum;
+        m_run = m_new;
+        // O rows are 8 (r / 4) + 4 g + r % 4 of the wave: their factors via LDS
+        if (g == 0) rowf[wv][li] = alpha;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own writes, read back below
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+            const float4 f = *reinterpret_cast<const float4*>(&rowf[wv][8 * a4 + 4 * g]);
+#pragma unroll
+            for (int n = 0; n < HD / 32; ++n) {
+                o[n][4 * a4] *= f.x;
+                o[n][4 * a4 + 1] *= f.y;
+                o[n][4 * a4 + 2] *= f.z;
+                o[n][4 * a4 + 3] *= f.w;
+            }
+        }
+        // O += P V: slice c takes the exponentials e[8 c .. 8 c + 7]
+#pragma unroll
+        for (int c = 0; c < kPfKeys / 16; ++c) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pv[i] = e[8 * c + i];
+            half8_t ph, plo;
+            split8(pv, ph, plo);
+#pragma unroll
+            for (int n = 0; n < HD / 32; ++n) {
+                const half8_t vh = vhi[n][c][lane], vl = vlo[n][c][lane];
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, vh, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, vl, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(plo, vh, o[n], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // every wave is done with this sub-chunk's K / V fragments
     }
+    // out = O / (l + 1e-12), the rows' sums through LDS like the factors
+    if (g == 0) rowf[wv][li] = 1.0f / (l_run + 1e-12f);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * g + (r & 3);
-        const int qt = row / G, h = row % G;
-        if (qt < nq)
-            p.out[static_cast<size_t>(q0 + qt) * q_dim + (static_cast<size_t>(hk) * G + h) * HD + 32 * wv + li] =
-                o[r] * (1.0f / (l_s[row] + 1e-12f));
+    for (int a4 = 0; a4 < 4; ++a4) {
+        const float4 f = *reinterpret_cast<const float4*>(&rowf[wv][8 * a4 + 4 * g]);
+        const float fr[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int row = 32 * wv + 8 * a4 + 4 * g + b;
+            const int t = row / G, h = row % G;
+            if (t < nq) {
+                float* dst = p.out + static_cast<size_t>(q0 + t) * q_dim + (static_cast<size_t>(hk) * G + h) * HD;
+#pragma unroll
+                for (int n = 0; n < HD / 32; ++n) dst[32 * n + li] = o[n][4 * a4 + b] * fr[b];
+            }
+        }
     }
 }
 
@@ -1099,7 +1196,7 @@ hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream) {
                          reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out) |
                          reinterpret_cast<uintptr_t>(a.k_cache) | reinterpret_cast<uintptr_t>(a.v_cache);
     if (al & 15u) return hipErrorInvalidValue;
-    const int32_t G = a.n_heads / a.n_kv_heads, TQ = 32 / G;
+    const int32_t G = a.n_heads / a.n_kv_heads, TQ = kPfRows / G;
     const int32_t nblk = (a.batch + TQ - 1) / TQ;
     if (nblk > 65535) return hipErrorInvalidValue;
     PrefillParams p{};
