@@ -558,6 +558,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 // block, matrix i's [b x n[i]] part at b npre[i] in it (npre: rows of the
 // matrices before i).
 constexpr int kMaxMbMats = 4;
+#ifndef GNCX_MB_XCD
+#define GNCX_MB_XCD 1
+#endif
 struct MbMats {
     const uint8_t* w[kMaxMbMats];
     float* y[kMaxMbMats];
@@ -566,7 +569,30 @@ struct MbMats {
     int32_t npre[kMaxMbMats];
     int32_t ntot;
     int32_t count;
+    int32_t xcd_a;  // XCD tile order (xcd_tiles): x-tile groups per plane, 0 = grid order
 };
+
+// XCD-aware tile order.  Work-groups are dealt to the 8 XCDs in turn (group
+// i of the grid to XCD i % 8), and each XCD has its own L2, so a tile order
+// decides how many XCDs fetch each operand: in grid order (x fastest, with a
+// multiple of 8 x-tiles) every XCD gets whole columns of x-tiles and reads
+// every token tile's activations, 8 times in all.  With xcd_a = a the
+// (x, y) plane is cut into a x (8 / a) blocks, one per XCD, walked y fastest:
+// each weight tile is then read by 8 / a XCDs and each token tile by a of
+// them (a chosen per launch from the operand sizes).  Requires x-tiles % a,
+// y-tiles % (8 / a) and the plane's size % 8 to be 0.
+__device__ __forceinline__ void xcd_tiles(int xcd_a, int& bx, int& by) {
+    bx = static_cast<int>(blockIdx.x);
+    by = static_cast<int>(blockIdx.y);
+    if (xcd_a <= 0) return;
+    const int gx = static_cast<int>(gridDim.x), gy = static_cast<int>(gridDim.y);
+    const int lin = bx + gx * by;
+    const int xcd = lin & 7, slot = lin >> 3;
+    const int nyb = 8 / xcd_a;
+    const int sxn = gx / xcd_a, syn = gy / nyb;
+    by = (xcd / xcd_a) * syn + slot % syn;
+    bx = (xcd % xcd_a) * sxn + slot / syn;
+}
 
 // The outputs of a split-K reduce: flat partial indices [end[i - 1], end[i])
 // go to y[i] (end[-1] = 0), each y[i] one contiguous [b x n] block.
@@ -581,12 +607,14 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     MbMats mats, size_t rbytes, const _Float16* __restrict xhl, const _Float16* __restrict pq,
     const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk, float* __restrict part) {
     constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
+    int bx, by;
+    xcd_tiles(mats.xcd_a, bx, by);
     const uint8_t* __restrict w = mats.w[0];
     float* __restrict y = mats.y[0];
     int32_t n = mats.n[0], tile0 = 0, npre = 0;
 #pragma unroll
     for (int i = 1; i < kMaxMbMats; ++i) {
-        if (mats.count > i && static_cast<int32_t>(blockIdx.x) >= mats.tile0[i]) {
+        if (mats.count > i && bx >= mats.tile0[i]) {
             w = mats.w[i];
             y = mats.y[i];
             n = mats.n[i];
@@ -632,7 +660,7 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = wv % MW, wn = wv / MW;
     const int li = lane & 31, lh = lane >> 5;
-    const int32_t t0 = blockIdx.y * BM, n0 = (static_cast<int32_t>(blockIdx.x) - tile0) * BN;
+    const int32_t t0 = by * BM, n0 = (bx - tile0) * BN;
     const int32_t kb = blockIdx.z * kchunk;
     const int32_t ke = min(k, kb + kchunk);
     const int32_t nsb = (ke - kb) / 256;
@@ -1086,7 +1114,28 @@ hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq
     constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
     const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
     const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
-    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, m,
+    // XCD tile order: the block split with the least operand traffic, counting
+    // a weight tile (BN rows of the K range) once per XCD that reads it, and
+    // an activation tile (BM tokens of the K range as fp16 pairs) likewise
+    MbMats mx = m;
+    mx.xcd_a = 0;
+#if GNCX_MB_XCD
+    const double wt = static_cast<double>(BN) * (p.kchunk / 256) * 144.0;
+    const double at = static_cast<double>(BM) * p.kchunk * 4.0;
+    const int gx = static_cast<int>(grid.x), gy = static_cast<int>(grid.y);
+    double best = gx * wt + 8.0 * gy * at;  // grid order (with gx % 8 == 0, the same as a = 8)
+    if ((gx * gy) % 8 == 0) {
+        for (int a = 1; a < 8; a *= 2) {
+            if (gx % a != 0 || gy % (8 / a) != 0) continue;
+            const double cost = 8.0 * gx * wt / a + 8.0 * gy * at / (8 / a);
+            if (cost < best) {
+                best = cost;
+                mx.xcd_a = a;
+            }
+        }
+    }
+#endif
+    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, mx,
                        row_bytes(kQ4_K, k), xhl, pq, rscale, b, k, p.kchunk, part);
     return hipGetLastError();
 }
