@@ -228,21 +228,25 @@ enum WeightTrust : int { kUntracked = 0, kRamBuffer = 1, kMapped = 2 };
 int tracked_host_range(const void* p, size_t bytes);
 
 // Device view of `bytes` weight bytes at p (host: uploaded once, cached).
+// A copy is keyed by the host address, and the signature reads only the
+// `bytes` this call names: the memory at p may now be a different, smaller
+// allocation than the one copied (a freed array whose address came back), so
+// bytes past the call's range may be unmapped.  A copy of another size is
+// dropped and made again.
 const uint8_t* device_weights(const uint8_t* p, size_t bytes, const char* where) {
     const uintptr_t key = reinterpret_cast<uintptr_t>(p);
     auto it = g_rt.weights.find(key);
     if (it != g_rt.weights.end() && it->second.bytes >= bytes) {
         if (it->second.trust == kMapped) return it->second.d;
         if (it->second.trust == kRamBuffer) {
-            if (it->second.sig == host_signature(p, it->second.bytes)) return it->second.d;
+            if (it->second.bytes == bytes && it->second.sig == host_signature(p, bytes)) return it->second.d;
             forget_weight(key);
             it = g_rt.weights.end();
         }
     }
     if (is_device_ptr(p)) return p;
     if (it != g_rt.weights.end()) {
-        if (it->second.bytes >= bytes && it->second.sig == host_signature(p, it->second.bytes))
-            return it->second.d;
+        if (it->second.bytes == bytes && it->second.sig == host_signature(p, bytes)) return it->second.d;
         forget_weight(key);
     }
     DevWeight w;

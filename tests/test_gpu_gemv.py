@@ -158,6 +158,42 @@ def test_weight_cache_detects_rewritten_host_buffer(lib, oracle):
     assert rel_l2(y, oracle.matvec(Q6_K, w, x, k, n)) < TOL
 
 
+def test_weight_cache_reads_only_the_calls_range(lib, oracle):
+    """A weight copy is keyed by host address; when the memory there is now a
+    smaller allocation (a freed array whose address came back), the cache
+    check must read only the bytes this call names.  Here the tail of the
+    first call's mapping is unmapped before a call with fewer rows at the same
+    address: a check over the first call's size would read unmapped pages."""
+    libc = C.CDLL(None, use_errno=True)
+    libc.mmap.restype = C.c_void_p
+    libc.mmap.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_long]
+    libc.munmap.argtypes = [C.c_void_p, C.c_size_t]
+    k, n_big, n_small = 256, 1024, 256  # 144-byte rows: 36 and 9 pages of 4 KiB
+    rb = 144
+    big, small = n_big * rb, n_small * rb
+    assert small % 4096 == 0
+    addr = libc.mmap(None, big, 0x1 | 0x2, 0x02 | 0x20, -1, 0)  # PROT_READ|WRITE, MAP_PRIVATE|ANONYMOUS
+    assert addr not in (None, C.c_void_p(-1).value)
+    mapped = big
+    try:
+        w = synth.make_weights(Q4_K, n_big, k, seed=71)
+        C.memmove(addr, w.ctypes.data, big)
+        x = synth.make_activations(1, k, seed=72)
+        y = np.zeros(n_big, np.float32)
+        lib.gncx_xfold_universal_matvec(C.c_void_p(addr), 0, Q4_K, ptr(x), None, k, n_big, ptr(y), None)
+        gncx.check(lib)
+        assert rel_l2(y, oracle.matvec(Q4_K, w, x, k, n_big)) < TOL
+        assert libc.munmap(C.c_void_p(addr + small), big - small) == 0
+        mapped = small
+        ys = np.zeros(n_small, np.float32)
+        lib.gncx_xfold_universal_matvec(C.c_void_p(addr), 0, Q4_K, ptr(x), None, k, n_small, ptr(ys), None)
+        gncx.check(lib)
+        assert rel_l2(ys, oracle.matvec(Q4_K, w[:small], x, k, n_small)) < TOL
+    finally:
+        lib.gncx_hip_weight_forget(C.c_void_p(addr))
+        libc.munmap(C.c_void_p(addr), mapped)
+
+
 def test_activation_cache_follows_reference_rule(lib, oracle):
     """With in_tokens given, the same in_vec pointer and no new norm epoch,
     the reference reuses its quantised activations (cpp:1345) -- even when
@@ -206,9 +242,7 @@ MATBATCH_CASES = [
     (Q4_K, 4096, 512, 64), (Q6_K, 14336, 256, 16), (Q4_0, 4096, 300, 5), (Q8_0, 2048, 200, 9), (Q4_K, 512, 96, 1),
     (BF16, 1024, 64, 4), (Q4_K, 4096, 1024, 256), (Q6_K, 2048, 4160, 100), (Q4_0, 96, 130, 70),
     (Q8_0, 2080, 333, 33),
-    pytest.param(Q4_K, 256, 16384, 300, marks=pytest.mark.skip(
-        reason="ran the 256x128 MFMA tile, whose one launch ended the process with a host segmentation fault; "
-               "that tile is switched off and this case stays off the GPU until the cause is found")),
+    (Q4_K, 256, 16384, 300),
     (Q4_K, 256, 8192, 500), (Q6_K, 256, 16384, 128), (Q4_K, 256, 16384, 512), (Q6_K, 512, 8192, 520),
     # the 256-token tiles of 8 waves (256 x 128 and 256 x 64), ragged B and N
     (Q6_K, 256, 24576, 260), (Q4_K, 256, 8192, 300), (Q8_0, 512, 6000, 257),
@@ -218,6 +252,8 @@ MATBATCH_CASES = [
     (Q4_K, 4096, 3000, 200), (Q4_K, 2048, 700, 33),
     # 128 x 128 tiles of 4 waves with K split (65 to 128 tokens, types other than Q4_K)
     (Q8_0, 1024, 640, 128), (Q6_K, 14336, 512, 77),
+    # Q4_K at small B: one super-block, K of 3, 5 and 48 super-blocks, ragged B and N
+    (Q4_K, 256, 100, 17), (Q4_K, 768, 50, 64), (Q4_K, 1280, 33, 2), (Q4_K, 12288, 200, 48),
 ]
 
 
