@@ -271,6 +271,22 @@ struct WSeg<kQ6_K> {
         scw = r.ldu16(blk + 192u + 8u * h + 2u * g);  // scales l0 / 16 + 2g of this half
         d = r.ldu16(blk + 208u);
     }
+    // sc (q - 32) as integers, |sc (q - 32)| <= 4096 (d is applied per
+    // super-block); returns sc
+    __device__ __forceinline__ int get_int(int32_t e0, int (&v)[16]) const {
+        const int rr = e0 % 256, g = (rr % 128) / 32, l0 = rr % 32;
+        const int sc = static_cast<int8_t>((scw >> (l0 >= 16 ? 8 : 0)) & 0xffu);
+        const uint4 a = raw16_get(ql, sh), b = raw16_get(qh, sh);
+        const uint32_t L[4] = {a.x, a.y, a.z, a.w}, H[4] = {b.x, b.y, b.z, b.w};
+        const int lsh = 4 * (g >> 1), hsh = 2 * g;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int sh8 = 8 * (i & 3);
+            const int q = static_cast<int>(((L[i >> 2] >> (lsh + sh8)) & 15u) | (((H[i >> 2] >> (hsh + sh8)) & 3u) << 4));
+            v[i] = sc * (q - 32);
+        }
+        return sc;
+    }
     __device__ __forceinline__ void get(int32_t e0, float (&v)[16]) const {
         const int rr = e0 % 256, g = (rr % 128) / 32, l0 = rr % 32;
         const float s = half_bits_to_float(d) * static_cast<float>(static_cast<int8_t>((scw >> (l0 >= 16 ? 8 : 0)) & 0xffu));
@@ -308,6 +324,17 @@ struct WSeg<kQ6_K> {
 // blockIdx.z selects a K range of kchunk (split K); with gridDim.z > 1 the
 // tile goes to part[z][t][m] and matbatch_reduce_kernel adds the ranges in
 // order.
+// Q6_K weights are d (sc (q - 32)) (cpp:742-757) with sc (q - 32) an integer
+// of magnitude at most 4096 and d fixed over a 256-value super-block, so the
+// weight operand is that integer: exact in fp16 up to 2048 (|sc| <= 64),
+// else its fp16 rounding (hi) plus an exact remainder of -1, 0 or 1 (lo).
+// On the 256-token tiles (B > 128) the products of a super-block go to a
+// second accumulator D, folded in as
+// acc += d D at its end (d of the lane's weight row), and x_hi w_lo, the
+// third product, runs only in steps where some weight of the tile has
+// |sc| > 64: elsewhere w_lo is zero.  The third product's step flag is the
+// step's first K index, written to LDS by any thread that dequantised such
+// a scale (a stale flag never equals a later step's index).
 constexpr int kMfKs = 32;
 constexpr int kMfLd = kMfKs + 8;  // halves per LDS row (16-byte aligned, staggers banks)
 // a buffer offset past any resource (resources here are below 2^30 bytes);
@@ -349,13 +376,27 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
     const int32_t ke = min(k, kb + kchunk);
     const int32_t nsteps = (ke - kb + kMfKs - 1) / kMfKs;
 
-    floatx16 acc[WM][WN];
+    // (the 256-token tiles only: on the smaller ones D's registers cost
+    // occupancy, measured 5-11% slower at B = 16 to 100)
+    constexpr bool Q6 = TYPE == kQ6_K && MW == 4;
+    // Q6_K: d of the tile's rows per super-block parity, the third-product flags
+    __shared__ float q6d[Q6 ? 2 : 1][Q6 ? BN : 1];
+    __shared__ int32_t q6big[2];
+    floatx16 acc[WM][WN], D[Q6 ? WM : 1][Q6 ? WN : 1];
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    if constexpr (Q6) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) D[i][j][r] = 0.0f;
+    }
 
     // activation chunks c = tid + THREADS i: token row c / 4 of the tile,
     // values 8 (c % 4) .. + 8 of the step, hi at byte 32 j and lo at 32 j + 16
@@ -407,12 +448,33 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
             *reinterpret_cast<uint4*>(&xs[buf][1][r * kMfLd + 8 * seg]) = xr[i][1];
         }
         if (tid < 2 * BN) {
-            float v[16];
             const int32_t kw = k0 + 16 * wseg;
-            wr[set].get(kw < ke ? kw : 0, v);
             uint32_t hi[8], lo[8];
+            if constexpr (Q6) {
+                int v[16];
+                const int sc = wr[set].get_int(kw < ke ? kw : 0, v);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) split2(v[2 * i], v[2 * i + 1], hi[i], lo[i]);
+                for (int i = 0; i < 8; ++i) {
+                    const _Float16 h0 = static_cast<_Float16>(static_cast<float>(v[2 * i]));
+                    const _Float16 h1 = static_cast<_Float16>(static_cast<float>(v[2 * i + 1]));
+                    const _Float16 l0 = static_cast<_Float16>(static_cast<float>(v[2 * i]) - static_cast<float>(h0));
+                    const _Float16 l1 =
+                        static_cast<_Float16>(static_cast<float>(v[2 * i + 1]) - static_cast<float>(h1));
+                    hi[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+                    lo[i] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l0)) |
+                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+                }
+                if (sc > 64 || sc < -64) q6big[buf] = k0;
+                // a super-block's first step in this range stores the rows' d
+                if (wseg == 0 && (k0 == kb || k0 % 256 == 0))
+                    q6d[(k0 / 256) & 1][wrow] = half_bits_to_float(kw < ke ? wr[set].d : 0u);
+            } else {
+                float v[16];
+                wr[set].get(kw < ke ? kw : 0, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) split2(v[2 * i], v[2 * i + 1], hi[i], lo[i]);
+            }
             uint4* dh = reinterpret_cast<uint4*>(&ws[buf][0][wrow * kMfLd + 16 * wseg]);
             uint4* dl = reinterpret_cast<uint4*>(&ws[buf][1][wrow * kMfLd + 16 * wseg]);
             dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -423,6 +485,59 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
     };
 
     const int li = lane & 31, lk = 8 * (lane >> 5);
+    // Q6_K: products into D, the third only where a weight has |sc| > 64;
+    // D folded into acc with d at a super-block's last step in the range
+    auto compute_q6 = [&](int buf, int32_t k0) {
+        const bool third = q6big[buf] == k0;
+#pragma unroll
+        for (int kk = 0; kk < kMfKs; kk += 16) {
+            half8 ah[WM], al[WM], bh[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int o = (wm * 32 * WM + 32 * i + li) * kMfLd + kk + lk;
+                ah[i] = *reinterpret_cast<const half8*>(&xs[buf][0][o]);
+                al[i] = *reinterpret_cast<const half8*>(&xs[buf][1][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                bh[j] = *reinterpret_cast<const half8*>(&ws[buf][0][(wn * 32 * WN + 32 * j + li) * kMfLd + kk + lk]);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], D[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], D[i][j], 0, 0, 0);
+            if (third) {
+                half8 bl[WN];
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    bl[j] =
+                        *reinterpret_cast<const half8*>(&ws[buf][1][(wn * 32 * WN + 32 * j + li) * kMfLd + kk + lk]);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int j = 0; j < WN; ++j)
+                        D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], D[i][j], 0, 0, 0);
+            }
+        }
+        if ((k0 + kMfKs) % 256 == 0 || k0 + kMfKs >= ke) {
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const float dv = q6d[(k0 / 256) & 1][wn * 32 * WN + 32 * j + li];
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        acc[i][j][r] = fmaf(D[i][j][r], dv, acc[i][j][r]);
+                        D[i][j][r] = 0.0f;
+                    }
+            }
+        }
+    };
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kMfKs; kk += 16) {
@@ -475,13 +590,15 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
         const int32_t k0 = kb + s * kMfKs;
         gload_x(k0 + kMfKs);
         gload_w(0, k0 + 2 * kMfKs);
-        compute(0);
+        if constexpr (Q6) compute_q6(0, k0);
+        else compute(0);
         if (s + 1 < nsteps) lstore(1, 1, k0 + kMfKs);
         __syncthreads();
         if (s + 1 >= nsteps) break;
         gload_x(k0 + 2 * kMfKs);
         gload_w(1, k0 + 3 * kMfKs);
-        compute(1);
+        if constexpr (Q6) compute_q6(1, k0 + kMfKs);
+        else compute(1);
         if (s + 2 < nsteps) lstore(0, 0, k0 + 2 * kMfKs);
         __syncthreads();
     }

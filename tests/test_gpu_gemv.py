@@ -269,6 +269,31 @@ def test_matbatch_parity(lib, oracle, t, k, n, b):
     assert err < (TOL if t == BF16 else TOL_MATBATCH)
 
 
+# Q6_K scales beyond +-64 (real quantisers use the whole int8 range): then
+# sc (q - 32) can exceed 2048 and the 256-token tiles add the third product in
+# the steps that hold such a scale.  All rows large, none, and one row in
+# 37 large (single steps of a tile), with K split (k=2048, b=200) and unsplit.
+@pytest.mark.parametrize("mode", ["all", "sparse"])
+@pytest.mark.parametrize("k,n,b", [(2048, 512, 200), (1024, 3000, 300)])
+def test_matbatch_q6k_large_scales(lib, oracle, mode, k, n, b):
+    w = synth.make_weights(Q6_K, n, k, seed=8100 + k + n).reshape(n, k // 256, 210)
+    rng = np.random.default_rng(8200 + b)
+    big = rng.integers(-128, 128, size=w[..., 192:208].shape).astype(np.int8).view(np.uint8)
+    if mode == "all":
+        w[..., 192:208] = big
+    else:
+        rows = np.arange(n) % 37 == 5
+        w[rows, :, 192:208] = big[rows]
+    w = np.ascontiguousarray(w.reshape(-1))
+    x = synth.make_activations(b, k, seed=8300 + b).reshape(b, k)
+    y = np.full((b, n), np.nan, np.float32)
+    lib.gncx_xfold_universal_matbatch(ptr(w), 0, Q6_K, ptr(x), b, k, n, ptr(y), None)
+    gncx.check(lib)
+    err = rel_l2(y, oracle.matbatch(Q6_K, w, x, b, k, n))
+    print(f"matbatch Q6_K {mode} large scales k={k} n={n} b={b} rel_l2={err:.3e}", flush=True)
+    assert err < TOL_MATBATCH
+
+
 # The prefill workloads at their own shapes: Q4_K 4096x4096 (Q/O) and
 # 4096 -> 14336 (gate/up), Q6_K 14336 -> 4096 (down), at B = 64, 256 and 512,
 # plus ragged B past one 256-token tile and the B = 2048 prefill of the
