@@ -18,6 +18,8 @@ at the full widths; and the decode workload's own 2048-token prompt (the
 B = 2048 matbatch plans, causal attention over 2048 positions, then decode
 steps at positions 2048-2050 whose attention spans the whole prefilled cache)
 runs 4 layers at the full widths against the oracle's batched prefill.
+The 36-layer model also runs from a GGUF file through host pointers and host
+buffers, as the unchanged streamer drives it.
 """
 from __future__ import annotations
 
@@ -115,3 +117,56 @@ def test_qwen3_8b_widths_2048_token_prompt(lib, oracle, torch_mod):
         lib.gncx_hip_weight_forget(None)
         del model
         torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_8b_36_layers_gguf_host_buffers(lib, oracle, torch_mod, tmp_path):
+    """The unchanged streamer's contract at the full model: a 36-layer
+    Qwen3-8B-shaped GGUF file mapped read-only (every weight reaches the
+    library as a host pointer, base + offset, lua/gncx_gguf.lua:223-306), every
+    activation buffer and KV cache from gncx_ram_alloc_colored (host memory,
+    lua/gncx_streamer.lua:461-477), the streamer's own call sequence for an
+    8-token prompt and 2 decode steps, synchronous and with lazy coherence;
+    logits against the oracle's within 1e-3 after the prompt and each step."""
+    import gncx_amd.decode as dec
+
+    torch = torch_mod
+    path = tmp_path / "qwen3_8b.gguf"
+    dec.write_model_gguf(path, dec.QWEN3_8B, seed=2025)
+    print(f"wrote {path.stat().st_size / 1e9:.2f} GB", flush=True)
+    m = dec.load_model_gguf(path)
+    assert m.shape.n_layers == 36 and m.shape.embed == 4096 and m.shape.vocab == dec.QWEN3_8B.vocab
+    rng = np.random.default_rng(14)
+    prompt = [int(t) for t in rng.integers(0, m.shape.vocab, 8)]
+    ref = OracleModel(oracle, m, max_seq=16)
+    for pos, tok in enumerate(prompt[:-1]):
+        ref.step(tok, pos, logits=False)
+        print(f"oracle position {pos}", flush=True)
+    want = [ref.step(prompt[-1], len(prompt) - 1)]
+    toks = []
+    for i in range(2):
+        toks.append(int(np.argmax(want[-1])))
+        want.append(ref.step(toks[-1], len(prompt) + i))
+    print(f"oracle tokens {toks}", flush=True)
+    try:
+        for lazy in (0, 1):
+            lib.gncx_hip_set_host_coherence(lazy)
+            d = dec.Decoder(lib, torch, m, max_seq=16, device="cpu", host="ram")
+            try:
+                got = d.prefill(prompt).numpy().copy()
+                gncx.check(lib)
+                errs = [rel_l2(got, want[0])]
+                for i, tok in enumerate(toks):
+                    got = d.forward_token(tok, len(prompt) + i).numpy().copy()
+                    gncx.check(lib)
+                    errs.append(rel_l2(got, want[i + 1]))
+                print(f"36 layers, GGUF host pointers, host buffers, lazy={lazy}: rel_l2 "
+                      + " ".join(f"{e:.2e}" for e in errs), flush=True)
+                assert all(np.isfinite(errs)) and max(errs) < TOL, errs
+            finally:
+                lib.gncx_hip_set_host_coherence(0)
+                d.close()
+                lib.gncx_hip_kv_forget(None)
+    finally:
+        lib.gncx_hip_weight_forget(None)
+        del m
