@@ -68,6 +68,37 @@ def test_noalloc_step_equals_decode_step(lib, torch_mod):
     gncx.check(lib)
 
 
+def test_noalloc_first_call_on_fresh_model(lib, torch_mod):
+    """The first call of a model and state the library has not seen (its plan
+    is built inside that call) allocates nothing either, and equals the
+    regular step.  A regular step on another model runs first, so every kernel
+    has been launched once (the runtime loads code objects on first use)."""
+    import gncx_amd.decode as dec
+
+    torch = torch_mod
+    warm_shape = dec.Qwen3Shape(n_layers=1, embed=256, n_heads=4, n_kv=2, head_dim=64, ffn=512, vocab=600)
+    w = dec.Decoder(lib, torch, dec.build_model(torch, warm_shape, seed=40), max_seq=16, fused=True, native=True)
+    w._step(1, 0, True)
+    torch.cuda.synchronize()
+    gncx.check(lib)
+    shape = dec.Qwen3Shape(n_layers=3, embed=256, n_heads=8, n_kv=2, head_dim=64, ffn=512, vocab=700)
+    model = dec.build_model(torch, shape, seed=41)
+    a = dec.Decoder(lib, torch, model, max_seq=16, fused=True, native=True)
+    b = dec.Decoder(lib, torch, model, max_seq=16, fused=True, native=True)
+    b._native_structs()
+    torch.cuda.synchronize()
+    free0 = _mem_free()
+    rc = _noalloc(lib, b, 123, 0, 1)
+    assert rc == 0, lib.gncx_hip_last_error().decode()
+    torch.cuda.synchronize()
+    assert _mem_free() == free0
+    a._step(123, 0, True)
+    torch.cuda.synchronize()
+    gncx.check(lib)
+    assert torch.equal(a.logits, b.logits)
+    assert torch.equal(a.token_dev, b.token_dev)
+
+
 def test_noalloc_step_rejects_oversized_scratch(lib, torch_mod):
     """One KV head and 32 query heads at position 32767: the attention split
     plan has 1024 chunks, about 17 MB of partials, more than the fixed array."""
