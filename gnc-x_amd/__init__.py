@@ -126,6 +126,8 @@ SIGNATURES = {
     "gncx_hip_matbatch_multi": (None, [_i32, _vp, _vp, _i32, _fp, _i32, _i32, _vp]),
     "gncx_hip_fetch_token_embeddings": (None, [_i32, _vp, _sz, _vp, _i32, _i32, _i32, _f32, _fp]),
     "gncx_hip_add_rmsnorm": (None, [_fp, _fp, _vp, _sz, _i32, _f32, _fp]),
+    "gncx_hip_add_rmsnorm_rows": (None, [_fp, _fp, _i32, _vp, _sz, _i32, _f32, _fp]),
+    "gncx_hip_swiglu_matbatch": (None, [_vp, _sz, _i32, _fp, _fp, _i32, _i32, _i32, _fp]),
     "gncx_hip_attention_prefill": (
         None,
         [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _sz, _sz, _i32, _f32, _sz, _i32,

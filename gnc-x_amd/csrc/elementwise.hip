@@ -7,6 +7,7 @@
 //                         Q4_0/Q4_K decoders (cpp:1023-1030, 1127-1178)
 #include <hip/hip_runtime.h>
 
+#include "gncx_act.h"
 #include "gncx_device.h"
 #include "gncx_launch.h"
 
@@ -117,7 +118,7 @@ __device__ void encode_row(const float* v, int32_t dim, int32_t lay_k, uint32_t*
 constexpr int kNormThreads = 1024;
 constexpr int kNormRegs = 4;  // float4 per thread held in registers
 
-// ADD: x is the residual stream h (one row), updated in place to h + r
+// ADD: x is the residual stream h (row blockIdx.x), updated in place to h + r
 // before it is normalised -- the fp32 add of the separate vec_add kernel, so
 // the result is the same bit for bit.  ENC: the 4-phase encode of the
 // normalised row follows in the same work-group (one row).
@@ -131,6 +132,10 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
     __shared__ float part[kNormThreads / 64];
     const float* xr = x + static_cast<size_t>(blockIdx.x) * dim;
     float* yr = out + static_cast<size_t>(blockIdx.x) * dim;
+    if (ADD) {  // one row per work-group: its residual row and delta row
+        r += static_cast<size_t>(blockIdx.x) * dim;
+        xo += static_cast<size_t>(blockIdx.x) * dim;
+    }
     const int tid = threadIdx.x;
     float s = 0.0f;
     float4 xv[kNormRegs], gv[kNormRegs];
@@ -219,10 +224,8 @@ __global__ void rope_kernel(float* __restrict q, float* __restrict k, RopeTable 
 
 __global__ void swiglu_kernel(const float* __restrict g, const float* __restrict u, int32_t n,
                               float* __restrict out) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        const float x = g[i];
-        out[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), u[i]);
-    }
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = swiglu_value(g[i], u[i]);
 }
 
 // tanh-approximated GELU of the gate times up, in the reference's order of
@@ -445,6 +448,17 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int3
     const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
     hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(rows), dim3(kNormThreads), 0, stream, x, gamma, dim, eps, out,
                        vec4, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm_rows(float* h, const float* r, const float* gamma, int32_t rows, int32_t dim, float eps,
+                                   float* out, hipStream_t stream) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(r) |
+                         reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(out);
+    const int32_t vec4 = (dim % 4 == 0 && (al & 15u) == 0) ? 1 : 0;
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(rows), dim3(kNormThreads), 0, stream, h, gamma, dim, eps, out, vec4,
+                       r, h);
     return hipGetLastError();
 }
 

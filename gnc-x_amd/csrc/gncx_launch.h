@@ -58,11 +58,13 @@ hipError_t launch_act_quant(const float* x, int32_t rows, int32_t k, int8_t* q, 
 hipError_t launch_dequant(int32_t type, const uint8_t* w, int32_t k, int32_t n, float* out,
                           hipStream_t stream);
 
-// Y[b x n] = Q8(X[b x k]) . W^T  (per-row activation quantisation).
+// Y[b x n] = Q8(X[b x k]) . W^T  (per-row activation quantisation).  With up
+// non-null, X is SwiGLU(x, up) (the values of gncx_swiglu_activation), formed
+// by the quantisation pass (quantised types; BF16 weights: hipErrorNotSupported).
 size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n);
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k,
                            int32_t n, float* y, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream);
+                           hipStream_t stream, const float* up = nullptr);
 // ys[i][b x ns[i]] = Q8(X) . W_i^T for count (1..4) matrices of one type
 // sharing X: the activations are quantised once, and Q4_K matrices whose rows
 // are whole tiles of the summed plan run as one launch.  Each output equals
@@ -141,6 +143,9 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, int32_t rows, int3
                           float* out, hipStream_t stream);
 // h += r, then out = RMSNorm(h) * gamma, one row of dim, in one kernel (the
 // same arithmetic as launch_vec_add followed by launch_rmsnorm).
+// rows contiguous rows: h[r] += d[r], out[r] = RMSNorm(h[r]) (as launch_add_rmsnorm per row)
+hipError_t launch_add_rmsnorm_rows(float* h, const float* r, const float* gamma, int32_t rows, int32_t dim, float eps,
+                                   float* out, hipStream_t stream);
 hipError_t launch_add_rmsnorm(float* h, const float* r, const float* gamma, int32_t dim, float eps, float* out,
                               hipStream_t stream);
 // NEOX RoPE with a host-computed cos/sin table (reference cpp:1797-1862).

@@ -1281,6 +1281,49 @@ GNCX_API void gncx_xfold_universal_matbatch(const uint8_t* mmap_base, size_t wei
     }
 }
 
+// gncx_swiglu_activation of the batch's gate and up rows followed by
+// gncx_xfold_universal_matbatch of the result, with the SwiGLU formed by the
+// matbatch's own activation pass (the prefill's down projection without the
+// activation rows in memory).  The same values as the two calls.
+GNCX_API void gncx_hip_swiglu_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                                       const float* gate_batch, const float* up_batch, int32_t batch_size,
+                                       int32_t in_dim, int32_t out_dim, float* out_batch) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_swiglu_matbatch";
+    bool ok = true;
+    const size_t xn = dim_count(batch_size) * dim_count(in_dim);
+    gate_batch = lazy_ptr(gate_batch, xn, kRd, ok, where);
+    up_batch = lazy_ptr(up_batch, xn, kRd, ok, where);
+    out_batch = lazy_ptr(out_batch, dim_count(batch_size) * dim_count(out_dim), kWr, ok, where);
+    if (!ok) return;
+    if (!gate_batch || !up_batch || !out_batch || !type_supported(ggml_type) || batch_size <= 0 || out_dim <= 0 ||
+        in_dim <= 0 || !ensure_runtime(where))
+        return;
+    const size_t wbytes = row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dim);
+    const uint8_t* w = device_weights(mmap_base + weight_abs_offset, wbytes, where);
+    if (!w) return;
+    const float* g = stage_in(gate_batch, xn, g_rt.aux, where);
+    if (!g) return;
+    const float* u = stage_in(up_batch, xn, g_rt.x, where);
+    if (!u) return;
+    const size_t yn = static_cast<size_t>(batch_size) * out_dim;
+    bool host_out = false;
+    float* y = out_target(out_batch, yn, g_rt.y, host_out, where);
+    if (!y) return;
+    if (!g_rt.ws.ensure(matbatch_workspace_bytes(ggml_type, batch_size, in_dim, out_dim), where)) return;
+    hipError_t e = launch_matbatch(ggml_type, w, g, batch_size, in_dim, out_dim, y, g_rt.ws.p, g_rt.ws.cap,
+                                   g_rt.stream, u);
+    if (e == hipErrorNotSupported) {
+        // BF16 weights take fp32 activations: the SwiGLU rows are formed first
+        if (!g_rt.v.ensure(xn * sizeof(float), where)) return;
+        float* act = g_rt.v.as<float>();
+        if (!check(launch_swiglu(g, u, static_cast<int32_t>(xn), act, g_rt.stream), where)) return;
+        e = launch_matbatch(ggml_type, w, act, batch_size, in_dim, out_dim, y, g_rt.ws.p, g_rt.ws.cap, g_rt.stream);
+    }
+    if (!check(e, where)) return;
+    finish_out(out_batch, y, yn, host_out, where);
+}
+
 // cpp:1694-1707
 GNCX_API void gncx_xfold_q4_0_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, const float* in_batch,
                                        int32_t batch_size, int32_t in_dim, int32_t out_dim, float* out_batch,
@@ -2211,6 +2254,40 @@ GNCX_API void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t
     if (!o) return;
     if (!check(launch_rmsnorm(x, g, rows, dim, eps, o, g_rt.stream), where)) return;
     finish_out(out, o, n, host, where);
+}
+
+// gncx_hip_add_rmsnorm over `rows` contiguous rows of dim: hidden[r] +=
+// delta[r], then out[r] = the RMSNorm of the new hidden[r], one launch; the
+// same values as gncx_hip_vec_add of the rows followed by gncx_hip_rmsnorm_rows.
+GNCX_API void gncx_hip_add_rmsnorm_rows(float* hidden, const float* delta, int32_t rows, const uint8_t* mmap_base,
+                                        size_t norm_weight_offset, int32_t dim, float eps, float* out) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_add_rmsnorm_rows";
+    g_norm_epoch++;
+    if (rows <= 0 || dim <= 0 || !hidden || !delta || !out || !ensure_runtime(where)) return;
+    const size_t n = static_cast<size_t>(rows) * dim;
+    bool ok = true;
+    hidden = lazy_ptr(hidden, n, kRd | kWr, ok, where);
+    delta = lazy_ptr(delta, n, kRd, ok, where);
+    out = lazy_ptr(out, n, kWr, ok, where);
+    if (!ok) return;
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(dim), where));
+    if (!g) return;
+    const float* dd = stage_in(delta, n, g_rt.k, where);
+    if (!dd) return;
+    const bool host_h = !is_device_ptr(hidden);
+    float* hd = hidden;
+    if (host_h) {
+        hd = const_cast<float*>(stage_in(hidden, n, g_rt.q, where));
+        if (!hd) return;
+    }
+    bool host_o = false;
+    float* o = out_target(out, n, g_rt.o, host_o, where);
+    if (!o) return;
+    if (!check(launch_add_rmsnorm_rows(hd, dd, g, rows, dim, eps, o, g_rt.stream), where)) return;
+    if (!finish_out(hidden, hd, n, host_h, where)) return;
+    finish_out(out, o, n, host_o, where);
 }
 
 // ---- fused decode-chain matvecs ------------------------------------------

@@ -31,6 +31,7 @@
 
 #include <algorithm>
 
+#include "gncx_act.h"
 #include "gncx_device.h"
 #include "gncx_launch.h"
 #include "gncx_slots.h"
@@ -104,13 +105,30 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // quantised activations, P = (sum q) * d / s, as an fp16 pair: per token row
 // and 256-value super-block, 8 hi then 8 lo values (the Q4_K kernel's min
 // term, cpp:1177-1178).
-template <int kHiloU>
+// With SW the row is the SwiGLU of two rows, x the gates and up the ups
+// (the values gncx_swiglu_activation writes), formed as they are read.
+template <int kHiloU, bool SW = false>
 __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
                                                             uint2* __restrict xhl, float* __restrict rscale,
-                                                            _Float16* __restrict pq) {
+                                                            _Float16* __restrict pq, const float* __restrict up) {
     __shared__ float red[kThreads / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
+    const float4* xg = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
+    const float4* xu = SW ? reinterpret_cast<const float4*>(up + static_cast<size_t>(row) * k) : nullptr;
+    struct Row {
+        const float4* g;
+        const float4* u;
+        __device__ float4 operator[](int32_t t) const {
+            if constexpr (!SW) {
+                return g[t];
+            } else {
+                const float4 a = g[t], b = u[t];
+                return make_float4(swiglu_value(a.x, b.x), swiglu_value(a.y, b.y), swiglu_value(a.z, b.z),
+                                   swiglu_value(a.w, b.w));
+            }
+        }
+    };
+    const Row xr{xg, xu};
     auto amax4 = [](const float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
     float4 xv[kHiloU];
 #pragma unroll
@@ -169,14 +187,21 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
     for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) emit(xr[t], t);
 }
 
+// up non-null: the rows are SwiGLU(x, up)
 void launch_act_hilo(const float* x, int32_t b, int32_t k, _Float16* xhl, float* rscale, _Float16* pq,
-                     hipStream_t stream) {
-    if (k <= 4 * 4 * kThreads)
-        hipLaunchKernelGGL((act_hilo_kernel<4>), dim3(b), dim3(kThreads), 0, stream, x, k,
-                           reinterpret_cast<uint2*>(xhl), rscale, pq);
-    else
-        hipLaunchKernelGGL((act_hilo_kernel<16>), dim3(b), dim3(kThreads), 0, stream, x, k,
-                           reinterpret_cast<uint2*>(xhl), rscale, pq);
+                     hipStream_t stream, const float* up = nullptr) {
+    uint2* o = reinterpret_cast<uint2*>(xhl);
+    if (up) {
+        if (k <= 4 * 4 * kThreads)
+            hipLaunchKernelGGL((act_hilo_kernel<4, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale, pq, up);
+        else
+            hipLaunchKernelGGL((act_hilo_kernel<16, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale, pq,
+                               up);
+    } else if (k <= 4 * 4 * kThreads) {
+        hipLaunchKernelGGL((act_hilo_kernel<4>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale, pq, nullptr);
+    } else {
+        hipLaunchKernelGGL((act_hilo_kernel<16>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale, pq, nullptr);
+    }
 }
 
 // Weights e0 .. e0 + 15 (e0 a multiple of 16) of one row: raw block bytes
@@ -1176,8 +1201,8 @@ hipError_t launch_mfma_t(const uint8_t* w, const _Float16* xhl, const float* rsc
 
 template <int TYPE>
 hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
-                       float* rscale, float* part, hipStream_t stream) {
-    launch_act_hilo(x, b, k, xhl, rscale, nullptr, stream);
+                       float* rscale, float* part, hipStream_t stream, const float* up) {
+    launch_act_hilo(x, b, k, xhl, rscale, nullptr, stream, up);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const MfmaPlan p = mfma_plan(b, k, n);
@@ -1281,8 +1306,8 @@ hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, c
 }
 
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
-                      _Float16* pq, float* rscale, float* part, hipStream_t stream) {
-    launch_act_hilo(x, b, k, xhl, rscale, pq, stream);
+                      _Float16* pq, float* rscale, float* part, hipStream_t stream, const float* up) {
+    launch_act_hilo(x, b, k, xhl, rscale, pq, stream, up);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
@@ -1329,7 +1354,7 @@ size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n) {
 }
 
 hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n,
-                           float* y, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                           float* y, void* workspace, size_t workspace_bytes, hipStream_t stream, const float* up) {
     if (b <= 0 || n <= 0) return hipSuccess;
     if (k <= 0 || k > (1 << 20) || b > 65535) return hipErrorInvalidValue;  // keeps buffer offsets in int32
     if (type != kBF16 && (k % 32) != 0) return hipErrorInvalidValue;
@@ -1349,11 +1374,11 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     float* part = reinterpret_cast<float*>(ws + xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
     switch (type) {
-    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
-    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xhl, rscale, part, stream);
-    case kQ4_K: return launch_q4k(w, x, b, k, n, y, xhl, pq, rscale, part, stream);
-    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream);
-    case kBF16: return launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
+    case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
+    case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
+    case kQ4_K: return launch_q4k(w, x, b, k, n, y, xhl, pq, rscale, part, stream, up);
+    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
+    case kBF16: return up ? hipErrorNotSupported : launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }
 }

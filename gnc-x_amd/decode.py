@@ -574,13 +574,19 @@ class Decoder:
 
     def _prefill_fused(self, B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf):
         """prefill's layers with the extensions: every token's RMSNorm in one
-        launch, and the per-token prologue + attention loop as one causal
-        batch (gncx_hip_attention_prefill)."""
+        launch (with the residual add before it), the per-token prologue +
+        attention loop as one causal batch (gncx_hip_attention_prefill), and
+        the SwiGLU inside the down projection's matbatch."""
         s, L, m = self.s, self.lib, self.m
         for l in range(s.n_layers):
             p = f"blk.{l}"
-            L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"), s.embed, s.eps,
-                                    bn.data_ptr())
+            # the previous layer's residual add goes into this layer's first norm
+            if l == 0:
+                L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"), s.embed, s.eps,
+                                        bn.data_ptr())
+            else:
+                L.gncx_hip_add_rmsnorm_rows(bh.data_ptr(), bp.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"),
+                                            s.embed, s.eps, bn.data_ptr())
             self._matbatch_multi(p, "qkv", bn.data_ptr(), B, s.embed, (s.q_dim, s.kv_dim, s.kv_dim),
                                  (bq, bk, bv))
             L.gncx_hip_attention_prefill(bq.data_ptr(), bk.data_ptr(), bv.data_ptr(), self.kc[l].data_ptr(),
@@ -588,13 +594,13 @@ class Decoder:
                                          m.base, m.off(f"{p}.attn_q_norm.weight"), m.off(f"{p}.attn_k_norm.weight"),
                                          1, s.eps, 0, 0, s.rope_base, ba.data_ptr())
             self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
-            self._add(bh, bp)
-            L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"), s.embed, s.eps,
-                                    bn.data_ptr())
+            L.gncx_hip_add_rmsnorm_rows(bh.data_ptr(), bp.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"),
+                                        s.embed, s.eps, bn.data_ptr())
             self._matbatch_multi(p, ("ffn_gate", "ffn_up"), bn.data_ptr(), B, s.embed, (s.ffn, s.ffn), (bg, bu))
-            L.gncx_swiglu_activation(bg.data_ptr(), bu.data_ptr(), B * s.ffn, bf.data_ptr())
-            self._matbatch(f"{p}.ffn_down.weight", bf.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
-            self._add(bh, bp)
+            # SwiGLU formed by the down projection's activation pass
+            L.gncx_hip_swiglu_matbatch(m.base, m.off(f"{p}.ffn_down.weight"), s.layer_type, bg.data_ptr(),
+                                       bu.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
+        self._add(bh, bp)
         self.hidden.copy_(bh[B - 1])
         return self._lm_head()
 

@@ -321,6 +321,21 @@ void gncx_hip_rmsnorm_rows(const float* in, int32_t rows, const uint8_t* mmap_ba
  * kernel; the same values as gncx_hip_vec_add followed by that call. */
 void gncx_hip_add_rmsnorm(float* hidden, const float* delta, const uint8_t* mmap_base, size_t norm_weight_offset,
                           int32_t dim, float eps, float* out_normed_fp32);
+/* gncx_hip_add_rmsnorm over `rows` contiguous rows of dim in one launch: the
+ * prefill's residual add followed by the next RMSNorm of every batch row
+ * (lua/gncx_streamer.lua:1122 then :1126-1132, and :1153 then the next
+ * layer's :1059-1065); the same values as gncx_hip_vec_add of the rows
+ * followed by gncx_hip_rmsnorm_rows. */
+void gncx_hip_add_rmsnorm_rows(float* hidden, const float* delta, int32_t rows, const uint8_t* mmap_base,
+                               size_t norm_weight_offset, int32_t dim, float eps, float* out);
+/* out_batch = gncx_xfold_universal_matbatch of W over the rows
+ * gncx_swiglu_activation(gate_batch, up_batch) would write, with the SwiGLU
+ * formed inside the matbatch's activation pass (the prefill's down
+ * projection, lua/gncx_streamer.lua:1138-1142); the same values as the two
+ * calls.  Inputs of batch_size x in_dim, output batch_size x out_dim. */
+void gncx_hip_swiglu_matbatch(const uint8_t* mmap_base, size_t weight_abs_offset, int32_t ggml_type,
+                              const float* gate_batch, const float* up_batch, int32_t batch_size, int32_t in_dim,
+                              int32_t out_dim, float* out_batch);
 
 /* The decode chain's neighbours fused into a matvec launch, for callers whose
  * activations are device memory (weights may be host or device memory, as

@@ -408,6 +408,23 @@ def test_rmsnorm_rows_equals_per_row_calls(lib, rows, dim):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("rows,dim", [(5, 4096), (3, 4098), (2, 20000), (64, 256)])
+def test_add_rmsnorm_rows_equals_add_then_rows(lib, rows, dim):
+    """gncx_hip_add_rmsnorm_rows == gncx_hip_vec_add over the rows followed by
+    gncx_hip_rmsnorm_rows, bit for bit, in host memory and in place."""
+    rng = np.random.default_rng(rows + dim)
+    h = (rng.standard_normal((rows, dim)) * 2).astype(np.float32)
+    d = rng.standard_normal((rows, dim)).astype(np.float32)
+    g = synth.make_norm_gamma(dim, 12)
+    h1, want = h.copy(), np.zeros_like(h)
+    lib.gncx_hip_vec_add(ptr(h1), ptr(d), rows * dim)
+    lib.gncx_hip_rmsnorm_rows(ptr(h1), rows, ptr(g), 0, dim, 1e-6, ptr(want))
+    h2, got = h.copy(), np.zeros_like(h)
+    lib.gncx_hip_add_rmsnorm_rows(ptr(h2), ptr(d), rows, ptr(g), 0, dim, 1e-6, ptr(got))
+    gncx.check(lib)
+    assert np.array_equal(h2, h1) and np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("n", [1, 7, 4096, 4097, 151936])
 def test_argmax_first_of_equal_maxima(lib, n):
     """gncx_hip_argmax: torch.argmax's pick (the first of equal maxima), NaN

@@ -294,6 +294,29 @@ def test_matbatch_q6k_large_scales(lib, oracle, mode, k, n, b):
     assert err < TOL_MATBATCH
 
 
+# gncx_hip_swiglu_matbatch: the SwiGLU formed in the activation pass, bit for
+# bit the values of gncx_swiglu_activation followed by matbatch; K past the
+# quantiser's registers (20480) and BF16 weights (the rows formed first).
+@pytest.mark.parametrize("t,k,n,b", [(Q4_K, 4096, 512, 64), (Q4_K, 12288, 256, 300), (Q4_K, 20480, 128, 7),
+                                     (Q6_K, 2048, 300, 200), (Q8_0, 1024, 96, 33), (BF16, 512, 64, 5)])
+def test_swiglu_matbatch_equals_two_calls(lib, t, k, n, b):
+    w = synth.make_weights(t, n, k, seed=9000 + t + k)
+    rng = np.random.default_rng(9100 + b + k)
+    gate = (rng.standard_normal((b, k)) * 2).astype(np.float32)
+    up = rng.standard_normal((b, k)).astype(np.float32)
+    act = np.zeros((b, k), np.float32)
+    lib.gncx_swiglu_activation(ptr(gate), ptr(up), b * k, ptr(act))
+    want = np.full((b, n), np.nan, np.float32)
+    lib.gncx_xfold_universal_matbatch(ptr(w), 0, t, ptr(act), b, k, n, ptr(want), None)
+    got = np.full((b, n), np.nan, np.float32)
+    try:
+        lib.gncx_hip_swiglu_matbatch(ptr(w), 0, t, ptr(gate), ptr(up), b, k, n, ptr(got))
+        gncx.check(lib)
+    finally:
+        lib.gncx_hip_weight_forget(ptr(w))
+    assert np.array_equal(got, want)
+
+
 # The prefill workloads at their own shapes: Q4_K 4096x4096 (Q/O) and
 # 4096 -> 14336 (gate/up), Q6_K 14336 -> 4096 (down), at B = 64, 256 and 512,
 # plus ragged B past one 256-token tile and the B = 2048 prefill of the
