@@ -67,47 +67,68 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_long_kernel(float* __restri
 // bit-exact.  qscale[0] receives the quant scale and qscale[1] (as a
 // uint32) the cancellation count sum_d min(#positive, #negative) over the
 // digits d (cpp:882-887).  red: kNormThreads / 64 floats of LDS.
+// One element of the encode: the token, and the counter of its (sign, digit)
+// pair (0-9: val >= 0, 10-19: val < 0) for the cancellation count.
+struct EncScale {
+    int64_t r_k;
+    float to_int, inv_rk, half_rk;
+};
+template <class I>
+__device__ __forceinline__ uint32_t encode_value(float v, const EncScale& e, uint32_t& ctr) {
+#pragma clang fp contract(off)
+    const I val = static_cast<I>(rintf(__fmul_rn(v, e.to_int)));
+    const I av = val >= 0 ? val : -val;
+    int32_t d = static_cast<int32_t>(__fmul_rn(__fadd_rn(static_cast<float>(av), e.half_rk), e.inv_rk));
+    if (d > 9) d = 9;
+    const I anchor = static_cast<I>(d) * static_cast<I>(e.r_k);
+    const I res = val - (val >= 0 ? anchor : -anchor);
+    const uint32_t ares = static_cast<uint32_t>(static_cast<uint16_t>(res >= 0 ? res : -res));
+    const uint32_t phase = (val >= 0 ? 2u : 0u) | (res >= 0 ? 1u : 0u);
+    ctr = static_cast<uint32_t>(d) + (val >= 0 ? 0u : 10u);
+    return phase | (static_cast<uint32_t>(d) << 8) | (ares << 16);
+}
+// Up to k = 8 every integer of the encode (|val| <= 9 R_k < 10^9, the residual
+// below 2 x 10^9) fits 32 bits, and the 32-bit steps give the 64-bit results.
+constexpr int32_t kEnc32MaxK = 8;
+
+// the scale of the layer's range from the largest |v| m (qscale[0] = m / 9 R_k)
+__device__ __forceinline__ EncScale encode_scale(float m, int32_t lay_k, float* __restrict qscale) {
+#pragma clang fp contract(off)
+    EncScale e;
+    e.r_k = 1;
+    for (int i = 0; i < lay_k; ++i) e.r_k = e.r_k * 10 + 1;
+    const float target = static_cast<float>(9 * e.r_k);
+    e.to_int = __fdiv_rn(target, m);
+    if (threadIdx.x == 0) *qscale = __fdiv_rn(m, target);
+    e.inv_rk = __fdiv_rn(1.0f, static_cast<float>(e.r_k));
+    e.half_rk = static_cast<float>(e.r_k >> 1);
+    return e;
+}
+
 __device__ void encode_row(const float* v, int32_t dim, int32_t lay_k, uint32_t* __restrict tokens,
                            float* __restrict qscale, float* red) {
-    __shared__ uint32_t signs[2][10];
-    if (threadIdx.x < 20) signs[threadIdx.x / 10][threadIdx.x % 10] = 0;
+    __shared__ uint32_t signs[20];
+    if (threadIdx.x < 20) signs[threadIdx.x] = 0;
     float m = 1e-9f;
     for (int32_t i = threadIdx.x; i < dim; i += blockDim.x) {
         const float a = fabsf(v[i]);
         m = a > m ? a : m;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float t = __shfl_xor(m, o, 64);
-        m = t > m ? t : m;
-    }
+    m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = red[0];
     for (int w = 1; w < static_cast<int>(blockDim.x / 64); ++w) m = red[w] > m ? red[w] : m;
-    int64_t r_k = 1;
-    for (int i = 0; i < lay_k; ++i) r_k = r_k * 10 + 1;
-    const float target = static_cast<float>(9 * r_k);
-    const float to_int = __fdiv_rn(target, m);
-    if (threadIdx.x == 0) *qscale = __fdiv_rn(m, target);
-    const float inv_rk = __fdiv_rn(1.0f, static_cast<float>(r_k));
-    const float half_rk = static_cast<float>(r_k >> 1);
+    const EncScale e = encode_scale(m, lay_k, qscale);
     for (int32_t i = threadIdx.x; i < dim; i += blockDim.x) {
-        const int64_t val = static_cast<int64_t>(rintf(__fmul_rn(v[i], to_int)));
-        const int64_t av = val >= 0 ? val : -val;
-        int32_t d = static_cast<int32_t>(__fmul_rn(__fadd_rn(static_cast<float>(av), half_rk), inv_rk));
-        if (d > 9) d = 9;
-        const int64_t anchor = static_cast<int64_t>(d) * r_k;
-        const int64_t res = val - (val >= 0 ? anchor : -anchor);
-        const uint32_t ares = static_cast<uint32_t>(static_cast<uint16_t>(res >= 0 ? res : -res));
-        const uint32_t phase = (val >= 0 ? 2u : 0u) | (res >= 0 ? 1u : 0u);
-        tokens[i] = phase | (static_cast<uint32_t>(d) << 8) | (ares << 16);
-        __hip_atomic_fetch_add(&signs[val >= 0 ? 0 : 1][d], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t ctr;
+        tokens[i] = lay_k <= kEnc32MaxK ? encode_value<int32_t>(v[i], e, ctr) : encode_value<int64_t>(v[i], e, ctr);
+        __hip_atomic_fetch_add(&signs[ctr], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t c = 0;
-        for (int d = 0; d < 10; ++d) c += signs[0][d] < signs[1][d] ? signs[0][d] : signs[1][d];
+        for (int d = 0; d < 10; ++d) c += signs[d] < signs[10 + d] ? signs[d] : signs[10 + d];
         reinterpret_cast<uint32_t*>(qscale)[1] = c;
     }
 }
@@ -117,6 +138,78 @@ __device__ void encode_row(const float* v, int32_t dim, int32_t lay_k, uint32_t*
 // squares is a fp32 tree over the work-group, y = (x * inv) * gamma.
 constexpr int kNormThreads = 1024;
 constexpr int kNormRegs = 4;  // float4 per thread held in registers
+
+// The encode of a row whose normalised values a work-group of kNormThreads
+// holds in registers (y[j]: float4 t = threadIdx.x + kNormThreads j, t < n4):
+// no second pass over memory, tokens stored as uint4 (16-byte aligned), and
+// the (sign, digit) counts formed per wave with ballots instead of LDS
+// atomics on 20 addresses.  Max, tokens and counts are those of encode_row
+// (a max and integer counts do not depend on the order).
+__device__ void encode_regs(const float4 (&y)[kNormRegs], int32_t n4, int32_t lay_k, uint32_t* __restrict tokens,
+                            float* __restrict qscale) {
+    __shared__ float red[kNormThreads / 64];
+    __shared__ uint32_t cnt[kNormThreads / 64][20];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float m = 1e-9f;
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+        if (tid + kNormThreads * j < n4) {
+            const float a0 = fabsf(y[j].x), a1 = fabsf(y[j].y), a2 = fabsf(y[j].z), a3 = fabsf(y[j].w);
+            m = a0 > m ? a0 : m;
+            m = a1 > m ? a1 : m;
+            m = a2 > m ? a2 : m;
+            m = a3 > m ? a3 : m;
+        }
+    }
+    m = wave_max(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < kNormThreads / 64; ++i) m = red[i] > m ? red[i] : m;
+    const EncScale e = encode_scale(m, lay_k, qscale);
+    uint4* t4 = reinterpret_cast<uint4*>(tokens);
+    const bool small = lay_k <= kEnc32MaxK;
+    uint32_t n[20] = {};
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+        if (kNormThreads * j >= n4) break;  // no thread holds float4 j
+        const int32_t t = tid + kNormThreads * j;
+        uint32_t ctr[4] = {20u, 20u, 20u, 20u};  // 20: counted nowhere
+        if (t < n4) {
+            uint4 tk;
+            const float* yj = &y[j].x;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                (&tk.x)[q] = small ? encode_value<int32_t>(yj[q], e, ctr[q]) : encode_value<int64_t>(yj[q], e, ctr[q]);
+            t4[t] = tk;
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < 20; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) n[c] += static_cast<uint32_t>(__popcll(__ballot(ctr[q] == c)));
+    }
+    if (lane == 0)
+#pragma unroll
+        for (int c = 0; c < 20; ++c) cnt[w][c] = n[c];
+    __syncthreads();
+    if (w == 0) {
+        // lane d < 10 sums digit d's two counts over the waves; the ten
+        // minima meet in one wave sum (integers below 2^24: exact in fp32)
+        float mn = 0.0f;
+        if (lane < 10) {
+            uint32_t pos = 0, neg = 0;
+#pragma unroll
+            for (int i = 0; i < kNormThreads / 64; ++i) {
+                pos += cnt[i][lane];
+                neg += cnt[i][10 + lane];
+            }
+            mn = static_cast<float>(pos < neg ? pos : neg);
+        }
+        mn = wave_sum(mn);
+        if (lane == 0) reinterpret_cast<uint32_t*>(qscale)[1] = static_cast<uint32_t>(mn);
+    }
+}
 
 // ADD: x is the residual stream h (row blockIdx.x), updated in place to h + r
 // before it is normalised -- the fp32 add of the separate vec_add kernel, so
@@ -187,12 +280,16 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
     for (int w = 0; w < kNormThreads / 64; ++w) tot += part[w];
     const float inv = 1.0f / sqrtf(tot / static_cast<float>(dim) + eps);
     float4* y4 = reinterpret_cast<float4*>(yr);
+    float4 yv[kNormRegs];
 #pragma unroll
     for (int j = 0; j < kNormRegs; ++j) {
         const int32_t t = tid + kNormThreads * j;
-        if (t < n4)
-            y4[t] = make_float4(xv[j].x * inv * gv[j].x, xv[j].y * inv * gv[j].y, xv[j].z * inv * gv[j].z,
+        yv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (t < n4) {
+            yv[j] = make_float4(xv[j].x * inv * gv[j].x, xv[j].y * inv * gv[j].y, xv[j].z * inv * gv[j].z,
                                 xv[j].w * inv * gv[j].w);
+            y4[t] = yv[j];
+        }
     }
     for (int32_t t = tid + kNormThreads * kNormRegs; t < n4; t += kNormThreads) {
         const float4 a = x4[t], b = g4[t];
@@ -200,6 +297,12 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
     }
     for (int32_t i = 4 * n4 + tid; i < dim; i += kNormThreads) yr[i] = xr[i] * inv * g[i];
     if constexpr (ENC) {
+        // the whole row in registers and 16-byte token stores: encode from
+        // the registers; otherwise from the row just stored
+        if (4 * n4 == dim && n4 <= kNormThreads * kNormRegs && (reinterpret_cast<uintptr_t>(tokens) & 15u) == 0) {
+            encode_regs(yv, n4, lay_k, tokens, qscale);
+            return;
+        }
         __threadfence_block();
         __syncthreads();
         encode_row(yr, dim, lay_k, tokens, qscale, part);

@@ -72,6 +72,17 @@ enum KeepPending { kKeepNone = 0, kKeepGemv = 1, kKeepPrologue = 2 };
 thread_local int t_keep = kKeepNone;
 void queue_readbacks();
 bool flush_pending(const char* where, int keep = kKeepNone);
+// Page-locked host memory that the current call's kernels read in place (a
+// lazy host buffer's pinned copy, read once by a call that waits for its
+// kernels); stage_in passes these through.  Cleared when the call releases
+// the lock.
+std::array<const void*, 4> g_direct{};
+int g_ndirect = 0;
+bool is_direct(const void* p) {
+    for (int i = 0; i < g_ndirect; ++i)
+        if (g_direct[i] == p) return true;
+    return false;
+}
 struct CallLock {
     std::mutex m;
     void lock() {
@@ -81,6 +92,7 @@ struct CallLock {
     }
     void unlock() {
         queue_readbacks();
+        g_ndirect = 0;
         t_in_call = false;
         m.unlock();
     }
@@ -338,7 +350,7 @@ bool d2h(void* host, const void* dev, size_t bytes, const char* where) {
 // Input vector: device pointers pass through, host data is staged into buf.
 const float* stage_in(const float* p, size_t count, DevBuf& buf, const char* where) {
     if (!p) return nullptr;
-    if (is_device_ptr(p)) return p;
+    if (is_direct(p) || is_device_ptr(p)) return p;
     if (!buf.ensure(count * sizeof(float), where)) return nullptr;
     if (!h2d(buf.p, p, count * sizeof(float), where)) return nullptr;
     return buf.as<float>();
@@ -1004,7 +1016,11 @@ bool device_only_lazy(const void* p) {
 // making that copy current (read) and taking ownership for the device
 // (write).  Any other pointer comes back unchanged.  A range that leaves its
 // buffer makes the buffer host-resident and is used as host memory.
-constexpr int kRd = 1, kWr = 2;
+// kRdPinned: a read by a call that waits for its kernels before it returns;
+// a host-owned buffer the host rewrites after every call is then read by the
+// kernels from a page-locked copy in place (no upload into the device copy,
+// which stays stale while the host owns the buffer).
+constexpr int kRd = 1, kWr = 2, kRdPinned = 4;
 template <class T>
 T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
     if (!p || !ok || g_lazy != 1) return p;
@@ -1035,6 +1051,17 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
     // a sync-return buffer that the call overwrites whole is not uploaded
     // first (its next copy home replaces the pages anyway)
     const bool whole_output = access == kWr && b->sync_return && a == lo && bytes == b->bytes;
+    if ((access & kRdPinned) && !(access & kWr) && b->home == Home::kHost && b->keep_rw &&
+        bytes <= kPinnedMax && g_ndirect < static_cast<int>(g_direct.size())) {
+        PinnedSlot* sl = pinned_slot(bytes, where);
+        if (!sl) {
+            ok = false;
+            return nullptr;
+        }
+        std::memcpy(sl->p, p, bytes);
+        g_direct[g_ndirect++] = sl->p;
+        return static_cast<T*>(sl->p);
+    }
     if (b->home == Home::kHost && !whole_output) {
         // uploaded for writes too: a call that writes nothing keeps the data
         if (!upload(*b, where)) {
@@ -1846,7 +1873,9 @@ GNCX_API void gncx_rmsnorm_and_encode_4phase(const float* input_hidden, const ui
     g_norm_epoch++;
     if (dim <= 0 || !ensure_runtime(where)) return;
     bool ok = true;
-    input_hidden = lazy_ptr(input_hidden, dim_count(dim), kRd, ok, where);
+    // with tokens the call waits before it returns: the kernel may read a
+    // host-owned hidden vector from a page-locked copy
+    input_hidden = lazy_ptr(input_hidden, dim_count(dim), out_tokens ? kRd | kRdPinned : kRd, ok, where);
     out_normed_fp32 = lazy_ptr(out_normed_fp32, dim_count(dim), kWr, ok, where);
     if (!ok) return;
     const float* g = reinterpret_cast<const float*>(

@@ -309,6 +309,43 @@ def test_rmsnorm_encode_tokens_bitexact(lib, golden, lk):
     assert rel_l2(out, golden["rms_y"]) < 1e-6
 
 
+def _cancellations(tok):
+    """sum over digits d of min(#tokens with value >= 0, #tokens below 0)."""
+    d, pos = (tok >> 8) & 0xFF, (tok >> 1) & 1
+    return sum(min(int(np.sum((d == i) & (pos == 1))), int(np.sum((d == i) & (pos == 0)))) for i in range(10))
+
+
+@pytest.mark.parametrize("dim,lk", [(4096, 0), (4096, 3), (12288, 2), (16384, 1), (4098, 2), (20000, 0), (100, 9)])
+def test_rmsnorm_encode_paths_and_cancellations(lib, oracle, dim, lk):
+    """Both encode paths -- the row held in registers (dim a multiple of 4 up
+    to 16384) and the second pass over the stored row (other dims) -- give
+    the oracle's tokens and scale for the normed vector, and the cancellation
+    count the device forms reaches the telemetry of a matvec on those tokens
+    (cpp:882-887, cpp:1464-1470)."""
+    rng = np.random.default_rng(dim + lk)
+    x = rng.standard_normal(dim).astype(np.float32)
+    x[rng.integers(0, dim, 5)] *= 40.0
+    g = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    out = np.zeros_like(x)
+    tok = (gncx.GNCXCompactToken * dim)()
+    qs = np.zeros(1, np.float32)
+    lib.gncx_rmsnorm_and_encode_4phase(ptr(x), ptr(g), 0, dim, 1e-6, lk, ptr(out), C.addressof(tok), ptr(qs))
+    gncx.check(lib)
+    got = np.frombuffer(bytes(tok), dtype=np.uint32).copy()
+    want, want_qs = oracle.encode(out, lk)
+    assert np.array_equal(got, want)
+    assert qs[0] == want_qs
+    # the encode's own tokens: the count is the one formed with them
+    k, n = 256, 8
+    w = synth.make_weights(12, n, k, seed=dim)
+    xk = synth.make_activations(1, k, seed=lk)
+    y = np.zeros(n, np.float32)
+    tel = gncx.GNCXTelemetryStats()
+    lib.gncx_xfold_universal_matvec(ptr(w), 0, 12, ptr(xk), C.addressof(tok), k, n, ptr(y), C.addressof(tel))
+    gncx.check(lib)
+    assert tel.zero_origin_cancellations == _cancellations(want) > 0
+
+
 PREFILL_CASES = [
     # (H, KV, hd, pos0, B, sw): fresh prompt, a cache prefix, a sliding window,
     # MQA (32 heads on one KV head), one head per KV head, and a head_dim the
