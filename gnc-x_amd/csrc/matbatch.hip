@@ -107,10 +107,15 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // term, cpp:1177-1178).
 // With SW the row is the SwiGLU of two rows, x the gates and up the ups
 // (the values gncx_swiglu_activation writes), formed as they are read.
-template <int kHiloU, bool SW = false>
+// With QX (the Q4_K one-product kernel) the quantised values q themselves
+// go out instead of the pairs, as fp16 (integers of at most 127, exact):
+// xhl holds 4 of them per task, row-major [B x K], and dxs (set) each
+// 32-block's d / s as fp32 [B x K / 32]; P as above.
+template <int kHiloU, bool SW = false, bool QX = false>
 __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
                                                             uint2* __restrict xhl, float* __restrict rscale,
-                                                            _Float16* __restrict pq, const float* __restrict up) {
+                                                            _Float16* __restrict pq, const float* __restrict up,
+                                                            float* __restrict dxs = nullptr) {
     __shared__ float red[kThreads / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
     const float4* xg = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
@@ -155,13 +160,22 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
         int q0, q1, q2, q3;
         float d;
         quantize_values(v, q0, q1, q2, q3, d);
-        uint2 hi, lo;
-        split2((static_cast<float>(q0) * d) * inv, (static_cast<float>(q1) * d) * inv, hi.x, lo.x);
-        split2((static_cast<float>(q2) * d) * inv, (static_cast<float>(q3) * d) * inv, hi.y, lo.y);
-        // task t is elements 4t .. 4t + 3: chunk t / 2 of 8, half t % 2
-        uint2* c = out + 4 * (t >> 1) + (t & 1);
-        c[0] = hi;
-        c[2] = lo;
+        if constexpr (QX) {
+            auto h2 = [](int a, int b) {
+                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+            };
+            xhl[static_cast<size_t>(row) * tasks + t] = make_uint2(h2(q0, q1), h2(q2, q3));
+            if ((t & 7) == 0) dxs[static_cast<size_t>(row) * (k / 32) + (t >> 3)] = d * inv;
+        } else {
+            uint2 hi, lo;
+            split2((static_cast<float>(q0) * d) * inv, (static_cast<float>(q1) * d) * inv, hi.x, lo.x);
+            split2((static_cast<float>(q2) * d) * inv, (static_cast<float>(q3) * d) * inv, hi.y, lo.y);
+            // task t is elements 4t .. 4t + 3: chunk t / 2 of 8, half t % 2
+            uint2* c = out + 4 * (t >> 1) + (t & 1);
+            c[0] = hi;
+            c[2] = lo;
+        }
         if (pq) {
             // the 8 lanes of block t / 8: quad sums, then lane i adds lane 7 - i
             const int s4 = quad_sum(q0 + q1 + q2 + q3);
@@ -185,6 +199,27 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
         if (t < tasks) emit(xv[u], t);
     }
     for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) emit(xr[t], t);
+}
+
+// the one-product Q4_K kernel's activations: q as fp16 [B x K], then the
+// blocks' d / s [B x K / 32] (dxs), the P pairs and the row scales
+void launch_act_q(const float* x, int32_t b, int32_t k, _Float16* xq, float* dxs, float* rscale, _Float16* pq,
+                  hipStream_t stream, const float* up) {
+    uint2* o = reinterpret_cast<uint2*>(xq);
+    if (up) {
+        if (k <= 4 * 4 * kThreads)
+            hipLaunchKernelGGL((act_hilo_kernel<4, true, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
+                               pq, up, dxs);
+        else
+            hipLaunchKernelGGL((act_hilo_kernel<16, true, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
+                               pq, up, dxs);
+    } else if (k <= 4 * 4 * kThreads) {
+        hipLaunchKernelGGL((act_hilo_kernel<4, false, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale, pq,
+                           nullptr, dxs);
+    } else {
+        hipLaunchKernelGGL((act_hilo_kernel<16, false, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
+                           pq, nullptr, dxs);
+    }
 }
 
 // up non-null: the rows are SwiGLU(x, up)
@@ -1090,6 +1125,325 @@ __global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1)
         }
 }
 
+// ---- Q4_K, one product per K slice ------------------------------------------
+//
+// The weights sc q and the quantised activations q are both small integers,
+// exact in fp16, so one v_mfma_f32_32x32x16_f16 per K slice gives a
+// 32-block's integer dot, sum (sc q) q (at most 32 x 945 x 127 < 2^24, exact
+// in fp32 whatever the order of the additions).  The block's activation
+// scale d_x / s then multiplies it on the VALU, S += (d_x / s) blk, and S
+// folds into the output once per super-block as acc += d S, with the min
+// term as in matbatch_q4k_kernel.  Against the two-product kernel this is
+// half the matrix-core work and half the activation bytes in LDS, for 16
+// fp32 fmas per accumulator tile and block.  The weights are the MFMA's A
+// operand (accumulator rows) and the tokens its B operand (columns), so a
+// lane's accumulator column is one token and its block scale one value; d
+// and dmin vary along the lane's 16 registers (4 x 4 consecutive rows).
+// Loads, ring stages and staging are those of matbatch_q4k_kernel, the
+// activation ring holding q alone, and the super-block loads bringing the
+// blocks' scales with P.
+template <int WM, int WN, int MW, int NW>
+__global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
+    MbMats mats, size_t rbytes, const _Float16* __restrict xq, const float* __restrict dxs,
+    const _Float16* __restrict pq, const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk,
+    float* __restrict part) {
+    constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
+    int bx, by;
+    xcd_tiles(mats.xcd_a, bx, by);
+    const uint8_t* __restrict w = mats.w[0];
+    float* __restrict y = mats.y[0];
+    int32_t n = mats.n[0], tile0 = 0, npre = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxMbMats; ++i) {
+        if (mats.count > i && bx >= mats.tile0[i]) {
+            w = mats.w[i];
+            y = mats.y[i];
+            n = mats.n[i];
+            tile0 = mats.tile0[i];
+            npre = mats.npre[i];
+        }
+    }
+    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
+    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage
+    static_assert(XBLK % WAVES == 0, "the same number of activation loads for every wave");
+    static_assert(2 * BN <= THREADS && BM <= THREADS, "one weight piece and one P row per thread at most");
+    __shared__ __align__(16) _Float16 xs0[BM * 32], xs1[BM * 32], xs2[BM * 32], xs3[BM * 32];
+    static_assert(kXStages == 4, "four ring arrays");
+    auto xstage = [&](int stage) -> _Float16* { return stage == 0 ? xs0 : stage == 1 ? xs1 : stage == 2 ? xs2 : xs3; };
+    __shared__ __align__(16) _Float16 ws[2][BN * 32];    // [step parity] sc q
+    __shared__ __align__(16) _Float16 sp[2][2][BM * 8];  // [super-block parity][hi, lo] P of 8 blocks
+    __shared__ __align__(16) float sdx[2][BM * 8];       // [super-block parity] d_x / s of 8 blocks
+    __shared__ __align__(16) _Float16 smn[2][BN * 8];    // [super-block parity] mins of 8 blocks
+    __shared__ __align__(16) float sdm[2][2][BN];        // [super-block parity][d, dmin]
+    __shared__ __align__(16) float srs[THREADS];         // the tile's token scales (entries from BM on unused)
+    static_assert((BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
+                      (2 * BM * 16) % (THREADS * 4) == 0 && (BM * 8 * 4) % (THREADS * 4) == 0,
+                  "the same number of weight, header, P and scale loads for every wave");
+    __shared__ __align__(16) uint8_t wq0[BN * 32], wq1[BN * 32], wq2[BN * 32], wq3[BN * 32];
+    __shared__ __align__(16) uint8_t whd[2][BN * 16];
+    auto wstage = [&](int stage) -> uint8_t* { return stage == 0 ? wq0 : stage == 1 ? wq1 : stage == 2 ? wq2 : wq3; };
+    constexpr int kXLoads = XBLK / WAVES;
+    constexpr int kWLoads = BN * 32 / (THREADS * 16);
+    constexpr int kDLoads = BM * 8 / THREADS;
+    constexpr int kHLoads = BN * 16 / (THREADS * 4) + 2 * BM * 16 / (THREADS * 4) + kDLoads;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv % MW, wn = wv / MW;
+    const int li = lane & 31, lh = lane >> 5;
+    const int32_t t0 = by * BM, n0 = (bx - tile0) * BN;
+    const int32_t kb = blockIdx.z * kchunk;
+    const int32_t ke = min(k, kb + kchunk);
+    const int32_t nsb = (ke - kb) / 256;
+    const int32_t sbs_row = k / 256;
+
+    const int32_t rows_here = min(BM, b - t0);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(xq + static_cast<size_t>(t0) * k), static_cast<short>(0),
+        rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * sbs_row * 16), static_cast<short>(0),
+        rows_here * sbs_row * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(dxs + static_cast<size_t>(t0) * (k / 32)), static_cast<short>(0),
+        rows_here * (k / 32) * static_cast<int32_t>(sizeof(float)), 0x00020000);
+    const int wrow = tid >> 1, whalf = tid & 1;
+    const int32_t wrows_here = min(BN, n - n0);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
+        wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
+
+    floatx16 acc[WM][WN], S[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = S[i][j][r] = 0.0f;
+
+    // q of the step at k0 into ring stage `stage`: load q is block q (token
+    // rows 16 q .. + 16), 64 lanes x 16 B, lane L at segment position L % 4
+    // of row L / 4 (logical segment (L % 4) ^ ((row / 4) % 4)); past the
+    // range: zeros
+    auto dma_x = [&](int stage, int32_t k0) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int blk = i * WAVES + wv;
+            const int row = 16 * blk + (lane >> 2);
+            const int lseg = (lane & 3) ^ ((row >> 2) & 3);
+            const int32_t off = k0 < ke ? (row * k + k0 + 8 * lseg) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)(xstage(stage) + blk * 16 * 32), 16, off, 0, 0, 0);
+        }
+    };
+    auto dma_w = [&](int stage, int32_t k0) {
+        const int32_t kk = k0 < ke ? k0 : 0;
+        const int32_t koff = (kk / 256) * 144 + 16 + 32 * ((kk % 256) / 64);
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i) {
+            const int piece = (i * WAVES + wv) * 64 + lane;
+            const int row = piece >> 1;
+            const int32_t off =
+                k0 < ke && row < wrows_here ? row * static_cast<int32_t>(rbytes) + koff + 16 * (piece & 1) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(wstage(stage) + (i * WAVES + wv) * 1024), 16, off,
+                                                     0, 0, 0);
+        }
+    };
+    // headers, P pairs and block scales of the super-block at s0 into parity par
+    auto dma_hp = [&](int par, int32_t s0) {
+        const bool in = s0 < ke;
+        constexpr int HL = BN * 16 / (THREADS * 4), PH = BM * 16 / (64 * 4), PL = 2 * PH / WAVES;
+#pragma unroll
+        for (int i = 0; i < HL; ++i) {
+            const int dw = (i * WAVES + wv) * 64 + lane;
+            const int row = dw >> 2;
+            const int32_t off =
+                in && row < wrows_here ? row * static_cast<int32_t>(rbytes) + (s0 / 256) * 144 + 4 * (dw & 3) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(&whd[par][(i * WAVES + wv) * 256]), 4, off, 0, 0,
+                                                     0);
+        }
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int q = i * WAVES + wv, h = q / PH, qq = q % PH;
+            const int dw = qq * 64 + lane;
+            const int row = dw >> 2;
+            const int32_t off = in && row < rows_here
+                                    ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) * static_cast<int32_t>(sizeof(_Float16)) +
+                                          4 * (dw & 3)
+                                    : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][qq * 128]), 4, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kDLoads; ++i) {
+            const int dw = (i * WAVES + wv) * 64 + lane;  // token row dw / 8, block dw % 8
+            const int row = dw >> 3;
+            const int32_t off =
+                in && row < rows_here ? (row * (k / 32) + s0 / 32 + (dw & 7)) * static_cast<int32_t>(sizeof(float))
+                                      : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_ptr)(&sdx[par][(i * WAVES + wv) * 64]), 4, off, 0, 0,
+                                                     0);
+        }
+    };
+    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int hpar) {
+        if (tid < 2 * BN) {
+            const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
+            const u32x4 hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
+            const u32x4 qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
+            int sc, mn;
+            k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
+            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
+            const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
+            const _Float16 off = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
+            const half2 s2 = {scf, scf}, m2 = {off, off};
+            uint32_t o[8];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t x = (qw[d] >> sh) & 0x0f0f0f0fu;
+                const half2 p0 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
+                const half2 p1 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
+                o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p0, s2, m2));
+                o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p1, s2, m2));
+            }
+            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
+            if (sb_first && whalf == 0) {
+                sdm[hpar][0][wrow] = half_bits_to_float(hh.x & 0xffffu);
+                sdm[hpar][1][wrow] = half_bits_to_float(hh.x >> 16);
+                uint32_t m2[4];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj += 2) {
+                    int s0, m0, s1, m1;
+                    k4_scale_min(jj, hh.y, hh.z, hh.w, s0, m0);
+                    k4_scale_min(jj + 1, hh.y, hh.z, hh.w, s1, m1);
+                    const _Float16 h0 = static_cast<_Float16>(static_cast<float>(m0));
+                    const _Float16 h1 = static_cast<_Float16>(static_cast<float>(m1));
+                    m2[jj / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
+                                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+                }
+                *reinterpret_cast<uint4*>(&smn[hpar][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
+            }
+        }
+    };
+    // block st of super-block parity sbp: its integer dots, one tile at a
+    // time (both K slices' operands first), scaled into S
+    auto compute = [&](int stage, int buf, int sbp, int st) {
+        const _Float16* xs = xstage(stage);
+        half8 xa[2][WM], wa[2][WN];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                xa[kk][i] = *reinterpret_cast<const half8*>(&xs[swz(wm * 32 * WM + 32 * i + li, 2 * kk + lh)]);
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                wa[kk][j] = *reinterpret_cast<const half8*>(&ws[buf][swz(wn * 32 * WN + 32 * j + li, 2 * kk + lh)]);
+        }
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const float dv = sdx[sbp][(wm * 32 * WM + 32 * i + li) * 8 + st];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const floatx16 zero = {};
+                floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[0][j], xa[0][i], zero, 0, 0, 0);
+                blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[1][j], xa[1][i], blk, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) S[i][j][r] = fmaf(dv, blk[r], S[i][j][r]);
+            }
+            // the tiles of one token tile at a time: hoisting every tile's
+            // products ahead of the fmas would hold all their results at once
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // acc += d S - dmin (m . P) for super-block parity sbp; S restarts at 0
+    auto fold = [&](int sbp) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int rb = wn * 32 * WN + 32 * j + 4 * lh;  // rows rb + 8 g + 0..3 in registers 4 g + 0..3
+            const half4 mn = *reinterpret_cast<const half4*>(&smn[sbp][(wn * 32 * WN + 32 * j + li) * 8 + 4 * lh]);
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+                const int t = wm * 32 * WM + 32 * i + li;
+                const half4 ph = *reinterpret_cast<const half4*>(&sp[sbp][0][t * 8 + 4 * lh]);
+                const half4 pl = *reinterpret_cast<const half4*>(&sp[sbp][1][t * 8 + 4 * lh]);
+                const floatx16 zero = {};
+                floatx16 M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn, ph, zero, 0, 0, 0);
+                M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn, pl, M, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 d4 = *reinterpret_cast<const float4*>(&sdm[sbp][0][rb + 8 * g]);
+                    const float4 m4 = *reinterpret_cast<const float4*>(&sdm[sbp][1][rb + 8 * g]);
+                    const float dq[4] = {d4.x, d4.y, d4.z, d4.w}, mq[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int r = 4 * g + q;
+                        acc[i][j][r] = fmaf(S[i][j][r], dq[q], acc[i][j][r]);
+                        acc[i][j][r] = fmaf(M[r], -mq[q], acc[i][j][r]);
+                        S[i][j][r] = 0.0f;
+                    }
+                }
+            }
+        }
+    };
+
+    {
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(rscale + t0), static_cast<short>(0), rows_here * static_cast<int32_t>(sizeof(float)),
+            0x00020000);
+        const int32_t off = tid < rows_here ? tid * static_cast<int32_t>(sizeof(float)) : kMfOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (lds_ptr)&srs[64 * wv], 4, off, 0, 0, 0);
+    }
+    dma_hp(0, kb);
+    dma_x(0, kb);
+    dma_w(0, kb);
+    dma_x(1, kb + 32);
+    dma_w(1, kb + 32);
+    dma_x(2, kb + 64);
+    dma_w(2, kb + 64);
+    step_barrier<2 * (kXLoads + kWLoads)>();
+    lstore(0, 0, kb, true, 0);
+    step_barrier<kXLoads + kWLoads>();
+    for (int32_t sb = 0; sb < nsb; ++sb) {
+        const int32_t s0 = kb + sb * 256;
+        const int sbp = sb & 1;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const int32_t k0 = s0 + 32 * st;
+            const int buf = st & 1;
+            auto issue_loads = [&]() {
+                dma_x((st + 3) & 3, k0 + 96);
+                dma_w((st + 3) & 3, k0 + 96);
+                if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
+            };
+            const int wset = (st + 1) & 3;
+            const int hpar = st == 7 ? (sbp ^ 1) : sbp;
+            if (wv < WAVES / 2) {
+                issue_loads();
+                compute(st & 3, buf, sbp, st);
+                if (st == 7) fold(sbp);
+                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
+            } else {
+                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
+                issue_loads();
+                compute(st & 3, buf, sbp, st);
+                if (st == 7) fold(sbp);
+            }
+            if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
+            else step_barrier<kXLoads + kWLoads>();
+        }
+    }
+    // lane: token t0 + wm 32 WM + 32 i + li, rows 8 g + 4 lh + 0..3 of tile j in registers 4 g + 0..3
+    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const int32_t tl = wm * 32 * WM + 32 * i + li, t = t0 + tl;
+        const float rs = srs[tl];
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int32_t mm = n0 + wn * 32 * WN + 32 * j + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rs;
+            }
+    }
+}
+
 // y = sum over the split K ranges, added in range order (deterministic);
 // range z's partials are the flat block [z count, (z + 1) count).  The
 // first kRedU ranges are loaded together before the adds (a loop of
@@ -1282,9 +1636,62 @@ hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq
     return hipGetLastError();
 }
 
+// Long batches with whole K per work-group (B >= 1024, no split) run the
+// one-product kernel; their activations are q as fp16 in xhl's first B K
+// halves and the blocks' d / s after them (the pairs' space holds both).
+// Measured full calls, two-product against one-product kernel (us): B = 2048
+// 4096 x 4096 183-185 / 176, 4096 -> 12288 515-518 / 497, 12288 -> 4096
+// 534-537 / 473-477, 4096 -> 24576 969-973 / 938-942; but with K split
+// (4096 x 4096 at B = 256 / 512, 4096 -> 14336 at B = 256) 45 / 67 / 100
+// against 57 / 77 / 108, and 4096 -> 14336 at B = 512 (whole K) 165-167
+// against 168: the 16 fmas per tile and block cost more than the halved
+// matrix-core work saves unless the halved activation bytes dominate.
+#ifndef GNCX_Q4K_ONE
+#define GNCX_Q4K_ONE 1
+#endif
+bool q4k_one(const Q4kPlan& p, int32_t b) { return GNCX_Q4K_ONE && p.cfg == 0 && p.splits == 1 && b >= 1024; }
+float* q4k_dxs(_Float16* xhl, int32_t b, int32_t k) { return reinterpret_cast<float*>(xhl + static_cast<size_t>(b) * k); }
+
+void launch_q4k_act(const float* x, int32_t b, int32_t k, _Float16* xhl, float* rscale, _Float16* pq,
+                    const Q4kPlan& p, hipStream_t stream, const float* up) {
+    if (q4k_one(p, b)) launch_act_q(x, b, k, xhl, q4k_dxs(xhl, b, k), rscale, pq, stream, up);
+    else launch_act_hilo(x, b, k, xhl, rscale, pq, stream, up);
+}
+
+template <int WM, int WN, int MW, int NW>
+hipError_t launch_q4k1_t(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
+                         const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part,
+                         hipStream_t stream) {
+    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
+    const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
+    const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
+    MbMats mx = m;
+    mx.xcd_a = 0;
+#if GNCX_MB_XCD
+    // as launch_q4k_t, the activation tile now q alone (2 bytes per value)
+    const double wt = static_cast<double>(BN) * (p.kchunk / 256) * 144.0;
+    const double at = static_cast<double>(BM) * p.kchunk * 2.0;
+    const int gx = static_cast<int>(grid.x), gy = static_cast<int>(grid.y);
+    double best = gx * wt + 8.0 * gy * at;
+    if ((gx * gy) % 8 == 0) {
+        for (int a = 1; a < 8; a *= 2) {
+            if (gx % a != 0 || gy % (8 / a) != 0) continue;
+            const double cost = 8.0 * gx * wt / a + 8.0 * gy * at / (8 / a);
+            if (cost < best) {
+                best = cost;
+                mx.xcd_a = a;
+            }
+        }
+    }
+#endif
+    hipLaunchKernelGGL((matbatch_q4k1_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, mx,
+                       row_bytes(kQ4_K, k), xq, dxs, pq, rscale, b, k, p.kchunk, part);
+    return hipGetLastError();
+}
+
 // The product of plan p over the matrices of m (w, y, n and count set), then
 // with split K the reduce of the partials into each y
-hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
+hipError_t launch_q4k_mats(MbMats& m, _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
                            int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
     const int32_t bn = kQ4kTileRows;
     int32_t t = 0, rows = 0;
@@ -1299,15 +1706,18 @@ hipError_t launch_q4k_mats(MbMats& m, const _Float16* xhl, const _Float16* pq, c
     }
     m.ntot = rows;
     r.count = m.count;
-    const hipError_t e = p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
-                                    : launch_q4k_t<1, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
+    const hipError_t e =
+        q4k_one(p, b) ? launch_q4k1_t<2, 2, 2, 4>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
+        : p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
+                     : launch_q4k_t<1, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     return launch_reduce(part, p.splits, r, stream);
 }
 
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                       _Float16* pq, float* rscale, float* part, hipStream_t stream, const float* up) {
-    launch_act_hilo(x, b, k, xhl, rscale, pq, stream, up);
+    const Q4kPlan p = q4k_plan(b, k, n);
+    launch_q4k_act(x, b, k, xhl, rscale, pq, p, stream, up);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
@@ -1315,7 +1725,7 @@ hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, in
     m.y[0] = y;
     m.n[0] = n;
     m.count = 1;
-    return launch_q4k_mats(m, xhl, pq, rscale, b, k, q4k_plan(b, k, n), part, stream);
+    return launch_q4k_mats(m, xhl, pq, rscale, b, k, p, part, stream);
 }
 
 template <int TYPE>
@@ -1333,8 +1743,9 @@ hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int3
 
 }  // namespace
 
-// fp16 pairs of the quantised activations [B x K x 2], their row scales [B],
-// then the split-K partials [splits x B x N]
+// fp16 pairs of the quantised activations [B x K x 2] (or, for the
+// one-product Q4_K kernel, q [B x K] and the blocks' d / s [B x K / 32]),
+// their row scales [B], then the split-K partials [splits x B x N]
 static size_t xh_bytes(int32_t b, int32_t k) {
     return (static_cast<size_t>(b) * k * 2 * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
 }
@@ -1443,7 +1854,7 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
     float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
     float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
-    launch_act_hilo(x, b, k, xhl, rscale, pq, stream);
+    launch_q4k_act(x, b, k, xhl, rscale, pq, p, stream, nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};

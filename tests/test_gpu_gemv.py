@@ -254,6 +254,8 @@ MATBATCH_CASES = [
     (Q8_0, 1024, 640, 128), (Q6_K, 14336, 512, 77),
     # Q4_K at small B: one super-block, K of 3, 5 and 48 super-blocks, ragged B and N
     (Q4_K, 256, 100, 17), (Q4_K, 768, 50, 64), (Q4_K, 1280, 33, 2), (Q4_K, 12288, 200, 48),
+    # Q4_K one-product kernel (B >= 1024, whole K): ragged B and N, one and 8 super-blocks
+    (Q4_K, 2048, 1000, 1100), (Q4_K, 256, 520, 1030),
 ]
 
 
@@ -296,9 +298,11 @@ def test_matbatch_q6k_large_scales(lib, oracle, mode, k, n, b):
 
 # gncx_hip_swiglu_matbatch: the SwiGLU formed in the activation pass, bit for
 # bit the values of gncx_swiglu_activation followed by matbatch; K past the
-# quantiser's registers (20480) and BF16 weights (the rows formed first).
+# quantiser's registers (20480), the one-product Q4_K kernel (B = 1024) and
+# BF16 weights (the rows formed first).
 @pytest.mark.parametrize("t,k,n,b", [(Q4_K, 4096, 512, 64), (Q4_K, 12288, 256, 300), (Q4_K, 20480, 128, 7),
-                                     (Q6_K, 2048, 300, 200), (Q8_0, 1024, 96, 33), (BF16, 512, 64, 5)])
+                                     (Q4_K, 12288, 256, 1024), (Q6_K, 2048, 300, 200), (Q8_0, 1024, 96, 33),
+                                     (BF16, 512, 64, 5)])
 def test_swiglu_matbatch_equals_two_calls(lib, t, k, n, b):
     w = synth.make_weights(t, n, k, seed=9000 + t + k)
     rng = np.random.default_rng(9100 + b + k)
