@@ -1059,6 +1059,9 @@ T* lazy_ptr(T* p, size_t count, int access, bool& ok, const char* where) {
             return nullptr;
         }
         std::memcpy(sl->p, p, bytes);
+        // the call's kernel reads the slot: a reuse before the next wait for
+        // the stream waits for it first (as for a slot holding device output)
+        sl->deferred = true;
         g_direct[g_ndirect++] = sl->p;
         return static_cast<T*>(sl->p);
     }

@@ -707,9 +707,6 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 // are loaded during its predecessor, and its d, dmin and mins are staged by
 // the threads that dequantise its first block.
 constexpr int kXStages = 4;
-// s_waitcnt vmcnt(n) with no lgkm / exp wait (gfx9 encoding: vmcnt in bits
-// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // vmcnt(N) and lgkmcnt(0), then a work-group barrier with no memory fence.
 // __syncthreads() also waits for the direct-to-LDS loads issued for later
