@@ -20,6 +20,9 @@
 // LDS before the scan, with the same arithmetic as the stand-alone kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "gncx_device.h"
 #include "gncx_launch.h"
 
@@ -642,6 +645,13 @@ struct PrefillParams {
     const float* rope;    // [B][2][HD / 2] cos then sin rows, or null
     int32_t pos0, batch, n_heads, n_kv, sw, norm_qk;
     float scale, eps;
+    // key-split plan (null: one work-group per block, longest first):
+    // plan[4 y .. 4 y + 3] = (block, slot, first key, last key) of grid row
+    // y, slot -1 for a whole block, else the partial slot of that part of a
+    // split block, whose (unnormalised o, max, sum) go to part_o / part_ml
+    const int32_t* plan;
+    float* part_o;   // [slots][n_kv][128 rows][HD]
+    float* part_ml;  // [slots][n_kv][128 rows][2]
 };
 
 template <int HD>
@@ -730,11 +740,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_prefill_kernel(PrefillParams
     const int li = lane & 31, g = lane >> 5;
     const int G = p.n_heads / p.n_kv, TQ = kPfRows / G;
     const int hk = blockIdx.x;
-    const int blk = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);  // longest key ranges first
+    int blk = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);  // longest key ranges first
+    int slot = -1;
+    if (p.plan) {
+        const int4 it = reinterpret_cast<const int4*>(p.plan)[blockIdx.y];
+        blk = it.x;
+        slot = it.y;
+    }
     const int q0 = blk * TQ;
     const int nq = min(TQ, p.batch - q0);
-    const int hi_last = p.pos0 + q0 + nq - 1;
-    const int lo_first = p.sw > 0 ? max(0, p.pos0 + q0 - p.sw + 1) : 0;
+    const int hi_block = p.pos0 + q0 + nq - 1;
+    const int lo_block = p.sw > 0 ? max(0, p.pos0 + q0 - p.sw + 1) : 0;
+    // this work-group's keys: the block's range, or one half of it
+    const int lo_first = p.plan ? reinterpret_cast<const int4*>(p.plan)[blockIdx.y].z : lo_block;
+    const int hi_last = p.plan ? reinterpret_cast<const int4*>(p.plan)[blockIdx.y].w : hi_block;
     const size_t kv_dim = static_cast<size_t>(p.n_kv) * HD;
     const size_t q_dim = static_cast<size_t>(p.n_heads) * HD;
     const float* kbase = p.k_cache + static_cast<size_t>(hk) * HD;
@@ -897,6 +916,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_prefill_kernel(PrefillParams
         }
         __syncthreads();  // every wave is done with this sub-chunk's K / V fragments
     }
+    if (slot >= 0) {
+        // half of a split block: the unnormalised O and the row's (max, sum)
+        // for attn_prefill_merge_kernel
+        const size_t base = (static_cast<size_t>(slot) * p.n_kv + hk) * kPfRows;
+        if (g == 0)
+            reinterpret_cast<float2*>(p.part_ml)[base + qrow] = make_float2(m_run, l_run);
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int row = 32 * wv + 8 * a4 + 4 * g + b;
+#pragma unroll
+                for (int n = 0; n < HD / 32; ++n) p.part_o[(base + row) * HD + 32 * n + li] = o[n][4 * a4 + b];
+            }
+        return;
+    }
     // out = O / (l + 1e-12), the rows' sums through LDS like the factors
     if (g == 0) rowf[wv][li] = 1.0f / (l_run + 1e-12f);
     __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -915,6 +950,57 @@ __global__ __launch_bounds__(kThreads, 2) void attn_prefill_kernel(PrefillParams
                 for (int n = 0; n < HD / 32; ++n) dst[32 * n + li] = o[n][4 * a4 + b] * fr[b];
             }
         }
+    }
+}
+
+// The parts of split block j = blockIdx.y (plan_split[3 j ..]: block, first
+// partial slot, parts) for KV head blockIdx.x, a slice of its rows per
+// blockIdx.z:
+// out = sum_i o_i 2^(m_i - M) / (sum_i l_i 2^(m_i - M) + 1e-12), M = max_i m_i
+// (the maxima are in base-2 units, the scores having been scaled by log2 e);
+// a part with no key in a row's window has m = -1e30 and weight 0.
+constexpr int kPfMaxParts = 8;
+__global__ __launch_bounds__(kThreads) void attn_prefill_merge_kernel(PrefillParams p, const int32_t* plan_split) {
+    constexpr int HD = 128;
+    const int hk = blockIdx.x, j = blockIdx.y;
+    const int G = p.n_heads / p.n_kv, TQ = kPfRows / G;
+    const int blk = plan_split[3 * j], slot0 = plan_split[3 * j + 1], parts = plan_split[3 * j + 2];
+    const int q0 = blk * TQ, nq = min(TQ, p.batch - q0);
+    const size_t q_dim = static_cast<size_t>(p.n_heads) * HD;
+    // one float4 of one row per thread (grid z: kPfRows HD / 4 / kThreads
+    // slices), every part's loads issued together
+    {
+        const int it = static_cast<int>(blockIdx.z) * kThreads + static_cast<int>(threadIdx.x);
+        const int row = it / (HD / 4), d4 = it % (HD / 4);
+        const int t = row / G, h = row % G;
+        if (t >= nq) return;
+        float2 ml[kPfMaxParts];
+        float M = -1e30f;
+#pragma unroll
+        for (int i = 0; i < kPfMaxParts; ++i) {
+            if (i < parts) {
+                ml[i] = reinterpret_cast<const float2*>(p.part_ml)[(static_cast<size_t>(slot0 + i) * p.n_kv + hk) * kPfRows + row];
+                M = fmaxf(M, ml[i].x);
+            }
+        }
+        float l = 0.0f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < kPfMaxParts; ++i) {
+            if (i < parts) {
+                const float a = __builtin_amdgcn_exp2f(ml[i].x - M);
+                const float4 o = reinterpret_cast<const float4*>(
+                    p.part_o + ((static_cast<size_t>(slot0 + i) * p.n_kv + hk) * kPfRows + row) * HD)[d4];
+                l += ml[i].y * a;
+                acc.x += o.x * a;
+                acc.y += o.y * a;
+                acc.z += o.z * a;
+                acc.w += o.w * a;
+            }
+        }
+        const float inv = 1.0f / (l + 1e-12f);
+        reinterpret_cast<float4*>(p.out + static_cast<size_t>(q0 + t) * q_dim + (static_cast<size_t>(hk) * G + h) * HD)[d4] =
+            make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
     }
 }
 
@@ -1193,6 +1279,88 @@ bool attention_prefill_supported(int32_t n_heads, int32_t n_kv_heads, int32_t he
     return sizeof(float) * static_cast<size_t>(n_heads + n_kv_heads) * head_dim <= kLdsBudget;
 }
 
+size_t attention_prefill_part_floats(int32_t part_slots, int32_t n_kv_heads) {
+    return static_cast<size_t>(part_slots) * n_kv_heads * kPfRows * (128 + 2);
+}
+constexpr size_t kPfPartMax = size_t{128} << 20;
+
+// The key-split plan of a prefill call.  A block's work is its number of
+// 32-key sub-chunks, and two work-groups share a CU, so the kernel's time is
+// about the larger of its longest work-group and the total work over the
+// resident work-groups.  Blocks longer than a third of the longest (and than
+// 8 sub-chunks) are cut into parts of their key range of at most that
+// length, each a work-group, whose partial results attn_prefill_merge_kernel
+// combines; grid rows are ordered longest first.  (2048 tokens, 32/8 heads:
+// kernel + merge 200 us per layer unsplit; halves 163 + 12, thirds best,
+// quarters 149 + 21: the partials' traffic grows with the parts.)  Up to 8
+// sub-chunks in the longest block there is nothing worth a second launch: no
+// plan.
+// Table: n_items rows of (block, slot, first key, last key), slot -1 for a
+// whole block, else its part's index in the partial buffers; then per split
+// block (block, first slot, parts).
+bool attention_prefill_plan(const PrefillArgs& a, std::vector<int32_t>& tab, int32_t& n_items, int32_t& n_split) {
+    n_items = n_split = 0;
+    tab.clear();
+    if (a.batch <= 0 || a.n_kv_heads <= 0 || a.n_heads % a.n_kv_heads != 0) return false;
+    const int32_t G = a.n_heads / a.n_kv_heads, TQ = kPfRows / G;
+    const int32_t nblk = (a.batch + TQ - 1) / TQ;
+    struct Item {
+        int32_t blk, slot, ks, ke;
+    };
+    std::vector<Item> items;
+    std::vector<int32_t> split;
+    int32_t maxsub = 0;
+    auto range = [&](int32_t blk, int32_t& lo, int32_t& hi) {
+        const int32_t q0 = blk * TQ, nq = std::min(TQ, a.batch - q0);
+        hi = a.pos0 + q0 + nq - 1;
+        lo = a.sliding_window > 0 ? std::max(0, a.pos0 + q0 - a.sliding_window + 1) : 0;
+    };
+    for (int32_t blk = 0; blk < nblk; ++blk) {
+        int32_t lo, hi;
+        range(blk, lo, hi);
+        maxsub = std::max(maxsub, (hi - lo) / kPfKeys + 1);
+    }
+    if (maxsub <= 8) return false;
+    const int32_t cut = std::max<int32_t>(8, (maxsub + 2) / 3);
+    int32_t slots = 0;
+    for (int32_t blk = nblk - 1; blk >= 0; --blk) {
+        int32_t lo, hi;
+        range(blk, lo, hi);
+        const int32_t nsub = (hi - lo) / kPfKeys + 1;
+        if (nsub > cut) {
+            const int32_t parts = (nsub + cut - 1) / cut;  // at most 3 (cut >= maxsub / 3)
+            if (parts > kPfMaxParts) return false;
+            split.insert(split.end(), {blk, slots, parts});
+            for (int32_t q = 0; q < parts; ++q) {
+                const int32_t s0 = nsub * q / parts, s1 = nsub * (q + 1) / parts;  // sub-chunks [s0, s1)
+                items.push_back({blk, slots + q, lo + kPfKeys * s0, q + 1 == parts ? hi : lo + kPfKeys * s1 - 1});
+            }
+            slots += parts;
+        } else {
+            items.push_back({blk, -1, lo, hi});
+        }
+    }
+    // the partial buffers stay within kPfPartMax (a long prompt's plan would
+    // need them per 128 rows of every part: it runs unsplit instead)
+    if (attention_prefill_part_floats(slots, a.n_kv_heads) * sizeof(float) > kPfPartMax) return false;
+    std::stable_sort(items.begin(), items.end(),
+                     [](const Item& x, const Item& y) { return x.ke - x.ks > y.ke - y.ks; });
+    if (items.size() > 65535 || split.size() / 3 > 65535) return false;
+    for (const Item& it : items) tab.insert(tab.end(), {it.blk, it.slot, it.ks, it.ke});
+    tab.insert(tab.end(), split.begin(), split.end());
+    n_items = static_cast<int32_t>(items.size());
+    n_split = static_cast<int32_t>(split.size() / 3);
+    return true;
+}
+
+// partial slots of a plan: the parts of its split blocks (the last table
+// entries: block, first slot, parts)
+int32_t attention_prefill_part_slots(const std::vector<int32_t>& tab, int32_t n_items, int32_t n_split) {
+    if (n_split <= 0) return 0;
+    const size_t last = 4 * static_cast<size_t>(n_items) + 3 * static_cast<size_t>(n_split - 1);
+    return tab[last + 1] + tab[last + 2];
+}
+
 hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream) {
     if (a.batch <= 0) return hipSuccess;
     if (!attention_prefill_supported(a.n_heads, a.n_kv_heads, a.head_dim) || a.pos0 < 0) return hipErrorInvalidValue;
@@ -1225,7 +1393,18 @@ hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(attn_prefill_prologue_kernel<128>, dim3(a.batch), dim3(kThreads), lds, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_kv_heads, nblk), dim3(kThreads), 0, stream, p);
+    if (!a.plan || a.n_items <= 0) {
+        hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_kv_heads, nblk), dim3(kThreads), 0, stream, p);
+        return hipGetLastError();
+    }
+    p.plan = a.plan;
+    p.part_o = a.part;
+    p.part_ml = a.part + static_cast<size_t>(a.part_slots) * a.n_kv_heads * kPfRows * 128;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(a.n_kv_heads, a.n_items), dim3(kThreads), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.n_split == 0) return e;
+    hipLaunchKernelGGL(attn_prefill_merge_kernel, dim3(a.n_kv_heads, a.n_split, kPfRows * 128 / 4 / kThreads),
+                       dim3(kThreads), 0, stream, p, a.plan + 4 * a.n_items);
     return hipGetLastError();
 }
 

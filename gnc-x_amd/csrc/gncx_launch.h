@@ -9,6 +9,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "gncx_formats.h"
 
@@ -128,9 +129,19 @@ struct PrefillArgs {
     const float* k_gamma;
     float eps;
     const float* rope;  // device [batch][head_dim]: cos[head_dim / 2] then sin, or null
+    // key-split plan from attention_prefill_plan (device copy of its table),
+    // or null; part: attention_prefill_part_floats(part_slots, n_kv_heads) floats
+    const int32_t* plan = nullptr;
+    int32_t n_items = 0, n_split = 0, part_slots = 0;
+    float* part = nullptr;
 };
 // shapes the batched kernels take: head_dim 128, n_heads / n_kv_heads dividing 32
 bool attention_prefill_supported(int32_t n_heads, int32_t n_kv_heads, int32_t head_dim);
+// host: the key-split plan of a call (n_items rows of 4 ints, then n_split
+// block indices); false when the call takes no plan
+bool attention_prefill_plan(const PrefillArgs& a, std::vector<int32_t>& tab, int32_t& n_items, int32_t& n_split);
+int32_t attention_prefill_part_slots(const std::vector<int32_t>& tab, int32_t n_items, int32_t n_split);
+size_t attention_prefill_part_floats(int32_t part_slots, int32_t n_kv_heads);
 hipError_t launch_attention_prefill(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs& a, void* workspace, size_t workspace_bytes,
                             hipStream_t stream);

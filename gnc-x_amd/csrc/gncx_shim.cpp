@@ -2135,6 +2135,54 @@ const float* rope_rows(int32_t pos0, int32_t batch, int32_t head_dim, float base
     if (factors) std::memcpy(r.fac.data(), factors, sizeof(float) * half);
     return r.buf.as<float>();
 }
+
+// The key-split plan of the last prefill shape (attention_prefill_plan),
+// uploaded once per shape with its partial-result buffer; the layers of one
+// prefill share both, their launches being in stream order.
+struct PrefillPlan {
+    int32_t pos0 = -1, batch = 0, sw = 0, n_heads = 0, n_kv = 0;
+    int32_t n_items = 0, n_split = 0, part_slots = 0;
+    bool some = false;
+    DevBuf tab, part;
+} g_pf_plan;
+
+bool prefill_plan(PrefillArgs& a, const char* where) {
+    PrefillPlan& pl = g_pf_plan;
+    if (!(pl.pos0 == a.pos0 && pl.batch == a.batch && pl.sw == a.sliding_window && pl.n_heads == a.n_heads &&
+          pl.n_kv == a.n_kv_heads)) {
+        std::vector<int32_t> tab;
+        int32_t ni = 0, ns = 0;
+        const bool some = attention_prefill_plan(a, tab, ni, ns);
+        const int32_t slots = some ? attention_prefill_part_slots(tab, ni, ns) : 0;
+        pl.pos0 = -1;
+        if (some) {
+            // a launch queued with the previous plan may still read it
+            if (!check(hipStreamSynchronize(g_rt.stream), where)) return false;
+            if (!pl.tab.ensure(sizeof(int32_t) * tab.size(), where) ||
+                !pl.part.ensure(sizeof(float) * attention_prefill_part_floats(slots, a.n_kv_heads), where))
+                return false;
+            if (!check(hipMemcpy(pl.tab.p, tab.data(), sizeof(int32_t) * tab.size(), hipMemcpyHostToDevice), where))
+                return false;
+        }
+        pl.some = some;
+        pl.n_items = ni;
+        pl.n_split = ns;
+        pl.part_slots = slots;
+        pl.pos0 = a.pos0;
+        pl.batch = a.batch;
+        pl.sw = a.sliding_window;
+        pl.n_heads = a.n_heads;
+        pl.n_kv = a.n_kv_heads;
+    }
+    if (pl.some) {
+        a.plan = pl.tab.as<int32_t>();
+        a.n_items = pl.n_items;
+        a.n_split = pl.n_split;
+        a.part_slots = pl.part_slots;
+        a.part = pl.part.as<float>();
+    }
+    return true;
+}
 }  // namespace
 
 GNCX_API void gncx_hip_attention_step_fused(float* q_vec, float* k_vec, const float* v_vec, float* k_cache_layer,
@@ -2252,6 +2300,7 @@ GNCX_API void gncx_hip_attention_prefill(float* q_batch, float* k_batch, const f
     a.k_gamma = kg;
     a.eps = norm_eps;
     a.rope = rope;
+    if (!prefill_plan(a, where)) return;
     if (!check(launch_attention_prefill(a, g_rt.stream), where)) return;
     // host copies: the caches' new rows (the reference writes them in the call), q / k (prologue results), out
     const size_t row0 = static_cast<size_t>(pos0) * kn;

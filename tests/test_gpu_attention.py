@@ -356,6 +356,15 @@ PREFILL_CASES = [
     (32, 1, 128, 3, 20, 0),
     (16, 16, 128, 0, 40, 0),
     (8, 2, 64, 2, 10, 0),
+    # key ranges of more than 8 sub-chunks of 32 keys: the longer blocks are
+    # cut into up to three work-groups whose parts a merge kernel combines --
+    # a fresh prompt, a cache prefix (every block cut), a sliding window, MQA,
+    # and one head per KV head (128-token blocks)
+    (32, 8, 128, 0, 600, 0),
+    (32, 8, 128, 500, 100, 0),
+    (32, 8, 128, 0, 700, 300),
+    (32, 1, 128, 0, 400, 0),
+    (16, 16, 128, 3, 520, 0),
 ]
 
 
@@ -400,35 +409,42 @@ def test_attention_prefill_equals_fused_steps(lib, H, KV, hd, pos0, B, sw):
     assert max(errs) < 1e-5
 
 
-def test_attention_prefill_device_buffers(lib, oracle):
+@pytest.mark.parametrize("pos0,B,sw", [(10, 64, 0), (300, 200, 0), (0, 600, 200)])
+def test_attention_prefill_device_buffers(lib, oracle, pos0, B, sw):
     """Device-resident buffers (used in place), against the oracle's
-    per-token prologue + attention sequence."""
+    per-token prologue followed by its batched causal attention.  The second
+    and third shapes run the key-split plan (a cache prefix; a sliding window
+    over a fresh prompt), so the parts' merge is checked against the oracle
+    directly."""
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
-    H, KV, hd, pos0, B = 32, 8, 128, 10, 64
-    kc, vc, q, k, v, norms = _prefill_inputs(H, KV, hd, pos0, B, 99)
+    H, KV, hd = 32, 8, 128
+    kc, vc, q, k, v, norms = _prefill_inputs(H, KV, hd, pos0, B, 99 + pos0 + B)
     eps, base, scale = 1e-6, 1e6, 1 / np.sqrt(hd)
     gq, gk = norms[:hd], norms[hd:]
     okc, ovc = kc.copy(), vc.copy()
-    want = np.zeros((B, H * hd), np.float32)
+    oqs = np.zeros((B, H * hd), np.float32)
     for t in range(B):
         oq = oracle.rmsnorm_heads(q[t], gq, H, hd, eps)
         ok = oracle.rmsnorm_heads(k[t], gk, KV, hd, eps)
-        oq, ok = oracle.rope(oq, ok, H, KV, hd, pos0 + t, base)
-        want[t], okc, ovc = oracle.attention(oq, ok, v[t], okc, ovc, pos0 + t, H, KV, hd, scale, 0, 1)
+        oqs[t], okc[pos0 + t] = oracle.rope(oq, ok, H, KV, hd, pos0 + t, base)
+        ovc[pos0 + t] = v[t]
+    want = oracle.attention_prefill(oqs, okc, ovc, pos0, B, H, KV, hd, scale, sw)
     d = {n: torch.from_numpy(a.copy()).cuda() for n, a in
          dict(q=q, k=k, v=v, kc=kc, vc=vc, norms=norms).items()}
     out = torch.zeros(B, H * hd, device="cuda")
     lib.gncx_hip_attention_prefill(d["q"].data_ptr(), d["k"].data_ptr(), d["v"].data_ptr(), d["kc"].data_ptr(),
-                                   d["vc"].data_ptr(), pos0, B, H, KV, hd, scale, 0, d["norms"].data_ptr(), 0,
+                                   d["vc"].data_ptr(), pos0, B, H, KV, hd, scale, sw, d["norms"].data_ptr(), 0,
                                    hd * 4, 1, eps, 0, 0, base, out.data_ptr())
     gncx.check(lib)
-    got = out.cpu().numpy()
+    got = out.cpu().numpy().reshape(B, H * hd)
+    want = np.asarray(want, np.float32).reshape(B, H * hd)
     errs = [rel_l2(got[t], want[t]) for t in range(B)]
-    print(f"prefill device vs oracle: max row rel_l2={max(errs):.2e}")
+    print(f"prefill device vs oracle pos0={pos0} B={B} sw={sw}: max row rel_l2={max(errs):.2e}")
     assert max(errs) < TOL
     assert rel_l2(d["kc"].cpu().numpy(), okc) < 1e-6
+    assert rel_l2(d["vc"].cpu().numpy(), ovc) < 1e-6
 
 
 @pytest.mark.parametrize("rows,dim", [(5, 4096), (3, 4098), (2, 20000)])
