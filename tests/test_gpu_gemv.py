@@ -256,6 +256,12 @@ MATBATCH_CASES = [
     (Q4_K, 256, 100, 17), (Q4_K, 768, 50, 64), (Q4_K, 1280, 33, 2), (Q4_K, 12288, 200, 48),
     # Q4_K one-product kernel (B >= 1024, whole K): ragged B and N, one and 8 super-blocks
     (Q4_K, 2048, 1000, 1100), (Q4_K, 256, 520, 1030),
+    # Q4_K short batches (weights streamed through registers, up to 64 tokens):
+    # one and two token tiles, ragged N, K ranges of 1 to 8 super-blocks (the
+    # three register sets in turn, ranges of unequal length), one token
+    (Q4_K, 12288, 1030, 64), (Q4_K, 20480, 300, 1), (Q4_K, 4096, 777, 40), (Q4_K, 2304, 4100, 63),
+    (Q4_K, 4096, 16384, 32), (Q4_K, 2048, 24576, 50), (Q4_K, 3072, 40000, 20), (Q4_K, 1792, 40000, 9),
+    (Q4_K, 4096, 6144, 64),
 ]
 
 
