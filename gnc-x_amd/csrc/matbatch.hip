@@ -1441,49 +1441,67 @@ __global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
     }
 }
 
-// ---- Q4_K, short batches: weights streamed through registers --------------
+// ---- Q4_K, weights streamed through registers --------------------------------
 //
-// Up to 64 tokens each weight byte meets at most 64 tokens, and the tiled
-// kernels' per-step pipeline (weights staged in LDS, dequantised, read back,
-// a barrier every 32 values) leaves the matrix cores idle most of each step.
-// Here a work-group copies the quantised activations of its K range (q as
-// fp16, the blocks' d / s and the P pairs, the one-product kernel's inputs)
-// into LDS once; then every wave streams its own 32 weight rows straight
-// into registers, two super-blocks ahead, with no further barrier.  Lane l
-// holds row l % 32 and bytes 16 h .. 16 h + 15 (h = l / 32) of each
-// sub-block pair's 32 qs bytes, i.e. values 16 h .. 16 h + 15 of both
-// sub-blocks, which dequantised to sc q are its A operands of
-// v_mfma_f32_32x32x16_f16: K slice s of a sub-block is values 16 h + 8 s ..
-// + 8 in lane half h, and the activation operand is read from LDS in the
-// same order, so the slice's products pair each value with its own
-// activation.  Each block's integer dot is one product, scaled on the VALU by
-// the block's d_x / s, and d, dmin and the min term fold once per
+// A work-group is RT row tiles of 32 weight rows (one wave each) times 64
+// tokens.  Each wave streams its rows' super-blocks straight from memory
+// into registers, a super-block ahead: lane l holds row l % 32 and bytes
+// 16 h .. 16 h + 15 (h = l / 32) of each sub-block pair's 32 qs bytes, i.e.
+// values 16 h .. 16 h + 15 of both sub-blocks, which dequantised to sc q
+// are its A operands of v_mfma_f32_32x32x16_f16: K slice s of a sub-block
+// is values 16 h + 8 s .. + 8 in lane half h, and the activation operand is
+// read from LDS in the same order, so each slice's products pair every
+// value with its own activation.  The activations (q as fp16, the blocks'
+// d / s and the P pairs of the one-product kernel) stream through two LDS
+// stages, one super-block per stage, filled by direct-to-LDS loads issued
+// with the next super-block's weights as a super-block starts; one barrier
+// per super-block.  Each block's
+// integer dot is one product, scaled on the VALU by the block's d_x / s into
+// a super-block accumulator, and d, dmin and the min term fold once per
 // super-block, as in matbatch_q4k1_kernel (the same operations in the same
-// order: with whole K it gives that kernel's results bit for bit).  A work-
-// group is RT row tiles of 32 rows times KW waves sharing each row tile over
-// parts of the K range (their accumulators added in LDS in wave order at the
-// end); with gridDim.z > 1 its result is a split-K partial.
-constexpr int q4ks_kc_max(int tt) { return tt == 1 ? 2048 : 1024; }  // K values of a work-group at most
+// order: with whole K it gives that kernel's results bit for bit).  Against
+// the tiled kernels nothing is staged, dequantised or barriered per 32
+// values: a work-group's weights are read once, by the wave that uses them.
+// With gridDim.z > 1 the work-group's result is a split-K partial.
+// The result leaves through LDS, so that each store instruction writes one
+// token's contiguous row range.
+constexpr int kQsTok = 64;            // tokens per work-group
+constexpr int kQsXHalves = 64 * 260;  // halves per q stage: 64 x 256 of q, or 32 x (256 + 4) floats of output
 
-template <int TT, int RT, int KW>
-__global__ __launch_bounds__(64 * RT * KW, 1) void matbatch_q4k_skinny_kernel(
+template <int RT>
+__global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
     MbMats mats, size_t rbytes, const _Float16* __restrict xq, const float* __restrict dxs,
     const _Float16* __restrict pq, const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk,
-    float* __restrict part) {
-    constexpr int WAVES = RT * KW, THREADS = 64 * WAVES, BM = 32 * TT, BN = 32 * RT;
-    constexpr int KCM = q4ks_kc_max(TT), XLD = KCM + 8;  // halves per LDS token row (staggers banks)
-    __shared__ __align__(16) _Float16 xs[BM * XLD];       // q of the range, [token][K]
-    // d_x / s, [token][block], and the P pairs, [token][super-block][8 hi,
-    // 8 lo], their token rows padded to an odd number of dwords (sdx) and to
-    // twice one (sp): the 32 tokens' reads of one block then fall in
-    // distinct banks (with the rows kc / 32 dwords apart they shared two)
-    __shared__ __align__(16) float sdx[BM * (KCM / 32 + 1)];
-    __shared__ __align__(16) _Float16 sp[BM * (KCM / 16 + 4)];
+    float* __restrict part, int32_t xmap_tg) {
+    constexpr int WAVES = RT, BM = kQsTok, BN = 32 * RT;
+    static_assert(RT == 8, "one d / s row and one P slice per wave and stage");
+    // stage s: q [token][256] with the 16-byte segments of token t at
+    // positions c ^ (t % 16) (conflict-free reads of one segment by 16
+    // tokens), d_x / s [block][token], P [token][8 hi, 8 lo]; separate
+    // arrays, so that a load into one stage does not make the compiler wait
+    // before reads of another
+    __shared__ __align__(16) _Float16 xs0[kQsXHalves], xs1[kQsXHalves];
+    __shared__ __align__(16) float sd0[8 * BM], sd1[8 * BM];
+    __shared__ __align__(16) _Float16 sp0[16 * BM], sp1[16 * BM];
     __shared__ __align__(16) float srs[BM];
     __shared__ __align__(16) float sdm[WAVES][2][32];  // per wave: its rows' d and dmin
-    static_assert((BM * KCM / 8) % THREADS == 0 && (BM * (KCM / 128)) % THREADS == 0, "whole loads per thread");
 
-    const int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y);
+    // the work-group's row group, token group and K range: with xmap_tg
+    // (a multiple of 8 token groups, no split) the 1-D grid is dealt so that
+    // each XCD (work-group i runs on XCD i % 8) keeps one eighth of the token
+    // groups and walks the row groups, its concurrent work-groups sharing
+    // row groups' weights and its token groups' activations in its L2
+    int bx, by, bz;
+    if (xmap_tg > 0) {
+        const int lin = static_cast<int>(blockIdx.x), xcd = lin & 7, slot = lin >> 3, tpx = xmap_tg / 8;
+        bx = slot / tpx;
+        by = xcd * tpx + slot % tpx;
+        bz = 0;
+    } else {
+        bx = static_cast<int>(blockIdx.x);
+        by = static_cast<int>(blockIdx.y);
+        bz = static_cast<int>(blockIdx.z);
+    }
     const uint8_t* __restrict w = mats.w[0];
     float* __restrict y = mats.y[0];
     int32_t n = mats.n[0], tile0 = 0, npre = 0;
@@ -1499,104 +1517,73 @@ __global__ __launch_bounds__(64 * RT * KW, 1) void matbatch_q4k_skinny_kernel(
     }
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int li = lane & 31, lh = lane >> 5;
-    const int rt = wv % RT, kw = wv / RT;
     const int32_t t0 = by * BM, n0 = (bx - tile0) * BN;
-    const int32_t kb = static_cast<int32_t>(blockIdx.z) * kchunk;
-    const int32_t kc = min(k, kb + kchunk) - kb;  // a multiple of 256
-    if (kc > KCM || kc <= 0) return;              // the plan never asks this (LDS holds KCM)
-    const int32_t nsb = kc / 256;
-    const int32_t sb0 = kw * nsb / KW, sb1 = (kw + 1) * nsb / KW;  // this wave's super-blocks
+    const int32_t kb = bz * kchunk;
+    const int32_t nsb = (min(k, kb + kchunk) - kb) / 256;  // super-blocks of the range
     const int32_t rows_here = min(BM, b - t0);
-    const int32_t sdxs = kc / 32 + 1, sps = kc / 16 + 4;  // padded row strides of sdx (floats) and sp (halves)
 
-    // this lane's weight row: 32 rt + l % 32 of the tile; rows past N and
-    // super-blocks past the wave's range read zeros (offsets past the resource)
+    // this lane's weight row, 32 wv + l % 32; rows past N and super-blocks
+    // past the range read zeros (offsets past the resource)
     const int32_t wrows_here = min(BN, n - n0);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
         wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
-    const int32_t wbase = (32 * rt + li) * static_cast<int32_t>(rbytes) + (kb / 256) * 144;
+    const int32_t wbase = (32 * wv + li) * static_cast<int32_t>(rbytes) + (kb / 256) * 144;
     struct SbRegs {
         u32x4 h, q[4];
     };
     auto wload = [&](SbRegs& r, int32_t s) {
-        const int32_t off = s < sb1 ? wbase + s * 144 : kMfOob;
+        const int32_t off = s < nsb ? wbase + s * 144 : kMfOob;
         r.h = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
 #pragma unroll
         for (int p = 0; p < 4; ++p) r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off + 16 + 32 * p + 16 * lh, 0, 0);
     };
-    SbRegs R0, R1, R2;
-    wload(R0, sb0);
-    wload(R1, sb0 + 1);
+    // the activations of super-block s into a stage: 4 q loads, one d / s
+    // row and one P slice per wave (token rows past B read zeros)
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(xq + static_cast<size_t>(t0) * k), static_cast<short>(0),
+        rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(dxs + static_cast<size_t>(t0) * (k / 32)), static_cast<short>(0),
+        rows_here * (k / 32) * static_cast<int32_t>(sizeof(float)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * (k / 256) * 16), static_cast<short>(0),
+        rows_here * (k / 256) * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+    auto xload = [&](_Float16* xst, float* sdt, _Float16* spt, int32_t s) {
+        const bool in = s < nsb;
+        const int32_t k0 = kb + 256 * s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = i * WAVES + wv;  // token rows 2 q, 2 q + 1
+            const int t = 2 * q + (lane >> 5), c = (lane & 31) ^ (t & 15);
+            const int32_t off = in ? (t * k + k0 + 8 * c) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)(xst + 512 * q), 16, off, 0, 0, 0);
+        }
+        {
+            const int32_t off = in ? (lane * (k / 32) + k0 / 32 + wv) * static_cast<int32_t>(sizeof(float)) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_ptr)(sdt + 64 * wv), 4, off, 0, 0, 0);
+        }
+        {
+            const int dw = 64 * wv + lane, t = dw >> 3;
+            const int32_t off =
+                in ? ((t * (k / 256) + k0 / 256) * 16 + 2 * (dw & 7)) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(spt + 128 * wv), 4, off, 0, 0, 0);
+        }
+    };
+    if (tid < BM) srs[tid] = tid < rows_here ? rscale[t0 + tid] : 0.0f;
+    SbRegs R0, R1;
+    wload(R0, 0);
+    xload(xs0, sd0, sp0, 0);
+    step_barrier<0>();
 
-    // the range's activations into LDS (token rows past B read zeros)
-    {
-        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<_Float16*>(xq + static_cast<size_t>(t0) * k), static_cast<short>(0),
-            rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-        const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(dxs + static_cast<size_t>(t0) * (k / 32)), static_cast<short>(0),
-            rows_here * (k / 32) * static_cast<int32_t>(sizeof(float)), 0x00020000);
-        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<_Float16*>(pq + static_cast<size_t>(t0) * (k / 256) * 16), static_cast<short>(0),
-            rows_here * (k / 256) * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-        constexpr int XIT = BM * KCM / 8 / THREADS, DIT = BM * (KCM / 128) / THREADS;
-        const int32_t segs = kc / 8, dsegs = kc / 128;  // 16-byte pieces per token row: q; scales (and P)
-        u32x4 xv[XIT], dv[DIT], pv[DIT];
+    floatx16 acc[2], S[2];
 #pragma unroll
-        for (int i = 0; i < XIT; ++i) {
-            const int32_t f = tid + i * THREADS, r = f / segs, g = f - r * segs;
-            const int32_t off = f < BM * segs ? (r * k + kb + 8 * g) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
-            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < DIT; ++i) {
-            const int32_t f = tid + i * THREADS, r = f / dsegs, g = f - r * dsegs;
-            const bool in = f < BM * dsegs;
-            dv[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                drs, in ? (r * (k / 32) + kb / 32 + 4 * g) * static_cast<int32_t>(sizeof(float)) : kMfOob, 0, 0);
-            pv[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                prs, in ? ((r * (k / 256) + kb / 256) * 16 + 8 * g) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob,
-                0, 0);
-        }
-        if (tid < BM) srs[tid] = tid < rows_here ? rscale[t0 + tid] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < XIT; ++i) {
-            const int32_t f = tid + i * THREADS, r = f / segs, g = f - r * segs;
-            if (f < BM * segs) *reinterpret_cast<u32x4*>(&xs[r * XLD + 8 * g]) = xv[i];
-        }
-#pragma unroll
-        for (int i = 0; i < DIT; ++i) {
-            const int32_t f = tid + i * THREADS, r = f / dsegs, g = f - r * dsegs;
-            if (f < BM * dsegs) {
-                // stored as the loaded integers: with this compiler, float
-                // bit casts of a 16-byte buffer load's elements let it shrink
-                // the load to one dword and store that element four times
-                uint32_t* dr = reinterpret_cast<uint32_t*>(&sdx[r * sdxs + 4 * g]);
-                dr[0] = dv[i].x;
-                dr[1] = dv[i].y;
-                dr[2] = dv[i].z;
-                dr[3] = dv[i].w;
-                uint2* pr = reinterpret_cast<uint2*>(&sp[r * sps + 8 * g]);
-                pr[0] = make_uint2(pv[i].x, pv[i].y);
-                pr[1] = make_uint2(pv[i].z, pv[i].w);
-            }
-        }
-    }
-    __syncthreads();
-
-    floatx16 acc[TT], S[TT];
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt)
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[tt][r] = S[tt][r] = 0.0f;
 
-    // one super-block (index s of the range) from its registers, as a
-    // software pipeline over its 8 blocks: the products of block j are
-    // issued, then the block scale of block j - 1 is applied to its products
-    // (independent VALU work while the matrix core runs), then the operands
-    // of block j + 1 are read from LDS and its weights dequantised
-    auto process = [&](const SbRegs& R, int32_t s) {
+    // one super-block from its registers and stage
+    auto process = [&](const SbRegs& R, const _Float16* xst, const float* sdt, const _Float16* spt) {
         if (lh == 0) {
             sdm[wv][0][li] = half_bits_to_float(R.h.x & 0xffffu);
             sdm[wv][1][li] = half_bits_to_float(R.h.x >> 16);
@@ -1611,14 +1598,16 @@ __global__ __launch_bounds__(64 * RT * KW, 1) void matbatch_q4k_skinny_kernel(
         // block j's operands: activations of both token tiles and K slices,
         // their block scales, and the weights as sc q (two codes per
         // instruction, as in the tiled kernels)
-        auto operands = [&](int j, half8 (&xo)[TT][2], float (&dvv)[TT], half8 (&wq)[2]) {
+        auto operands = [&](int j, half8 (&xo)[2][2], float (&dvv)[2], half8 (&wq)[2]) {
 #pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
+            for (int tt = 0; tt < 2; ++tt) {
                 const int tr = 32 * tt + li;
-                const _Float16* xr = &xs[tr * XLD + s * 256 + 32 * j + 16 * lh];
-                xo[tt][0] = *reinterpret_cast<const half8*>(xr);
-                xo[tt][1] = *reinterpret_cast<const half8*>(xr + 8);
-                dvv[tt] = sdx[tr * sdxs + s * 8 + j];
+#pragma unroll
+                for (int sl = 0; sl < 2; ++sl) {
+                    const int c = (4 * j + 2 * lh + sl) ^ (tr & 15);
+                    xo[tt][sl] = *reinterpret_cast<const half8*>(&xst[256 * tr + 8 * c]);
+                }
+                dvv[tt] = sdt[64 * j + tr];
             }
             const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc[j]));
             const _Float16 off = static_cast<_Float16>(-1024.0f * static_cast<float>(sc[j]));
@@ -1635,41 +1624,33 @@ __global__ __launch_bounds__(64 * RT * KW, 1) void matbatch_q4k_skinny_kernel(
             wq[0] = __builtin_bit_cast(half8, make_uint4(o[0], o[1], o[2], o[3]));
             wq[1] = __builtin_bit_cast(half8, make_uint4(o[4], o[5], o[6], o[7]));
         };
-        half8 xo[2][TT][2], wq[2][2];
-        float dvv[2][TT];
-        floatx16 blk[2][TT];
-        operands(0, xo[0], dvv[0], wq[0]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int c = j & 1;
+            half8 xo[2][2], wq[2];
+            float dvv[2];
+            operands(j, xo, dvv, wq);
+            floatx16 blk[2];
 #pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
+            for (int tt = 0; tt < 2; ++tt) {
                 const floatx16 zero = {};
-                blk[c][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[c][0], xo[c][tt][0], zero, 0, 0, 0);
-                blk[c][tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[c][1], xo[c][tt][1], blk[c][tt], 0, 0, 0);
+                blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[0], xo[tt][0], zero, 0, 0, 0);
+                blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wq[1], xo[tt][1], blk[tt], 0, 0, 0);
             }
-            if (j > 0) {
 #pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) S[tt][r] = fmaf(dvv[c ^ 1][tt], blk[c ^ 1][tt][r], S[tt][r]);
-            }
-            if (j < 7) operands(j + 1, xo[c ^ 1], dvv[c ^ 1], wq[c ^ 1]);
+                for (int r = 0; r < 16; ++r) S[tt][r] = fmaf(dvv[tt], blk[tt][r], S[tt][r]);
         }
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) S[tt][r] = fmaf(dvv[1][tt], blk[1][tt][r], S[tt][r]);
         // acc += d S - dmin (m . P); the mins of sub-blocks 4 h .. + 3 are
         // the min product's A operand (K = the super-block's 8 sub-blocks)
         half4 mn4;
 #pragma unroll
         for (int q = 0; q < 4; ++q) mn4[q] = static_cast<_Float16>(static_cast<float>(lh ? mn[4 + q] : mn[q]));
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
+        for (int tt = 0; tt < 2; ++tt) {
             const int tr = 32 * tt + li;
-            const half4 ph = *reinterpret_cast<const half4*>(&sp[tr * sps + s * 16 + 4 * lh]);
-            const half4 pl = *reinterpret_cast<const half4*>(&sp[tr * sps + s * 16 + 8 + 4 * lh]);
+            const half4 ph = *reinterpret_cast<const half4*>(&spt[16 * tr + 4 * lh]);
+            const half4 pl = *reinterpret_cast<const half4*>(&spt[16 * tr + 8 + 4 * lh]);
             const floatx16 zero = {};
             floatx16 M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn4, ph, zero, 0, 0, 0);
             M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn4, pl, M, 0, 0, 0);
@@ -1689,74 +1670,55 @@ __global__ __launch_bounds__(64 * RT * KW, 1) void matbatch_q4k_skinny_kernel(
         }
     };
 
-    // super-blocks s, s + 1, s + 2 in register sets 0, 1, 2 in turn, each
-    // set reloaded with the super-block three ahead as it is taken
-    for (int32_t s = sb0; s < sb1; s += 3) {
-        wload(R2, s + 2);
-        process(R0, s);
-        if (s + 1 >= sb1) break;
-        wload(R0, s + 3);
-        process(R1, s + 1);
-        if (s + 2 >= sb1) break;
-        wload(R1, s + 4);
-        process(R2, s + 2);
+    // super-blocks s, s + 1 in register sets and stages 0, 1 in turn: each
+    // starts the loads of the next into the other set and stage, and ends
+    // with the barrier after which they are in place for every wave and its
+    // own stage may be refilled
+    for (int32_t s = 0; s < nsb; s += 2) {
+        wload(R1, s + 1);
+        xload(xs1, sd1, sp1, s + 1);
+        process(R0, xs0, sd0, sp0);
+        step_barrier<0>();
+        if (s + 1 >= nsb) break;
+        wload(R0, s + 2);
+        xload(xs0, sd0, sp0, s + 2);
+        process(R1, xs1, sd1, sp1);
+        step_barrier<0>();
     }
 
-    // The result leaves through LDS, so that each store instruction writes
-    // one token's whole row range (BN floats, contiguous in y and in the
-    // partials): each wave first writes its tile there, [token][row] with
-    // rows padded to BN + 4 floats (conflict-free), after the waves of one
-    // row tile have added their parts in wave order.
+    // the tile of token tile tt in stage tt's q array as [32 tokens][BN + 4]
+    // floats (rows padded: conflict-free), then whole token rows out
     constexpr int OLD = BN + 4;
-    static_assert(BM * OLD * 4 + (KW - 1) * RT * TT * 16 * 64 * 4 <= static_cast<int>(sizeof(xs)), "staging fits in xs");
-    float* ost = reinterpret_cast<float*>(xs);
-    __syncthreads();  // every wave is done with the activations
-    if constexpr (KW > 1) {
-        float* red = ost + BM * OLD;
-        if (kw > 0) {
+    static_assert(32 * OLD * 2 <= kQsXHalves, "an output tile fits in a stage");
+    __syncthreads();
 #pragma unroll
-            for (int tt = 0; tt < TT; ++tt)
+    for (int tt = 0; tt < 2; ++tt) {
+        float* ost = reinterpret_cast<float*>(tt == 0 ? xs0 : xs1);
+        const float rs = srs[32 * tt + li];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) red[((((kw - 1) * RT + rt) * TT + tt) * 16 + r) * 64 + lane] = acc[tt][r];
-        }
-        __syncthreads();
-        if (kw == 0) {
-#pragma unroll
-            for (int q = 1; q < KW; ++q)
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[tt][r] += red[((((q - 1) * RT + rt) * TT + tt) * 16 + r) * 64 + lane];
-        }
-    }
-    if (kw == 0) {
-        // lane: token 32 tt + l % 32, rows 8 g + 4 h + 0..3 of row tile rt in registers 4 g + 0..3
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
-            const int tl = 32 * tt + li;
-            const float rs = srs[tl];
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<float4*>(&ost[tl * OLD + 32 * rt + 8 * g + 4 * lh]) =
-                    make_float4(acc[tt][4 * g] * rs, acc[tt][4 * g + 1] * rs, acc[tt][4 * g + 2] * rs,
-                                acc[tt][4 * g + 3] * rs);
-        }
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(&ost[li * OLD + 32 * wv + 8 * g + 4 * lh]) =
+                make_float4(acc[tt][4 * g] * rs, acc[tt][4 * g + 1] * rs, acc[tt][4 * g + 2] * rs,
+                            acc[tt][4 * g + 3] * rs);
     }
     __syncthreads();
-    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
+    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(bz) * mats.ntot + npre) * b : y;
     const int32_t rows = min(BN, n - n0);
     if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
         // 4 rows per lane, BN / 4 lanes per token
-        constexpr int LPT = BN / 4, TPI = 64 * WAVES / LPT;  // lanes per token, tokens per pass
-        const int tl0 = tid / LPT, c = 4 * (tid % LPT);
-        for (int tl = tl0; tl < rows_here; tl += TPI)
+        constexpr int LPT = BN / 4, TPI = 64 * WAVES / LPT;
+        const int c = 4 * (tid % LPT);
+        for (int tl = tid / LPT; tl < rows_here; tl += TPI) {
+            const float* ost = reinterpret_cast<const float*>(tl < 32 ? xs0 : xs1);
             if (c < rows)
                 *reinterpret_cast<float4*>(&dst[static_cast<size_t>(t0 + tl) * n + n0 + c]) =
-                    *reinterpret_cast<const float4*>(&ost[tl * OLD + c]);
+                    *reinterpret_cast<const float4*>(&ost[(tl & 31) * OLD + c]);
+        }
     } else {
         for (int e = tid; e < rows_here * BN; e += 64 * WAVES) {
             const int tl = e / BN, c = e % BN;
-            if (c < rows) dst[static_cast<size_t>(t0 + tl) * n + n0 + c] = ost[tl * OLD + c];
+            const float* ost = reinterpret_cast<const float*>(tl < 32 ? xs0 : xs1);
+            if (c < rows) dst[static_cast<size_t>(t0 + tl) * n + n0 + c] = ost[(tl & 31) * OLD + c];
         }
     }
 }
@@ -1892,9 +1854,9 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
 
 // Q4_K tiles: (waves along tokens, along rows, tiles per wave along each)
 struct Q4kPlan {
-    int cfg;  // 0: 128 tokens x 256 rows, 4: 64 x 256 (8 waves, one work-group per CU), 8: short batch
+    int cfg;  // 0: 128 tokens x 256 rows, 4: 64 x 256 (8 waves, one work-group per CU), 8: streamed weights
     int32_t splits, kchunk;
-    int tt = 0, rt = 0, kw = 0;  // short batch: 32-token tiles, row tiles and waves per row tile
+    int32_t xmap = 0;  // streamed weights: token groups of the XCD-aware order (0: grid order)
 };
 
 // Tiles of 256 rows with K split into ranges of whole super-blocks until
@@ -1909,39 +1871,27 @@ struct Q4kPlan {
 // (B = 100, 128): 4096 -> 14336 at B = 64: 46 against 54 us; 12288 -> 4096 at
 // B = 64: 49 against 58; 4096 x 4096 at B = 32 / 64 / 100 / 128: 23.6 / 28.9 /
 // 32.9 / 34.3 against 25.7 / 29.1 / 36.6 / 37.8 us.
-#ifndef GNCX_Q4K_SKINNY
-#define GNCX_Q4K_SKINNY 1
+#ifndef GNCX_Q4K_STREAM
+#define GNCX_Q4K_STREAM 1
 #endif
-#ifndef GNCX_Q4KS_RT
-#define GNCX_Q4KS_RT 8
-#endif
-#ifndef GNCX_Q4KS_KW
-#define GNCX_Q4KS_KW 1
-#endif
-#ifndef GNCX_Q4KS_WG
-#define GNCX_Q4KS_WG 256
-#endif
-// Up to 64 tokens, matbatch_q4k_skinny_kernel: work-groups of RT row tiles
-// (x KW waves), K split in ranges of whole super-blocks until about
-// GNCX_Q4KS_WG work-groups run, each range at most what LDS holds.
-Q4kPlan q4k_skinny_plan(int32_t b, int32_t k, int32_t n) {
+// matbatch_q4k_stream_kernel: row groups of 256 x 64 tokens, K split in
+// ranges of whole super-blocks until about 256 work-groups run; unsplit with
+// a multiple of 8 token groups, the XCD-aware order (xmap = token groups).
+Q4kPlan q4k_stream_plan(int32_t b, int32_t k, int32_t n) {
     Q4kPlan p{8, 1, k};
-    p.tt = b <= 32 ? 1 : 2;
-    p.rt = GNCX_Q4KS_RT;
-    p.kw = GNCX_Q4KS_KW;
-    const int32_t nsb = k / 256, kcm_sb = q4ks_kc_max(p.tt) / 256;
-    const int64_t groups = static_cast<int64_t>((n + 32 * p.rt - 1) / (32 * p.rt)) * ((b + 32 * p.tt - 1) / (32 * p.tt));
-    int32_t splits = static_cast<int32_t>(std::max<int64_t>(1, GNCX_Q4KS_WG / groups));
-    splits = std::min(splits, nsb);
-    int32_t csb = (nsb + splits - 1) / splits;
-    csb = std::min(csb, kcm_sb);
+    const int32_t nsb = k / 256;
+    const int64_t rg = (n + 255) / 256, tg = (b + kQsTok - 1) / kQsTok, wgs = rg * tg;
+    int32_t splits = wgs >= 256 ? 1 : static_cast<int32_t>(256 / wgs);
+    splits = std::max(1, std::min(splits, nsb));
+    const int32_t csb = (nsb + splits - 1) / splits;
     p.kchunk = csb * 256;
     p.splits = (nsb + csb - 1) / csb;
+    p.xmap = p.splits == 1 && tg % 8 == 0 ? static_cast<int32_t>(tg) : 0;
     return p;
 }
 
 Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
-    if (GNCX_Q4K_SKINNY && b <= 64 && k >= 256) return q4k_skinny_plan(b, k, n);
+    if (GNCX_Q4K_STREAM && k >= 256) return q4k_stream_plan(b, k, n);
     const int bm = b > 128 ? 128 : 64;
     const int64_t t = static_cast<int64_t>((n + 255) / 256) * ((b + bm - 1) / bm);
     int32_t splits = static_cast<int32_t>(256 / t);
@@ -2039,32 +1989,24 @@ hipError_t launch_q4k1_t(const MbMats& m, const _Float16* xq, const float* dxs, 
     return hipGetLastError();
 }
 
-template <int TT, int RT, int KW>
-hipError_t launch_q4ks_t(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
-                         const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part,
-                         hipStream_t stream) {
-    constexpr int BM = 32 * TT, BN = 32 * RT;
-    if (p.kchunk > q4ks_kc_max(TT) || p.kchunk % 256 != 0 || b > 64) return hipErrorInvalidValue;
-    const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
-    const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
-    hipLaunchKernelGGL((matbatch_q4k_skinny_kernel<TT, RT, KW>), grid, dim3(64 * RT * KW), 0, stream, m,
-                       row_bytes(kQ4_K, k), xq, dxs, pq, rscale, b, k, p.kchunk, part);
-    return hipGetLastError();
-}
-
 hipError_t launch_q4ks(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
                        const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part,
                        hipStream_t stream) {
-    static_assert(GNCX_Q4KS_RT * GNCX_Q4KS_KW == 8, "8 waves per work-group");
-    return p.tt == 1 ? launch_q4ks_t<1, GNCX_Q4KS_RT, GNCX_Q4KS_KW>(m, xq, dxs, pq, rscale, b, k, p, part, stream)
-                     : launch_q4ks_t<2, GNCX_Q4KS_RT, GNCX_Q4KS_KW>(m, xq, dxs, pq, rscale, b, k, p, part, stream);
+    constexpr int BN = 256;
+    if (p.kchunk % 256 != 0) return hipErrorInvalidValue;
+    const int32_t rg = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN, tg = (b + kQsTok - 1) / kQsTok;
+    if (p.xmap > 0 && (p.xmap != tg || tg % 8 != 0 || p.splits != 1)) return hipErrorInvalidValue;
+    const dim3 grid = p.xmap > 0 ? dim3(rg * tg) : dim3(rg, tg, p.splits);
+    hipLaunchKernelGGL(matbatch_q4k_stream_kernel<8>, grid, dim3(512), 0, stream, m, row_bytes(kQ4_K, k), xq, dxs,
+                       pq, rscale, b, k, p.kchunk, part, p.xmap);
+    return hipGetLastError();
 }
 
 // The product of plan p over the matrices of m (w, y, n and count set), then
 // with split K the reduce of the partials into each y
 hipError_t launch_q4k_mats(MbMats& m, _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
                            int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
-    const int32_t bn = p.cfg == 8 ? 32 * p.rt : kQ4kTileRows;
+    const int32_t bn = kQ4kTileRows;
     int32_t t = 0, rows = 0;
     RedMats r{};
     for (int32_t i = 0; i < m.count; ++i) {
