@@ -1452,10 +1452,10 @@ __global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
 // is values 16 h + 8 s .. + 8 in lane half h, and the activation operand is
 // read from LDS in the same order, so each slice's products pair every
 // value with its own activation.  The activations (q as fp16, the blocks'
-// d / s and the P pairs of the one-product kernel) stream through two LDS
-// stages, one super-block per stage, filled by direct-to-LDS loads issued
-// with the next super-block's weights as a super-block starts; one barrier
-// per super-block.  Each block's
+// d / s and the P pairs of the one-product kernel) stream through three LDS
+// stages, one super-block per stage, filled by direct-to-LDS loads two
+// super-blocks ahead, issued with the next super-block's weights as a
+// super-block starts; one barrier per super-block.  Each block's
 // integer dot is one product, scaled on the VALU by the block's d_x / s into
 // a super-block accumulator, and d, dmin and the min term fold once per
 // super-block, as in matbatch_q4k1_kernel (the same operations in the same
@@ -1480,9 +1480,9 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
     // tokens), d_x / s [block][token], P [token][8 hi, 8 lo]; separate
     // arrays, so that a load into one stage does not make the compiler wait
     // before reads of another
-    __shared__ __align__(16) _Float16 xs0[kQsXHalves], xs1[kQsXHalves];
-    __shared__ __align__(16) float sd0[8 * BM], sd1[8 * BM];
-    __shared__ __align__(16) _Float16 sp0[16 * BM], sp1[16 * BM];
+    __shared__ __align__(16) _Float16 xs0[kQsXHalves], xs1[kQsXHalves], xs2[kQsXHalves];
+    __shared__ __align__(16) float sd0[8 * BM], sd1[8 * BM], sd2[8 * BM];
+    __shared__ __align__(16) _Float16 sp0[16 * BM], sp1[16 * BM], sp2[16 * BM];
     __shared__ __align__(16) float srs[BM];
     __shared__ __align__(16) float sdm[WAVES][2][32];  // per wave: its rows' d and dmin
 
@@ -1570,11 +1570,13 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(spt + 128 * wv), 4, off, 0, 0, 0);
         }
     };
+    constexpr int kXLoads = 4 + 2;  // activation loads per wave and super-block (q; d / s and P)
     if (tid < BM) srs[tid] = tid < rows_here ? rscale[t0 + tid] : 0.0f;
     SbRegs R0, R1;
     wload(R0, 0);
     xload(xs0, sd0, sp0, 0);
-    step_barrier<0>();
+    xload(xs1, sd1, sp1, 1);
+    step_barrier<kXLoads>();
 
     floatx16 acc[2], S[2];
 #pragma unroll
@@ -1639,7 +1641,7 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) S[tt][r] = fmaf(dvv[tt], blk[tt][r], S[tt][r]);
+                for (int r = 0; r < 16; ++r) S[tt][r] = j == 0 ? dvv[tt] * blk[tt][r] : fmaf(dvv[tt], blk[tt][r], S[tt][r]);
         }
         // acc += d S - dmin (m . P); the mins of sub-blocks 4 h .. + 3 are
         // the min product's A operand (K = the super-block's 8 sub-blocks)
@@ -1664,27 +1666,32 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
                     const int r = 4 * g + q;
                     acc[tt][r] = fmaf(S[tt][r], dq[q], acc[tt][r]);
                     acc[tt][r] = fmaf(M[r], -mq[q], acc[tt][r]);
-                    S[tt][r] = 0.0f;
                 }
             }
         }
     };
 
-    // super-blocks s, s + 1 in register sets and stages 0, 1 in turn: each
-    // starts the loads of the next into the other set and stage, and ends
-    // with the barrier after which they are in place for every wave and its
-    // own stage may be refilled
-    for (int32_t s = 0; s < nsb; s += 2) {
-        wload(R1, s + 1);
-        xload(xs1, sd1, sp1, s + 1);
-        process(R0, xs0, sd0, sp0);
-        step_barrier<0>();
-        if (s + 1 >= nsb) break;
-        wload(R0, s + 2);
-        xload(xs0, sd0, sp0, s + 2);
-        process(R1, xs1, sd1, sp1);
-        step_barrier<0>();
+    // super-block s in register set s % 2 and stage s % 3: each starts
+    // the loads of the next super-block's weights and of the activations two
+    // ahead (into the stage the one before it left), and ends with the
+    // barrier after which the next is in place for every wave (only the
+    // activations two ahead may still be in flight) and its own stage may be
+    // refilled
+#define GNCX_QS_STEP(RA, RB, XA, DA, PA, XC, DC, PC, OFF) \
+    wload(RB, s + (OFF) + 1);                        \
+    xload(XC, DC, PC, s + (OFF) + 2);                \
+    process(RA, XA, DA, PA);                         \
+    step_barrier<kXLoads>();                         \
+    if (s + (OFF) + 1 >= nsb) break;
+    for (int32_t s = 0; s < nsb; s += 6) {
+        GNCX_QS_STEP(R0, R1, xs0, sd0, sp0, xs2, sd2, sp2, 0)
+        GNCX_QS_STEP(R1, R0, xs1, sd1, sp1, xs0, sd0, sp0, 1)
+        GNCX_QS_STEP(R0, R1, xs2, sd2, sp2, xs1, sd1, sp1, 2)
+        GNCX_QS_STEP(R1, R0, xs0, sd0, sp0, xs2, sd2, sp2, 3)
+        GNCX_QS_STEP(R0, R1, xs1, sd1, sp1, xs0, sd0, sp0, 4)
+        GNCX_QS_STEP(R1, R0, xs2, sd2, sp2, xs1, sd1, sp1, 5)
     }
+#undef GNCX_QS_STEP
 
     // the tile of token tile tt in stage tt's q array as [32 tokens][BN + 4]
     // floats (rows padded: conflict-free), then whole token rows out
