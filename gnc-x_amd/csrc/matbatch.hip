@@ -1441,7 +1441,7 @@ __global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
     }
 }
 
-// ---- Q4_K, weights streamed through registers --------------------------------
+// ---- Q4_K and Q6_K, weights streamed through registers ------------------------
 //
 // A work-group is RT row tiles of 32 weight rows (one wave each) times 64
 // tokens.  Each wave streams its rows' super-blocks straight from memory
@@ -1465,11 +1465,57 @@ __global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
 // With gridDim.z > 1 the work-group's result is a split-K partial.
 // The result leaves through LDS, so that each store instruction writes one
 // token's contiguous row range.
+// Q6_K (cpp:742-757) takes the same structure: the weights are the integers
+// sc (q - 32), d folds once per super-block and there is no min term.
+// sc (q - 32) can need 12 bits (|sc| up to 128), so each is taken as two
+// fp16 integers that are always exact, sc (l - 16) and 16 sc (u - 1) (q = l
+// + 16 u, l the 4 bits from ql, u the 2 from qh), and a block's dot is two
+// products per K slice (integers below 2^24: exact).  Lane half h takes
+// values 16 h .. 16 h + 15 of each 32-value group of both 128-value halves:
+// per half the 16 bytes of ql at 16 h and at 32 + 16 h and of qh at 16 h
+// (all four groups' values), so a group's two K slices are again values
+// 16 h + 8 s .. + 8.  Its blocks are only 2-byte aligned: each 16-byte piece
+// is read as a dwordx4 from the dword at or below it plus one dword, and
+// realigned.
 constexpr int kQsTok = 64;            // tokens per work-group
 constexpr int kQsXHalves = 64 * 260;  // halves per q stage: 64 x 256 of q, or 32 x (256 + 4) floats of output
 
-template <int RT>
-__global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
+// one super-block of a lane's weight row in registers
+template <int TYPE>
+struct QsW;
+template <>
+struct QsW<kQ4_K> {
+    static constexpr int32_t kBytes = 144;
+    u32x4 h, q[4];  // header; 16 bytes of each sub-block pair's qs
+    __device__ __forceinline__ void load(const __amdgpu_buffer_rsrc_t& rs, int32_t off, int lh) {
+        h = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) q[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 + 32 * p + 16 * lh, 0, 0);
+    }
+};
+template <>
+struct QsW<kQ6_K> {
+    static constexpr int32_t kBytes = 210;
+    // pieces: ql of half 0 at 16 h and 32 + 16 h, of half 1 at 64 + 16 h and
+    // 96 + 16 h, qh at 128 + 16 h and 160 + 16 h, the scales and d at 192;
+    // each as the 20 bytes from the dword at or below it
+    u32x4 p[7];
+    uint32_t e[7];
+    static __device__ __forceinline__ int32_t piece(int i, int lh) {
+        return i < 6 ? 32 * i + 16 * lh : 192;
+    }
+    __device__ __forceinline__ void load(const __amdgpu_buffer_rsrc_t& rs, int32_t off, int lh) {
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+            const int32_t o = (off + piece(i, lh)) & ~3;
+            p[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+            e[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 16, 0, 0);
+        }
+    }
+};
+
+template <int TYPE, int RT>
+__global__ __launch_bounds__(64 * RT, 1) void matbatch_qs_stream_kernel(
     MbMats mats, size_t rbytes, const _Float16* __restrict xq, const float* __restrict dxs,
     const _Float16* __restrict pq, const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk,
     float* __restrict part, int32_t xmap_tg) {
@@ -1528,16 +1574,10 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
         wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
-    const int32_t wbase = (32 * wv + li) * static_cast<int32_t>(rbytes) + (kb / 256) * 144;
-    struct SbRegs {
-        u32x4 h, q[4];
-    };
-    auto wload = [&](SbRegs& r, int32_t s) {
-        const int32_t off = s < nsb ? wbase + s * 144 : kMfOob;
-        r.h = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(wrs, off + 16 + 32 * p + 16 * lh, 0, 0);
-    };
+    constexpr int32_t kWB = QsW<TYPE>::kBytes;
+    const int32_t wbase = (32 * wv + li) * static_cast<int32_t>(rbytes) + (kb / 256) * kWB;
+    using SbRegs = QsW<TYPE>;
+    auto wload = [&](SbRegs& r, int32_t s) { r.load(wrs, s < nsb ? wbase + s * kWB : kMfOob, lh); };
     // the activations of super-block s into a stage: 4 q loads, one d / s
     // row and one P slice per wave (token rows past B read zeros)
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1547,8 +1587,8 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
         const_cast<float*>(dxs + static_cast<size_t>(t0) * (k / 32)), static_cast<short>(0),
         rows_here * (k / 32) * static_cast<int32_t>(sizeof(float)), 0x00020000);
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * (k / 256) * 16), static_cast<short>(0),
-        rows_here * (k / 256) * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
+        const_cast<_Float16*>(TYPE == kQ4_K ? pq + static_cast<size_t>(t0) * (k / 256) * 16 : xq), static_cast<short>(0),
+        TYPE == kQ4_K ? rows_here * (k / 256) * 16 * static_cast<int32_t>(sizeof(_Float16)) : 0, 0x00020000);
     auto xload = [&](_Float16* xst, float* sdt, _Float16* spt, int32_t s) {
         const bool in = s < nsb;
         const int32_t k0 = kb + 256 * s;
@@ -1563,14 +1603,15 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
             const int32_t off = in ? (lane * (k / 32) + k0 / 32 + wv) * static_cast<int32_t>(sizeof(float)) : kMfOob;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_ptr)(sdt + 64 * wv), 4, off, 0, 0, 0);
         }
-        {
+        if constexpr (TYPE == kQ4_K) {
             const int dw = 64 * wv + lane, t = dw >> 3;
             const int32_t off =
                 in ? ((t * (k / 256) + k0 / 256) * 16 + 2 * (dw & 7)) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(spt + 128 * wv), 4, off, 0, 0, 0);
         }
     };
-    constexpr int kXLoads = 4 + 2;  // activation loads per wave and super-block (q; d / s and P)
+    // activation loads per wave and super-block (q; d / s; Q4_K: P)
+    constexpr int kXLoads = TYPE == kQ4_K ? 6 : 5;
     if (tid < BM) srs[tid] = tid < rows_here ? rscale[t0 + tid] : 0.0f;
     SbRegs R0, R1;
     wload(R0, 0);
@@ -1584,8 +1625,8 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[tt][r] = S[tt][r] = 0.0f;
 
-    // one super-block from its registers and stage
-    auto process = [&](const SbRegs& R, const _Float16* xst, const float* sdt, const _Float16* spt) {
+    // one Q4_K super-block from its registers and stage
+    auto process_q4k = [&](const QsW<kQ4_K>& R, const _Float16* xst, const float* sdt, const _Float16* spt) {
         if (lh == 0) {
             sdm[wv][0][li] = half_bits_to_float(R.h.x & 0xffffu);
             sdm[wv][1][li] = half_bits_to_float(R.h.x >> 16);
@@ -1671,6 +1712,107 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
         }
     };
 
+    // one Q6_K super-block (index sidx of the range) from its registers and stage
+    auto process_q6k = [&](const QsW<kQ6_K>& R, const _Float16* xst, const float* sdt, int32_t sidx) {
+        // pieces realigned as they are used (blocks are 2-byte aligned: the shift is 0 or 2)
+        const int sh = (wbase + sidx * kWB) & 3;
+        auto piece = [&](int i, int d) {
+            const uint32_t lo = d == 0 ? R.p[i].x : d == 1 ? R.p[i].y : d == 2 ? R.p[i].z : R.p[i].w;
+            const uint32_t hi = d == 0 ? R.p[i].y : d == 1 ? R.p[i].z : d == 2 ? R.p[i].w : R.e[i];
+            return __builtin_amdgcn_alignbyte(hi, lo, sh);
+        };
+        if (lh == 0) sdm[wv][0][li] = half_bits_to_float((R.e[6] >> (8 * sh)) & 0xffffu);
+        // the lane's scales: group g of half hf uses byte 8 hf + 2 g + h of the 16
+        int sc[2][4];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t wd = piece(6, 2 * hf + (g >> 1));
+                sc[hf][g] = static_cast<int>(static_cast<int8_t>((wd >> (8 * (2 * (g & 1) + lh))) & 0xffu));
+            }
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int jb = 4 * hf + g;  // the 32-value block of the super-block
+                half8 xo[2][2];
+                float dvv[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int tr = 32 * tt + li;
+#pragma unroll
+                    for (int sl = 0; sl < 2; ++sl) {
+                        const int c = (4 * jb + 2 * lh + sl) ^ (tr & 15);
+                        xo[tt][sl] = *reinterpret_cast<const half8*>(&xst[256 * tr + 8 * c]);
+                    }
+                    dvv[tt] = sdt[64 * jb + tr];
+                }
+                // sc (q - 32) = sc (l - 16) + 16 sc (u - 1) with q = l + 16 u
+                // (l the ql nibble, u the qh pair): |sc (l - 16)| <= 2048 and
+                // 16 sc (u - 1) = 16 x an integer of at most 256, both exact in
+                // fp16 for every int8 scale; from the fp16 integers 1024 + l and
+                // 1024 + u, one exact add and one exact multiply each
+                const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc[hf][g]));
+                const _Float16 sc16 = static_cast<_Float16>(16.0f * static_cast<float>(sc[hf][g]));
+                const half2 s1 = {scf, scf}, s2 = {sc16, sc16};
+                const half2 o1 = {static_cast<_Float16>(-1040.0f), static_cast<_Float16>(-1040.0f)};
+                const half2 o2 = {static_cast<_Float16>(-1025.0f), static_cast<_Float16>(-1025.0f)};
+                uint32_t a1[8], a2[8];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t l4 = (piece(2 * hf + (g & 1), d) >> (4 * (g >> 1))) & 0x0f0f0f0fu;
+                    const uint32_t u4 = (piece(4 + hf, d) >> (2 * g)) & 0x03030303u;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const uint32_t sel = e == 0 ? 0x04010400u : 0x04030402u;
+                        const half2 pl = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, l4, sel));
+                        const half2 pu = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, u4, sel));
+                        a1[2 * d + e] = __builtin_bit_cast(uint32_t, (pl + o1) * s1);
+                        a2[2 * d + e] = __builtin_bit_cast(uint32_t, (pu + o2) * s2);
+                    }
+                }
+                const half8 w10 = __builtin_bit_cast(half8, make_uint4(a1[0], a1[1], a1[2], a1[3]));
+                const half8 w11 = __builtin_bit_cast(half8, make_uint4(a1[4], a1[5], a1[6], a1[7]));
+                const half8 w20 = __builtin_bit_cast(half8, make_uint4(a2[0], a2[1], a2[2], a2[3]));
+                const half8 w21 = __builtin_bit_cast(half8, make_uint4(a2[4], a2[5], a2[6], a2[7]));
+                floatx16 blk[2];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const floatx16 zero = {};
+                    blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w10, xo[tt][0], zero, 0, 0, 0);
+                    blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w11, xo[tt][1], blk[tt], 0, 0, 0);
+                    blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w20, xo[tt][0], blk[tt], 0, 0, 0);
+                    blk[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w21, xo[tt][1], blk[tt], 0, 0, 0);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        S[tt][r] = jb == 0 ? dvv[tt] * blk[tt][r] : fmaf(dvv[tt], blk[tt][r], S[tt][r]);
+            }
+        // acc += d S (d of the accumulator's rows, from the wave's exchange slots)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 d4 = *reinterpret_cast<const float4*>(&sdm[wv][0][8 * g + 4 * lh]);
+                acc[tt][4 * g] = fmaf(S[tt][4 * g], d4.x, acc[tt][4 * g]);
+                acc[tt][4 * g + 1] = fmaf(S[tt][4 * g + 1], d4.y, acc[tt][4 * g + 1]);
+                acc[tt][4 * g + 2] = fmaf(S[tt][4 * g + 2], d4.z, acc[tt][4 * g + 2]);
+                acc[tt][4 * g + 3] = fmaf(S[tt][4 * g + 3], d4.w, acc[tt][4 * g + 3]);
+            }
+    };
+    auto process = [&](const SbRegs& R, const _Float16* xst, const float* sdt, const _Float16* spt, int32_t sidx) {
+        if constexpr (TYPE == kQ4_K) {
+            (void)sidx;
+            process_q4k(R, xst, sdt, spt);
+        } else {
+            (void)spt;
+            process_q6k(R, xst, sdt, sidx);
+        }
+    };
+
     // super-block s in register set s % 2 and stage s % 3: each starts
     // the loads of the next super-block's weights and of the activations two
     // ahead (into the stage the one before it left), and ends with the
@@ -1680,7 +1822,7 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_q4k_stream_kernel(
 #define GNCX_QS_STEP(RA, RB, XA, DA, PA, XC, DC, PC, OFF) \
     wload(RB, s + (OFF) + 1);                        \
     xload(XC, DC, PC, s + (OFF) + 2);                \
-    process(RA, XA, DA, PA);                         \
+    process(RA, XA, DA, PA, s + (OFF));              \
     step_barrier<kXLoads>();                         \
     if (s + (OFF) + 1 >= nsb) break;
     for (int32_t s = 0; s < nsb; s += 6) {
@@ -1881,7 +2023,7 @@ struct Q4kPlan {
 #ifndef GNCX_Q4K_STREAM
 #define GNCX_Q4K_STREAM 1
 #endif
-// matbatch_q4k_stream_kernel: row groups of 256 x 64 tokens, K split in
+// matbatch_qs_stream_kernel: row groups of 256 x 64 tokens, K split in
 // ranges of whole super-blocks until about 256 work-groups run; unsplit with
 // a multiple of 8 token groups, the XCD-aware order (xmap = token groups).
 Q4kPlan q4k_stream_plan(int32_t b, int32_t k, int32_t n) {
@@ -1996,17 +2138,44 @@ hipError_t launch_q4k1_t(const MbMats& m, const _Float16* xq, const float* dxs, 
     return hipGetLastError();
 }
 
-hipError_t launch_q4ks(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
-                       const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part,
-                       hipStream_t stream) {
+template <int TYPE>
+hipError_t launch_qs(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
+                     const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
     constexpr int BN = 256;
     if (p.kchunk % 256 != 0) return hipErrorInvalidValue;
     const int32_t rg = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN, tg = (b + kQsTok - 1) / kQsTok;
     if (p.xmap > 0 && (p.xmap != tg || tg % 8 != 0 || p.splits != 1)) return hipErrorInvalidValue;
     const dim3 grid = p.xmap > 0 ? dim3(rg * tg) : dim3(rg, tg, p.splits);
-    hipLaunchKernelGGL(matbatch_q4k_stream_kernel<8>, grid, dim3(512), 0, stream, m, row_bytes(kQ4_K, k), xq, dxs,
-                       pq, rscale, b, k, p.kchunk, part, p.xmap);
+    hipLaunchKernelGGL((matbatch_qs_stream_kernel<TYPE, 8>), grid, dim3(512), 0, stream, m, row_bytes(TYPE, k), xq,
+                       dxs, pq, rscale, b, k, p.kchunk, part, p.xmap);
     return hipGetLastError();
+}
+
+#ifndef GNCX_Q6K_STREAM
+#define GNCX_Q6K_STREAM 1
+#endif
+// Q6_K through matbatch_qs_stream_kernel (plan as q4k_stream_plan): the
+// activations as q, d / s and row scales, the product, with split K the
+// reduce
+hipError_t launch_q6ks(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
+                       float* rscale, float* part, hipStream_t stream, const float* up) {
+    const Q4kPlan p = q4k_stream_plan(b, k, n);
+    launch_act_q(x, b, k, xhl, q4k_dxs(xhl, b, k), rscale, nullptr, stream, up);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    MbMats m{};
+    m.w[0] = w;
+    m.y[0] = y;
+    m.n[0] = n;
+    m.ntot = n;
+    m.count = 1;
+    e = launch_qs<kQ6_K>(m, xhl, q4k_dxs(xhl, b, k), nullptr, rscale, b, k, p, part, stream);
+    if (e != hipSuccess || p.splits == 1) return e;
+    RedMats r{};
+    r.y[0] = y;
+    r.end[0] = static_cast<size_t>(b) * n;
+    r.count = 1;
+    return launch_reduce(part, p.splits, r, stream);
 }
 
 // The product of plan p over the matrices of m (w, y, n and count set), then
@@ -2027,7 +2196,7 @@ hipError_t launch_q4k_mats(MbMats& m, _Float16* xhl, const _Float16* pq, const f
     m.ntot = rows;
     r.count = m.count;
     const hipError_t e =
-        p.cfg == 8    ? launch_q4ks(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
+        p.cfg == 8    ? launch_qs<kQ4_K>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
         : q4k_one(p, b) ? launch_q4k1_t<2, 2, 2, 4>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
         : p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
                      : launch_q4k_t<1, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
@@ -2080,7 +2249,9 @@ static size_t pq_bytes(int32_t type, int32_t b, int32_t k) {
 
 size_t matbatch_workspace_bytes(int32_t type, int32_t b, int32_t k, int32_t n) {
     if (type == kBF16) return 256;
-    const int32_t splits = type == kQ4_K ? q4k_plan(b, k, n).splits : mfma_plan(b, k, n).splits;
+    const int32_t splits = type == kQ4_K                     ? q4k_plan(b, k, n).splits
+                           : type == kQ6_K && GNCX_Q6K_STREAM ? q4k_stream_plan(b, k, n).splits
+                                                              : mfma_plan(b, k, n).splits;
     const size_t parts = splits > 1 ? static_cast<size_t>(splits) * b * n * sizeof(float) : 0;
     return xh_bytes(b, k) + pq_bytes(type, b, k) + rscale_bytes(b) + parts + 256;
 }
@@ -2109,7 +2280,9 @@ hipError_t launch_matbatch(int32_t type, const uint8_t* w, const float* x, int32
     case kQ4_0: return launch_mfma<kQ4_0>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
     case kQ8_0: return launch_mfma<kQ8_0>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
     case kQ4_K: return launch_q4k(w, x, b, k, n, y, xhl, pq, rscale, part, stream, up);
-    case kQ6_K: return launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
+    case kQ6_K:
+        return GNCX_Q6K_STREAM ? launch_q6ks(w, x, b, k, n, y, xhl, rscale, part, stream, up)
+                               : launch_mfma<kQ6_K>(w, x, b, k, n, y, xhl, rscale, part, stream, up);
     case kBF16: return up ? hipErrorNotSupported : launch_t<kBF16>(w, x, b, k, n, y, nullptr, nullptr, stream);
     default: return hipErrorInvalidValue;
     }

@@ -282,7 +282,7 @@ def test_matbatch_parity(lib, oracle, t, k, n, b):
 # the steps that hold such a scale.  All rows large, none, and one row in
 # 37 large (single steps of a tile), with K split (k=2048, b=200) and unsplit.
 @pytest.mark.parametrize("mode", ["all", "sparse"])
-@pytest.mark.parametrize("k,n,b", [(2048, 512, 200), (1024, 3000, 300)])
+@pytest.mark.parametrize("k,n,b", [(2048, 512, 200), (1024, 3000, 300), (4096, 600, 64), (768, 300, 7)])
 def test_matbatch_q6k_large_scales(lib, oracle, mode, k, n, b):
     w = synth.make_weights(Q6_K, n, k, seed=8100 + k + n).reshape(n, k // 256, 210)
     rng = np.random.default_rng(8200 + b)
