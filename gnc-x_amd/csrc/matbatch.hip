@@ -1532,16 +1532,25 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_qs_stream_kernel(
     __shared__ __align__(16) float srs[BM];
     __shared__ __align__(16) float sdm[WAVES][2][32];  // per wave: its rows' d and dmin
 
-    // the work-group's row group, token group and K range: with xmap_tg
-    // (a multiple of 8 token groups, no split) the 1-D grid is dealt so that
-    // each XCD (work-group i runs on XCD i % 8) keeps one eighth of the token
-    // groups and walks the row groups, its concurrent work-groups sharing
-    // row groups' weights and its token groups' activations in its L2
+    // the work-group's row group, token group and K range.  Without a split
+    // the 1-D grid can be dealt over the XCDs (work-group i runs on XCD i %
+    // 8, each with its own L2): xmap > 0 (token groups, a multiple of 8):
+    // each XCD keeps one eighth of the token groups and walks the row
+    // groups, its concurrent work-groups sharing row groups' weights and its
+    // token groups' activations; xmap < 0 (-row groups, a multiple of 8):
+    // each XCD keeps one eighth of the row groups, token groups fastest, so
+    // every weight is read by one XCD and the activations by all
     int bx, by, bz;
     if (xmap_tg > 0) {
         const int lin = static_cast<int>(blockIdx.x), xcd = lin & 7, slot = lin >> 3, tpx = xmap_tg / 8;
         bx = slot / tpx;
         by = xcd * tpx + slot % tpx;
+        bz = 0;
+    } else if (xmap_tg < 0) {
+        const int lin = static_cast<int>(blockIdx.x), xcd = lin & 7, slot = lin >> 3;
+        const int rgs = -xmap_tg, tgs = static_cast<int>(gridDim.x) / rgs;
+        bx = xcd * (rgs / 8) + slot / tgs;
+        by = slot % tgs;
         bz = 0;
     } else {
         bx = static_cast<int>(blockIdx.x);
@@ -2035,7 +2044,17 @@ Q4kPlan q4k_stream_plan(int32_t b, int32_t k, int32_t n) {
     const int32_t csb = (nsb + splits - 1) / splits;
     p.kchunk = csb * 256;
     p.splits = (nsb + csb - 1) / csb;
-    p.xmap = p.splits == 1 && tg % 8 == 0 ? static_cast<int32_t>(tg) : 0;
+    // the XCD order with the least L2-miss traffic, counting each XCD's own
+    // reads: by token groups every XCD reads all weights W and its share of
+    // the activations X; by row groups one XCD reads each weight and every
+    // XCD the activations once per round of 32 work-groups (rg tg / 256)
+    p.xmap = 0;
+    if (p.splits == 1) {
+        const double w = static_cast<double>(n) * (k / 256) * 210.0, x = static_cast<double>(b) * k * 2.2;
+        const double by_tok = 8.0 * w + x, by_row = w + 8.0 * x * std::max(1.0, static_cast<double>(wgs) / 256.0);
+        if (rg % 8 == 0 && (tg % 8 != 0 || by_row < by_tok)) p.xmap = -static_cast<int32_t>(rg);
+        else if (tg % 8 == 0) p.xmap = static_cast<int32_t>(tg);
+    }
     return p;
 }
 
@@ -2145,7 +2164,8 @@ hipError_t launch_qs(const MbMats& m, const _Float16* xq, const float* dxs, cons
     if (p.kchunk % 256 != 0) return hipErrorInvalidValue;
     const int32_t rg = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN, tg = (b + kQsTok - 1) / kQsTok;
     if (p.xmap > 0 && (p.xmap != tg || tg % 8 != 0 || p.splits != 1)) return hipErrorInvalidValue;
-    const dim3 grid = p.xmap > 0 ? dim3(rg * tg) : dim3(rg, tg, p.splits);
+    if (p.xmap < 0 && (-p.xmap != rg || rg % 8 != 0 || p.splits != 1)) return hipErrorInvalidValue;
+    const dim3 grid = p.xmap != 0 ? dim3(rg * tg) : dim3(rg, tg, p.splits);
     hipLaunchKernelGGL((matbatch_qs_stream_kernel<TYPE, 8>), grid, dim3(512), 0, stream, m, row_bytes(TYPE, k), xq,
                        dxs, pq, rscale, b, k, p.kchunk, part, p.xmap);
     return hipGetLastError();
