@@ -20,11 +20,13 @@
 // 3e-4).  An int8 MFMA path would be exact too, but its per-32-block scales
 // cost ~3 VALU operations per output and block, several times the
 // matrix-core time of the three fp16 products.
-// Q4_K (the layer format of the prefill workloads) has its own kernel,
-// matbatch_q4k_kernel: its weights are sc q, small integers exact in fp16,
-// with d and dmin fixed per 256-value super-block, so it needs two products
-// per K slice (x_hi, x_lo) and folds d and the dmin min term in once per
-// super-block.
+// Q4_K (the layer format of the prefill workloads) and Q6_K have their own
+// kernel, matbatch_qs_stream_kernel: the weights are small integers exact in
+// fp16 (sc q; sc (q - 32) as two parts) with d (and dmin) fixed per
+// 256-value super-block, and the activations are the quantised q as fp16
+// with each block's scale, so a block's integer dot is exact in one (Q6_K:
+// two) products per K slice; the block scale is applied on the VALU and d
+// and the min term once per super-block.
 // BF16 weights (fp32 activations, cpp:1432-1461) use the slot-dot kernel: a
 // wave per (row, token).
 #include <hip/hip_runtime.h>
@@ -107,7 +109,7 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // term, cpp:1177-1178).
 // With SW the row is the SwiGLU of two rows, x the gates and up the ups
 // (the values gncx_swiglu_activation writes), formed as they are read.
-// With QX (the Q4_K one-product kernel) the quantised values q themselves
+// With QX (the streamed Q4_K and Q6_K kernel) the quantised values q themselves
 // go out instead of the pairs, as fp16 (integers of at most 127, exact):
 // xhl holds 4 of them per task, row-major [B x K], and dxs (set) each
 // 32-block's d / s as fp32 [B x K / 32]; P as above.
@@ -201,8 +203,8 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
     for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) emit(xr[t], t);
 }
 
-// the one-product Q4_K kernel's activations: q as fp16 [B x K], then the
-// blocks' d / s [B x K / 32] (dxs), the P pairs and the row scales
+// the streamed kernel's activations: q as fp16 [B x K], then the blocks'
+// d / s [B x K / 32] (dxs), the P pairs (Q4_K) and the row scales
 void launch_act_q(const float* x, int32_t b, int32_t k, _Float16* xq, float* dxs, float* rscale, _Float16* pq,
                   hipStream_t stream, const float* up) {
     uint2* o = reinterpret_cast<uint2*>(xq);
@@ -676,37 +678,7 @@ __global__ __launch_bounds__(128 * MW, MW == 2 ? 2 : 1) void matbatch_mfma_kerne
         }
 }
 
-// ---- Q4_K: exact integer weights, one scale per super-block ---------------
-//
-// Q4_K weights are d * (sc q) - dmin * m (cpp:1135-1178) with sc q an integer
-// of at most 945, exact in fp16, and d, dmin fixed over a 256-value
-// super-block.  So the weight operand is sc q itself and each 16-wide K slice
-// costs two products (x_hi, x_lo against it); a super-block's accumulator D is
-// folded into the output once per super-block, acc += d D, where d belongs to
-// the lane's weight row (the accumulator column), so it is a per-lane scalar.
-// The min term, dmin sum_j m_j P_j with P_j = d_x sum q over 32-block j (also
-// an fp16 pair, from act_hilo_kernel), is one v_mfma_f32_32x32x8_f16 pair per
-// super-block over its 8 blocks.
-//
-// LDS rows hold 32 fp16 (64 B), the 16-byte segment index XORed with
-// (row / 4) % 4: an MFMA operand read (16 lanes = 16 rows, one segment) and a
-// staging write (16 lanes = 4 rows x 4 segments, or 8 rows x 2) each touch 16
-// distinct groups of 4 banks.
-__device__ __forceinline__ int swz(int row, int seg) { return row * 32 + 8 * (seg ^ ((row >> 2) & 3)); }
-
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-
-// Work-group of MW x NW waves (MW along the tokens, NW along the rows), each
-// owning WM x WN 32x32 accumulator tiles: a Y tile of (32 WM MW) tokens x
-// (32 WN NW) rows.  K advances 32 per step (one 32-block of Q4_K, 8 steps per
-// super-block).  Activations stream through a ring of 4 LDS stages filled by
-// direct-to-LDS buffer loads issued 3 steps ahead (each lane loads the chunk
-// that belongs at its position of the swizzled layout, so no registers hold
-// them); raw weight blocks are loaded two steps ahead into two register sets
-// and written to a double-buffered LDS array as sc q; a super-block's P values
-// are loaded during its predecessor, and its d, dmin and mins are staged by
-// the threads that dequantise its first block.
-constexpr int kXStages = 4;
 
 // vmcnt(N) and lgkmcnt(0), then a work-group barrier with no memory fence.
 // __syncthreads() also waits for the direct-to-LDS loads issued for later
@@ -732,9 +704,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 // block, matrix i's [b x n[i]] part at b npre[i] in it (npre: rows of the
 // matrices before i).
 constexpr int kMaxMbMats = 4;
-#ifndef GNCX_MB_XCD
-#define GNCX_MB_XCD 1
-#endif
 struct MbMats {
     const uint8_t* w[kMaxMbMats];
     float* y[kMaxMbMats];
@@ -743,30 +712,7 @@ struct MbMats {
     int32_t npre[kMaxMbMats];
     int32_t ntot;
     int32_t count;
-    int32_t xcd_a;  // XCD tile order (xcd_tiles): x-tile groups per plane, 0 = grid order
 };
-
-// XCD-aware tile order.  Work-groups are dealt to the 8 XCDs in turn (group
-// i of the grid to XCD i % 8), and each XCD has its own L2, so a tile order
-// decides how many XCDs fetch each operand: in grid order (x fastest, with a
-// multiple of 8 x-tiles) every XCD gets whole columns of x-tiles and reads
-// every token tile's activations, 8 times in all.  With xcd_a = a the
-// (x, y) plane is cut into a x (8 / a) blocks, one per XCD, walked y fastest:
-// each weight tile is then read by 8 / a XCDs and each token tile by a of
-// them (a chosen per launch from the operand sizes).  Requires x-tiles % a,
-// y-tiles % (8 / a) and the plane's size % 8 to be 0.
-__device__ __forceinline__ void xcd_tiles(int xcd_a, int& bx, int& by) {
-    bx = static_cast<int>(blockIdx.x);
-    by = static_cast<int>(blockIdx.y);
-    if (xcd_a <= 0) return;
-    const int gx = static_cast<int>(gridDim.x), gy = static_cast<int>(gridDim.y);
-    const int lin = bx + gx * by;
-    const int xcd = lin & 7, slot = lin >> 3;
-    const int nyb = 8 / xcd_a;
-    const int sxn = gx / xcd_a, syn = gy / nyb;
-    by = (xcd / xcd_a) * syn + slot % syn;
-    bx = (xcd % xcd_a) * sxn + slot / syn;
-}
 
 // The outputs of a split-K reduce: flat partial indices [end[i - 1], end[i])
 // go to y[i] (end[-1] = 0), each y[i] one contiguous [b x n] block.
@@ -775,671 +721,6 @@ struct RedMats {
     size_t end[kMaxMbMats];
     int32_t count;
 };
-
-template <int WM, int WN, int MW, int NW>
-__global__ __launch_bounds__(64 * MW * NW, MW * NW == 4 && WM * WN == 1 ? 2 : 1) void matbatch_q4k_kernel(
-    MbMats mats, size_t rbytes, const _Float16* __restrict xhl, const _Float16* __restrict pq,
-    const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk, float* __restrict part) {
-    constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
-    int bx, by;
-    xcd_tiles(mats.xcd_a, bx, by);
-    const uint8_t* __restrict w = mats.w[0];
-    float* __restrict y = mats.y[0];
-    int32_t n = mats.n[0], tile0 = 0, npre = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxMbMats; ++i) {
-        if (mats.count > i && bx >= mats.tile0[i]) {
-            w = mats.w[i];
-            y = mats.y[i];
-            n = mats.n[i];
-            tile0 = mats.tile0[i];
-            npre = mats.npre[i];
-        }
-    }
-    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage and half
-    static_assert((2 * XBLK) % WAVES == 0, "the same number of activation loads for every wave");
-    static_assert(2 * BN <= THREADS && BM <= THREADS, "one weight piece and one P row per thread at most");
-    // ring stages as separate arrays: the compiler then sees that a
-    // direct-to-LDS load into one stage does not alias reads of another and
-    // inserts no wait for it before those reads
-    __shared__ __align__(16) _Float16 xs0[2][BM * 32], xs1[2][BM * 32], xs2[2][BM * 32], xs3[2][BM * 32];
-    static_assert(kXStages == 4, "four ring arrays");
-    auto xstage = [&](int stage) -> _Float16(*)[BM * 32] {
-        return stage == 0 ? xs0 : stage == 1 ? xs1 : stage == 2 ? xs2 : xs3;
-    };
-    __shared__ __align__(16) _Float16 ws[2][BN * 32];            // [step parity] sc q
-    __shared__ __align__(16) _Float16 sp[2][2][BM * 8];          // [super-block parity][hi, lo] P of 8 blocks
-    __shared__ __align__(16) _Float16 smn[2][BN * 8];            // [super-block parity] mins of 8 blocks
-    __shared__ __align__(8) float sdm[2][BN][2];                 // [super-block parity] d, dmin
-    // the tile's token scales, loaded with the first loads: read from memory
-    // at the output they were one dependent load of every wave at the moment
-    // all work-groups store (2.5 us at B = 64, 5 us at B = 512); one dword per
-    // lane of every wave, entries from BM on unused
-    __shared__ __align__(16) float srs[THREADS];
-    // The raw weights stream through LDS as well, by direct-to-LDS loads
-    // with no registers in flight (register loads of them put memory waits on
-    // every step): a ring of 4 stages of each row's 32 qs bytes of a step's
-    // sub-block pair, and per super-block parity the rows' 16-byte headers and
-    // the tokens' P pairs, loaded at the 5th step of the super-block before.
-    // Every wave issues the same number of these loads (vmcnt is per wave).
-    static_assert((BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
-                      (2 * BM * 16) % (THREADS * 4) == 0,
-                  "the same number of weight, header and P loads for every wave");
-    __shared__ __align__(16) uint8_t wq0[BN * 32], wq1[BN * 32], wq2[BN * 32], wq3[BN * 32];
-    __shared__ __align__(16) uint8_t whd[2][BN * 16];  // [super-block parity] raw headers
-    auto wstage = [&](int stage) -> uint8_t* { return stage == 0 ? wq0 : stage == 1 ? wq1 : stage == 2 ? wq2 : wq3; };
-    constexpr int kWLoads = BN * 32 / (THREADS * 16);                                  // per wave and step
-    constexpr int kHLoads = BN * 16 / (THREADS * 4) + 2 * BM * 16 / (THREADS * 4);   // per super-block
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv % MW, wn = wv / MW;
-    const int li = lane & 31, lh = lane >> 5;
-    const int32_t t0 = by * BM, n0 = (bx - tile0) * BN;
-    const int32_t kb = blockIdx.z * kchunk;
-    const int32_t ke = min(k, kb + kchunk);
-    const int32_t nsb = (ke - kb) / 256;
-    const int32_t sbs_row = k / 256;
-
-    const int32_t rows_here = min(BM, b - t0);
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(xhl + static_cast<size_t>(t0) * k * 2), static_cast<short>(0),
-        rows_here * k * 2 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * sbs_row * 16), static_cast<short>(0),
-        rows_here * sbs_row * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-    const int wrow = tid >> 1, whalf = tid & 1;
-    const int32_t wrows_here = min(BN, n - n0);
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
-        wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
-
-    floatx16 acc[WM][WN], D[WM][WN];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = D[i][j][r] = 0.0f;
-
-    // activations of the step at k0 into ring stage `stage`: load q of the
-    // step is block q % XBLK (token rows 16 blk .. + 16) of half q / XBLK,
-    // 64 lanes x 16 B; lane L lands at segment position L % 4 of row L / 4,
-    // which holds logical segment (L % 4) ^ ((row / 4) % 4).  Past the
-    // range: zeros.
-    constexpr int kXLoads = 2 * XBLK / WAVES;  // ring loads per wave and step
-    auto dma_x = [&](int stage, int32_t k0) {
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int q = i * WAVES + wv, blk = q % XBLK, half = q / XBLK;
-            const int row = 16 * blk + (lane >> 2);
-            const int lseg = (lane & 3) ^ ((row >> 2) & 3);
-            const int32_t off = k0 < ke ? (row * k + k0 + 8 * lseg) * 2 * static_cast<int32_t>(sizeof(_Float16))
-                                        : kMfOob;
-            _Float16(*xs)[BM * 32] = xstage(stage);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)&xs[half][blk * 16 * 32], 16, off + 16 * half, 0,
-                                                     0, 0);
-        }
-    };
-    // raw qs of the step at k0 (each row's 32 bytes of its sub-block
-    // pair) into ring stage `stage`, 16 bytes per lane in row order
-    auto dma_w = [&](int stage, int32_t k0) {
-        {
-            const int32_t kk = k0 < ke ? k0 : 0;
-            const int32_t koff = (kk / 256) * 144 + 16 + 32 * ((kk % 256) / 64);
-#pragma unroll
-            for (int i = 0; i < kWLoads; ++i) {
-                const int piece = (i * WAVES + wv) * 64 + lane;  // two 16-byte pieces per row
-                const int row = piece >> 1;
-                const int32_t off = k0 < ke && row < wrows_here
-                                        ? row * static_cast<int32_t>(rbytes) + koff + 16 * (piece & 1)
-                                        : kMfOob;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(wstage(stage) + (i * WAVES + wv) * 1024), 16,
-                                                         off, 0, 0, 0);
-            }
-        }
-    };
-    // the rows' headers (d, dmin, scales) and the tokens' P pairs of the
-    // super-block at s0 into parity `par`, 4 bytes per lane in row order
-    auto dma_hp = [&](int par, int32_t s0) {
-        {
-            const bool in = s0 < ke;
-            // P: load q is dwords (q % PH) 64 .. + 64 of half q / PH
-            constexpr int HL = BN * 16 / (THREADS * 4), PH = BM * 16 / (64 * 4), PL = 2 * PH / WAVES;
-#pragma unroll
-            for (int i = 0; i < HL; ++i) {
-                const int dw = (i * WAVES + wv) * 64 + lane;
-                const int row = dw >> 2;
-                const int32_t off = in && row < wrows_here
-                                        ? row * static_cast<int32_t>(rbytes) + (s0 / 256) * 144 + 4 * (dw & 3)
-                                        : kMfOob;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(&whd[par][(i * WAVES + wv) * 256]), 4, off, 0,
-                                                         0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < PL; ++i) {
-                const int q = i * WAVES + wv, h = q / PH, qq = q % PH;
-                const int dw = qq * 64 + lane;
-                const int row = dw >> 2;
-                const int32_t off = in && row < rows_here
-                                        ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) *
-                                                  static_cast<int32_t>(sizeof(_Float16)) +
-                                              4 * (dw & 3)
-                                        : kMfOob;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][qq * 128]), 4, off, 0, 0, 0);
-            }
-        }
-    };
-    // weights of the step at k0 (ring stage `set`, headers of parity `hpar`)
-    // into LDS buffer `buf`; at a super-block's first step also its d, dmin
-    // and mins, parity hpar
-    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int hpar) {
-        if (tid < 2 * BN) {
-            const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
-            const u32x4 hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
-            const u32x4 qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
-            int sc, mn;
-            k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
-            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
-            // sc q as fp16, two codes per instruction: a byte permute puts
-            // codes a and c under the exponent of 1024 (fp16 bits 0x6400 | a
-            // are 1024 + a), and one packed fma gives (1024 + a) sc - 1024 sc
-            // = a sc with a single rounding of an exact value (a sc <= 945)
-            const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
-            const _Float16 off = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
-            const half2 s2 = {scf, scf}, m2 = {off, off};
-            uint32_t o[8];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t x = (qw[d] >> sh) & 0x0f0f0f0fu;
-                const half2 p0 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
-                const half2 p1 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
-                o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p0, s2, m2));
-                o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p1, s2, m2));
-            }
-            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
-            if (sb_first && whalf == 0) {
-                sdm[hpar][wrow][0] = half_bits_to_float(hh.x & 0xffffu);
-                sdm[hpar][wrow][1] = half_bits_to_float(hh.x >> 16);
-                uint32_t m2[4];
-#pragma unroll
-                for (int jj = 0; jj < 8; jj += 2) {
-                    int s0, m0, s1, m1;
-                    k4_scale_min(jj, hh.y, hh.z, hh.w, s0, m0);
-                    k4_scale_min(jj + 1, hh.y, hh.z, hh.w, s1, m1);
-                    const _Float16 h0 = static_cast<_Float16>(static_cast<float>(m0));
-                    const _Float16 h1 = static_cast<_Float16>(static_cast<float>(m1));
-                    m2[jj / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
-                                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
-                }
-                *reinterpret_cast<uint4*>(&smn[hpar][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
-            }
-        }
-    };
-    // two K16 slices of one step (D starts each super-block at 0)
-    auto compute = [&](int stage, int buf) {
-        _Float16(*xs)[BM * 32] = xstage(stage);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            half8 ah[WM], al[WM], bw[WN];
-#pragma unroll
-            for (int i = 0; i < WM; ++i) {
-                const int o = swz(wm * 32 * WM + 32 * i + li, 2 * kk + lh);
-                ah[i] = *reinterpret_cast<const half8*>(&xs[0][o]);
-                al[i] = *reinterpret_cast<const half8*>(&xs[1][o]);
-            }
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                bw[j] = *reinterpret_cast<const half8*>(&ws[buf][swz(wn * 32 * WN + 32 * j + li, 2 * kk + lh)]);
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], D[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-                    D[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], D[i][j], 0, 0, 0);
-        }
-    };
-    // acc += d D - dmin (P . m) for super-block parity sbp
-    auto fold = [&](int sbp) {
-        float dv[WN], mv[WN];
-        half4 mn[WN];
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int r = wn * 32 * WN + 32 * j + li;
-            dv[j] = sdm[sbp][r][0];
-            mv[j] = -sdm[sbp][r][1];
-            mn[j] = *reinterpret_cast<const half4*>(&smn[sbp][r * 8 + 4 * lh]);
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(D[i][j][r], dv[j], acc[i][j][r]);
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const int r = wm * 32 * WM + 32 * i + li;
-            const half4 ph = *reinterpret_cast<const half4*>(&sp[sbp][0][r * 8 + 4 * lh]);
-            const half4 pl = *reinterpret_cast<const half4*>(&sp[sbp][1][r * 8 + 4 * lh]);
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-#pragma unroll
-                for (int r2 = 0; r2 < 16; ++r2) D[i][j][r2] = 0.0f;
-                D[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(ph, mn[j], D[i][j], 0, 0, 0);
-                D[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(pl, mn[j], D[i][j], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    acc[i][j][r] = fmaf(D[i][j][r], mv[j], acc[i][j][r]);
-                    D[i][j][r] = 0.0f;
-                }
-    };
-
-    // Prologue: the headers and P of super-block 0, then steps 0-2 of
-    // activations and raw weights into ring stages 0-2; step 0's weights are
-    // dequantised once the first three groups of loads are in LDS for every
-    // wave.
-    {
-        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(rscale + t0), static_cast<short>(0), rows_here * static_cast<int32_t>(sizeof(float)),
-            0x00020000);
-        const int32_t off = tid < rows_here ? tid * static_cast<int32_t>(sizeof(float)) : kMfOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (lds_ptr)&srs[64 * wv], 4, off, 0, 0, 0);
-    }
-    dma_hp(0, kb);
-    dma_x(0, kb);
-    dma_w(0, kb);
-    dma_x(1, kb + 32);
-    dma_w(1, kb + 32);
-    dma_x(2, kb + 64);
-    dma_w(2, kb + 64);
-    step_barrier<2 * (kXLoads + kWLoads)>();
-    lstore(0, 0, kb, true, 0);
-    step_barrier<kXLoads + kWLoads>();
-    // Per step: the activation and raw-weight ring loads 3 steps ahead (plus
-    // the next super-block's headers and P at its 5th step); compute; the
-    // next step's weights dequantised into LDS; then the barrier (below).
-    for (int32_t sb = 0; sb < nsb; ++sb) {
-        const int32_t s0 = kb + sb * 256;
-        const int sbp = sb & 1;
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int32_t k0 = s0 + 32 * st;
-            const int buf = st & 1;  // 8 steps per super-block keep every parity static
-            auto issue_loads = [&]() {
-                dma_x((st + 3) & 3, k0 + 96);
-                dma_w((st + 3) & 3, k0 + 96);
-                if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
-            };
-            // the step dequantised here is k0 + 32: its raw weights' ring
-            // stage and its super-block's parity
-            const int wset = (st + 1) & 3;
-            const int hpar = st == 7 ? (sbp ^ 1) : sbp;
-            // the two waves on each SIMD (waves w and w + WAVES / 2) take the
-            // step's MFMA and VALU phases in opposite orders (staging writes
-            // the other weight buffer), so the barrier does not line up both
-            // waves' matrix-core work; each issues its loads as its MFMA phase
-            // starts, so the CU's memory pipeline takes half of the step's
-            // requests at a time (all of them right after the barrier stalled
-            // the issuing waves for about 400 clocks)
-            if (wv < WAVES / 2) {
-                issue_loads();
-                compute(st & 3, buf);
-                if (st == 7) fold(sbp);
-                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
-            } else {
-                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
-                issue_loads();
-                compute(st & 3, buf);
-                if (st == 7) fold(sbp);
-            }
-            // the next step reads loads issued one and two steps ago; only
-            // this step's may still run (and at the 5th step its headers and P)
-            if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
-            else step_barrier<kXLoads + kWLoads>();
-        }
-    }
-    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int32_t mm = n0 + wn * 32 * WN + 32 * j + li;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int32_t t = t0 + wm * 32 * WM + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * srs[t - t0];
-            }
-        }
-}
-
-// ---- Q4_K, one product per K slice ------------------------------------------
-//
-// The weights sc q and the quantised activations q are both small integers,
-// exact in fp16, so one v_mfma_f32_32x32x16_f16 per K slice gives a
-// 32-block's integer dot, sum (sc q) q (at most 32 x 945 x 127 < 2^24, exact
-// in fp32 whatever the order of the additions).  The block's activation
-// scale d_x / s then multiplies it on the VALU, S += (d_x / s) blk, and S
-// folds into the output once per super-block as acc += d S, with the min
-// term as in matbatch_q4k_kernel.  Against the two-product kernel this is
-// half the matrix-core work and half the activation bytes in LDS, for 16
-// fp32 fmas per accumulator tile and block.  The weights are the MFMA's A
-// operand (accumulator rows) and the tokens its B operand (columns), so a
-// lane's accumulator column is one token and its block scale one value; d
-// and dmin vary along the lane's 16 registers (4 x 4 consecutive rows).
-// Loads, ring stages and staging are those of matbatch_q4k_kernel, the
-// activation ring holding q alone, and the super-block loads bringing the
-// blocks' scales with P.
-template <int WM, int WN, int MW, int NW>
-__global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
-    MbMats mats, size_t rbytes, const _Float16* __restrict xq, const float* __restrict dxs,
-    const _Float16* __restrict pq, const float* __restrict rscale, int32_t b, int32_t k, int32_t kchunk,
-    float* __restrict part) {
-    constexpr int WAVES = MW * NW, THREADS = 64 * WAVES;
-    int bx, by;
-    xcd_tiles(mats.xcd_a, bx, by);
-    const uint8_t* __restrict w = mats.w[0];
-    float* __restrict y = mats.y[0];
-    int32_t n = mats.n[0], tile0 = 0, npre = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxMbMats; ++i) {
-        if (mats.count > i && bx >= mats.tile0[i]) {
-            w = mats.w[i];
-            y = mats.y[i];
-            n = mats.n[i];
-            tile0 = mats.tile0[i];
-            npre = mats.npre[i];
-        }
-    }
-    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    constexpr int XBLK = BM / 16;  // 1 KB blocks (16 token rows) per stage
-    static_assert(XBLK % WAVES == 0, "the same number of activation loads for every wave");
-    static_assert(2 * BN <= THREADS && BM <= THREADS, "one weight piece and one P row per thread at most");
-    __shared__ __align__(16) _Float16 xs0[BM * 32], xs1[BM * 32], xs2[BM * 32], xs3[BM * 32];
-    static_assert(kXStages == 4, "four ring arrays");
-    auto xstage = [&](int stage) -> _Float16* { return stage == 0 ? xs0 : stage == 1 ? xs1 : stage == 2 ? xs2 : xs3; };
-    __shared__ __align__(16) _Float16 ws[2][BN * 32];    // [step parity] sc q
-    __shared__ __align__(16) _Float16 sp[2][2][BM * 8];  // [super-block parity][hi, lo] P of 8 blocks
-    __shared__ __align__(16) float sdx[2][BM * 8];       // [super-block parity] d_x / s of 8 blocks
-    __shared__ __align__(16) _Float16 smn[2][BN * 8];    // [super-block parity] mins of 8 blocks
-    __shared__ __align__(16) float sdm[2][2][BN];        // [super-block parity][d, dmin]
-    __shared__ __align__(16) float srs[THREADS];         // the tile's token scales (entries from BM on unused)
-    static_assert((BN * 32) % (THREADS * 16) == 0 && (BN * 16) % (THREADS * 4) == 0 &&
-                      (2 * BM * 16) % (THREADS * 4) == 0 && (BM * 8 * 4) % (THREADS * 4) == 0,
-                  "the same number of weight, header, P and scale loads for every wave");
-    __shared__ __align__(16) uint8_t wq0[BN * 32], wq1[BN * 32], wq2[BN * 32], wq3[BN * 32];
-    __shared__ __align__(16) uint8_t whd[2][BN * 16];
-    auto wstage = [&](int stage) -> uint8_t* { return stage == 0 ? wq0 : stage == 1 ? wq1 : stage == 2 ? wq2 : wq3; };
-    constexpr int kXLoads = XBLK / WAVES;
-    constexpr int kWLoads = BN * 32 / (THREADS * 16);
-    constexpr int kDLoads = BM * 8 / THREADS;
-    constexpr int kHLoads = BN * 16 / (THREADS * 4) + 2 * BM * 16 / (THREADS * 4) + kDLoads;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv % MW, wn = wv / MW;
-    const int li = lane & 31, lh = lane >> 5;
-    const int32_t t0 = by * BM, n0 = (bx - tile0) * BN;
-    const int32_t kb = blockIdx.z * kchunk;
-    const int32_t ke = min(k, kb + kchunk);
-    const int32_t nsb = (ke - kb) / 256;
-    const int32_t sbs_row = k / 256;
-
-    const int32_t rows_here = min(BM, b - t0);
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(xq + static_cast<size_t>(t0) * k), static_cast<short>(0),
-        rows_here * k * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<_Float16*>(pq + static_cast<size_t>(t0) * sbs_row * 16), static_cast<short>(0),
-        rows_here * sbs_row * 16 * static_cast<int32_t>(sizeof(_Float16)), 0x00020000);
-    const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(dxs + static_cast<size_t>(t0) * (k / 32)), static_cast<short>(0),
-        rows_here * (k / 32) * static_cast<int32_t>(sizeof(float)), 0x00020000);
-    const int wrow = tid >> 1, whalf = tid & 1;
-    const int32_t wrows_here = min(BN, n - n0);
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(w + static_cast<size_t>(n0) * rbytes), static_cast<short>(0),
-        wrows_here * static_cast<int32_t>(rbytes), 0x00020000);
-
-    floatx16 acc[WM][WN], S[WM][WN];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = S[i][j][r] = 0.0f;
-
-    // q of the step at k0 into ring stage `stage`: load q is block q (token
-    // rows 16 q .. + 16), 64 lanes x 16 B, lane L at segment position L % 4
-    // of row L / 4 (logical segment (L % 4) ^ ((row / 4) % 4)); past the
-    // range: zeros
-    auto dma_x = [&](int stage, int32_t k0) {
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int blk = i * WAVES + wv;
-            const int row = 16 * blk + (lane >> 2);
-            const int lseg = (lane & 3) ^ ((row >> 2) & 3);
-            const int32_t off = k0 < ke ? (row * k + k0 + 8 * lseg) * static_cast<int32_t>(sizeof(_Float16)) : kMfOob;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_ptr)(xstage(stage) + blk * 16 * 32), 16, off, 0, 0, 0);
-        }
-    };
-    auto dma_w = [&](int stage, int32_t k0) {
-        const int32_t kk = k0 < ke ? k0 : 0;
-        const int32_t koff = (kk / 256) * 144 + 16 + 32 * ((kk % 256) / 64);
-#pragma unroll
-        for (int i = 0; i < kWLoads; ++i) {
-            const int piece = (i * WAVES + wv) * 64 + lane;
-            const int row = piece >> 1;
-            const int32_t off =
-                k0 < ke && row < wrows_here ? row * static_cast<int32_t>(rbytes) + koff + 16 * (piece & 1) : kMfOob;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(wstage(stage) + (i * WAVES + wv) * 1024), 16, off,
-                                                     0, 0, 0);
-        }
-    };
-    // headers, P pairs and block scales of the super-block at s0 into parity par
-    auto dma_hp = [&](int par, int32_t s0) {
-        const bool in = s0 < ke;
-        constexpr int HL = BN * 16 / (THREADS * 4), PH = BM * 16 / (64 * 4), PL = 2 * PH / WAVES;
-#pragma unroll
-        for (int i = 0; i < HL; ++i) {
-            const int dw = (i * WAVES + wv) * 64 + lane;
-            const int row = dw >> 2;
-            const int32_t off =
-                in && row < wrows_here ? row * static_cast<int32_t>(rbytes) + (s0 / 256) * 144 + 4 * (dw & 3) : kMfOob;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr)(&whd[par][(i * WAVES + wv) * 256]), 4, off, 0, 0,
-                                                     0);
-        }
-#pragma unroll
-        for (int i = 0; i < PL; ++i) {
-            const int q = i * WAVES + wv, h = q / PH, qq = q % PH;
-            const int dw = qq * 64 + lane;
-            const int row = dw >> 2;
-            const int32_t off = in && row < rows_here
-                                    ? ((row * sbs_row + s0 / 256) * 16 + 8 * h) * static_cast<int32_t>(sizeof(_Float16)) +
-                                          4 * (dw & 3)
-                                    : kMfOob;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, (lds_ptr)(&sp[par][h][qq * 128]), 4, off, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kDLoads; ++i) {
-            const int dw = (i * WAVES + wv) * 64 + lane;  // token row dw / 8, block dw % 8
-            const int row = dw >> 3;
-            const int32_t off =
-                in && row < rows_here ? (row * (k / 32) + s0 / 32 + (dw & 7)) * static_cast<int32_t>(sizeof(float))
-                                      : kMfOob;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_ptr)(&sdx[par][(i * WAVES + wv) * 64]), 4, off, 0, 0,
-                                                     0);
-        }
-    };
-    auto lstore = [&](int set, int buf, int32_t k0, bool sb_first, int hpar) {
-        if (tid < 2 * BN) {
-            const int j = (k0 % 256) / 32, sh = 4 * (j & 1);
-            const u32x4 hh = *reinterpret_cast<const u32x4*>(&whd[hpar][wrow * 16]);
-            const u32x4 qq = *reinterpret_cast<const u32x4*>(wstage(set) + wrow * 32 + 16 * whalf);
-            int sc, mn;
-            k4_scale_min(j, hh.y, hh.z, hh.w, sc, mn);
-            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w};
-            const _Float16 scf = static_cast<_Float16>(static_cast<float>(sc));
-            const _Float16 off = static_cast<_Float16>(-1024.0f * static_cast<float>(sc));
-            const half2 s2 = {scf, scf}, m2 = {off, off};
-            uint32_t o[8];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t x = (qw[d] >> sh) & 0x0f0f0f0fu;
-                const half2 p0 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u));
-                const half2 p1 = __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u));
-                o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p0, s2, m2));
-                o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(p1, s2, m2));
-            }
-            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf)]) = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4*>(&ws[buf][swz(wrow, 2 * whalf + 1)]) = make_uint4(o[4], o[5], o[6], o[7]);
-            if (sb_first && whalf == 0) {
-                sdm[hpar][0][wrow] = half_bits_to_float(hh.x & 0xffffu);
-                sdm[hpar][1][wrow] = half_bits_to_float(hh.x >> 16);
-                uint32_t m2[4];
-#pragma unroll
-                for (int jj = 0; jj < 8; jj += 2) {
-                    int s0, m0, s1, m1;
-                    k4_scale_min(jj, hh.y, hh.z, hh.w, s0, m0);
-                    k4_scale_min(jj + 1, hh.y, hh.z, hh.w, s1, m1);
-                    const _Float16 h0 = static_cast<_Float16>(static_cast<float>(m0));
-                    const _Float16 h1 = static_cast<_Float16>(static_cast<float>(m1));
-                    m2[jj / 2] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h0)) |
-                                 (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
-                }
-                *reinterpret_cast<uint4*>(&smn[hpar][wrow * 8]) = make_uint4(m2[0], m2[1], m2[2], m2[3]);
-            }
-        }
-    };
-    // block st of super-block parity sbp: its integer dots, one tile at a
-    // time (both K slices' operands first), scaled into S
-    auto compute = [&](int stage, int buf, int sbp, int st) {
-        const _Float16* xs = xstage(stage);
-        half8 xa[2][WM], wa[2][WN];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-                xa[kk][i] = *reinterpret_cast<const half8*>(&xs[swz(wm * 32 * WM + 32 * i + li, 2 * kk + lh)]);
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-                wa[kk][j] = *reinterpret_cast<const half8*>(&ws[buf][swz(wn * 32 * WN + 32 * j + li, 2 * kk + lh)]);
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const float dv = sdx[sbp][(wm * 32 * WM + 32 * i + li) * 8 + st];
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-                const floatx16 zero = {};
-                floatx16 blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[0][j], xa[0][i], zero, 0, 0, 0);
-                blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[1][j], xa[1][i], blk, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) S[i][j][r] = fmaf(dv, blk[r], S[i][j][r]);
-            }
-            // the tiles of one token tile at a time: hoisting every tile's
-            // products ahead of the fmas would hold all their results at once
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    // acc += d S - dmin (m . P) for super-block parity sbp; S restarts at 0
-    auto fold = [&](int sbp) {
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-            const int rb = wn * 32 * WN + 32 * j + 4 * lh;  // rows rb + 8 g + 0..3 in registers 4 g + 0..3
-            const half4 mn = *reinterpret_cast<const half4*>(&smn[sbp][(wn * 32 * WN + 32 * j + li) * 8 + 4 * lh]);
-#pragma unroll
-            for (int i = 0; i < WM; ++i) {
-                const int t = wm * 32 * WM + 32 * i + li;
-                const half4 ph = *reinterpret_cast<const half4*>(&sp[sbp][0][t * 8 + 4 * lh]);
-                const half4 pl = *reinterpret_cast<const half4*>(&sp[sbp][1][t * 8 + 4 * lh]);
-                const floatx16 zero = {};
-                floatx16 M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn, ph, zero, 0, 0, 0);
-                M = __builtin_amdgcn_mfma_f32_32x32x8f16(mn, pl, M, 0, 0, 0);
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 d4 = *reinterpret_cast<const float4*>(&sdm[sbp][0][rb + 8 * g]);
-                    const float4 m4 = *reinterpret_cast<const float4*>(&sdm[sbp][1][rb + 8 * g]);
-                    const float dq[4] = {d4.x, d4.y, d4.z, d4.w}, mq[4] = {m4.x, m4.y, m4.z, m4.w};
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int r = 4 * g + q;
-                        acc[i][j][r] = fmaf(S[i][j][r], dq[q], acc[i][j][r]);
-                        acc[i][j][r] = fmaf(M[r], -mq[q], acc[i][j][r]);
-                        S[i][j][r] = 0.0f;
-                    }
-                }
-            }
-        }
-    };
-
-    {
-        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(rscale + t0), static_cast<short>(0), rows_here * static_cast<int32_t>(sizeof(float)),
-            0x00020000);
-        const int32_t off = tid < rows_here ? tid * static_cast<int32_t>(sizeof(float)) : kMfOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (lds_ptr)&srs[64 * wv], 4, off, 0, 0, 0);
-    }
-    dma_hp(0, kb);
-    dma_x(0, kb);
-    dma_w(0, kb);
-    dma_x(1, kb + 32);
-    dma_w(1, kb + 32);
-    dma_x(2, kb + 64);
-    dma_w(2, kb + 64);
-    step_barrier<2 * (kXLoads + kWLoads)>();
-    lstore(0, 0, kb, true, 0);
-    step_barrier<kXLoads + kWLoads>();
-    for (int32_t sb = 0; sb < nsb; ++sb) {
-        const int32_t s0 = kb + sb * 256;
-        const int sbp = sb & 1;
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int32_t k0 = s0 + 32 * st;
-            const int buf = st & 1;
-            auto issue_loads = [&]() {
-                dma_x((st + 3) & 3, k0 + 96);
-                dma_w((st + 3) & 3, k0 + 96);
-                if (st == 4) dma_hp(sbp ^ 1, s0 + 256);
-            };
-            const int wset = (st + 1) & 3;
-            const int hpar = st == 7 ? (sbp ^ 1) : sbp;
-            if (wv < WAVES / 2) {
-                issue_loads();
-                compute(st & 3, buf, sbp, st);
-                if (st == 7) fold(sbp);
-                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
-            } else {
-                if (k0 + 32 < ke) lstore(wset, buf ^ 1, k0 + 32, st == 7, hpar);
-                issue_loads();
-                compute(st & 3, buf, sbp, st);
-                if (st == 7) fold(sbp);
-            }
-            if (st == 4) step_barrier<kXLoads + kWLoads + kHLoads>();
-            else step_barrier<kXLoads + kWLoads>();
-        }
-    }
-    // lane: token t0 + wm 32 WM + 32 i + li, rows 8 g + 4 lh + 0..3 of tile j in registers 4 g + 0..3
-    float* dst = gridDim.z > 1 ? part + (static_cast<size_t>(blockIdx.z) * mats.ntot + npre) * b : y;
-#pragma unroll
-    for (int i = 0; i < WM; ++i) {
-        const int32_t tl = wm * 32 * WM + 32 * i + li, t = t0 + tl;
-        const float rs = srs[tl];
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int32_t mm = n0 + wn * 32 * WN + 32 * j + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (t < b && mm < n) dst[static_cast<size_t>(t) * n + mm] = acc[i][j][r] * rs;
-            }
-    }
-}
 
 // ---- Q4_K and Q6_K, weights streamed through registers ------------------------
 //
@@ -1452,15 +733,13 @@ __global__ __launch_bounds__(64 * MW * NW, 2) void matbatch_q4k1_kernel(
 // is values 16 h + 8 s .. + 8 in lane half h, and the activation operand is
 // read from LDS in the same order, so each slice's products pair every
 // value with its own activation.  The activations (q as fp16, the blocks'
-// d / s and the P pairs of the one-product kernel) stream through three LDS
+// d / s and, for the min term, the P pairs) stream through three LDS
 // stages, one super-block per stage, filled by direct-to-LDS loads two
 // super-blocks ahead, issued with the next super-block's weights as a
 // super-block starts; one barrier per super-block.  Each block's
 // integer dot is one product, scaled on the VALU by the block's d_x / s into
 // a super-block accumulator, and d, dmin and the min term fold once per
-// super-block, as in matbatch_q4k1_kernel (the same operations in the same
-// order: with whole K it gives that kernel's results bit for bit).  Against
-// the tiled kernels nothing is staged, dequantised or barriered per 32
+// super-block.  No weight is staged in LDS and nothing is barriered per 32
 // values: a work-group's weights are read once, by the wave that uses them.
 // With gridDim.z > 1 the work-group's result is a split-K partial.
 // The result leaves through LDS, so that each store instruction writes one
@@ -1648,8 +927,11 @@ __global__ __launch_bounds__(64 * RT, 1) void matbatch_qs_stream_kernel(
                                    {R.q[2].x, R.q[2].y, R.q[2].z, R.q[2].w},
                                    {R.q[3].x, R.q[3].y, R.q[3].z, R.q[3].w}};
         // block j's operands: activations of both token tiles and K slices,
-        // their block scales, and the weights as sc q (two codes per
-        // instruction, as in the tiled kernels)
+        // their block scales, and the weights as sc q, two codes per
+        // instruction: a byte permute puts codes a and c under the exponent
+        // of 1024 (fp16 bits 0x6400 | a are 1024 + a), and one packed fma
+        // gives (1024 + a) sc - 1024 sc = a sc with a single rounding of an
+        // exact value (a sc <= 945)
         auto operands = [&](int j, half8 (&xo)[2][2], float (&dvv)[2], half8 (&wq)[2]) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -2010,33 +1292,16 @@ hipError_t launch_mfma(const uint8_t* w, const float* x, int32_t b, int32_t k, i
     return launch_reduce(part, p.splits, r, stream);
 }
 
-// Q4_K tiles: (waves along tokens, along rows, tiles per wave along each)
+// A launch plan of matbatch_qs_stream_kernel: K ranges and the XCD order
 struct Q4kPlan {
-    int cfg;  // 0: 128 tokens x 256 rows, 4: 64 x 256 (8 waves, one work-group per CU), 8: streamed weights
     int32_t splits, kchunk;
-    int32_t xmap = 0;  // streamed weights: token groups of the XCD-aware order (0: grid order)
+    int32_t xmap = 0;  // token groups of the XCD-aware order (> 0), minus row groups (< 0), 0: grid order
 };
 
-// Tiles of 256 rows with K split into ranges of whole super-blocks until
-// about 256 work-groups run (one per CU): 64 tokens up to B = 128, 128 tokens
-// above.  Measured full calls (quantisation, product, reduce) against the
-// plans before them (128 x 256 only from 192 tiles, else 128 x 128 from 192
-// tiles, else 64 x 64 with K split to about 512 work-groups): Q4_K 4096 x 4096
-// at B = 256 / 512 / 1024: 48 / 68 / 115 against 66 / 108 / 140 us; 4096 ->
-// 14336 at B = 256 / 384: 103 / 157 against 130 / 235 us; 12288 -> 4096 at
-// B = 256 / 512: 93 / 158 against 170 / 305 us; B = 2048 unchanged (no split).
-// The 64-token tiles against 64 x 64 tiles with K split (B <= 64) or 128 x 256
-// (B = 100, 128): 4096 -> 14336 at B = 64: 46 against 54 us; 12288 -> 4096 at
-// B = 64: 49 against 58; 4096 x 4096 at B = 32 / 64 / 100 / 128: 23.6 / 28.9 /
-// 32.9 / 34.3 against 25.7 / 29.1 / 36.6 / 37.8 us.
-#ifndef GNCX_Q4K_STREAM
-#define GNCX_Q4K_STREAM 1
-#endif
-// matbatch_qs_stream_kernel: row groups of 256 x 64 tokens, K split in
-// ranges of whole super-blocks until about 256 work-groups run; unsplit with
-// a multiple of 8 token groups, the XCD-aware order (xmap = token groups).
+// Row groups of 256 x 64 tokens, K split in ranges of whole super-blocks
+// until about 256 work-groups run (one per CU).
 Q4kPlan q4k_stream_plan(int32_t b, int32_t k, int32_t n) {
-    Q4kPlan p{8, 1, k};
+    Q4kPlan p{1, k};
     const int32_t nsb = k / 256;
     const int64_t rg = (n + 255) / 256, tg = (b + kQsTok - 1) / kQsTok, wgs = rg * tg;
     int32_t splits = wgs >= 256 ? 1 : static_cast<int32_t>(256 / wgs);
@@ -2058,103 +1323,18 @@ Q4kPlan q4k_stream_plan(int32_t b, int32_t k, int32_t n) {
     return p;
 }
 
-Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) {
-    if (GNCX_Q4K_STREAM && k >= 256) return q4k_stream_plan(b, k, n);
-    const int bm = b > 128 ? 128 : 64;
-    const int64_t t = static_cast<int64_t>((n + 255) / 256) * ((b + bm - 1) / bm);
-    int32_t splits = static_cast<int32_t>(256 / t);
-    if (splits > k / 256) splits = k / 256;
-    if (splits < 1) splits = 1;
-    const int32_t kchunk = (k / 256 + splits - 1) / splits * 256;
-    return {b > 128 ? 0 : 4, (k + kchunk - 1) / kchunk, kchunk};
-}
+Q4kPlan q4k_plan(int32_t b, int32_t k, int32_t n) { return q4k_stream_plan(b, k, n); }
 
-// rows per x-tile of both Q4_K configurations
+// rows per row group of the streamed kernel (8 waves x 32 rows)
 constexpr int32_t kQ4kTileRows = 256;
 
-template <int WM, int WN, int MW, int NW>
-hipError_t launch_q4k_t(const MbMats& m, const _Float16* xhl, const _Float16* pq, const float* rscale, int32_t b,
-                        int32_t k, const Q4kPlan& p, float* part, hipStream_t stream) {
-    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
-    const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
-    // XCD tile order: the block split with the least operand traffic, counting
-    // a weight tile (BN rows of the K range) once per XCD that reads it, and
-    // an activation tile (BM tokens of the K range as fp16 pairs) likewise
-    MbMats mx = m;
-    mx.xcd_a = 0;
-#if GNCX_MB_XCD
-    const double wt = static_cast<double>(BN) * (p.kchunk / 256) * 144.0;
-    const double at = static_cast<double>(BM) * p.kchunk * 4.0;
-    const int gx = static_cast<int>(grid.x), gy = static_cast<int>(grid.y);
-    double best = gx * wt + 8.0 * gy * at;  // grid order (with gx % 8 == 0, the same as a = 8)
-    if ((gx * gy) % 8 == 0) {
-        for (int a = 1; a < 8; a *= 2) {
-            if (gx % a != 0 || gy % (8 / a) != 0) continue;
-            const double cost = 8.0 * gx * wt / a + 8.0 * gy * at / (8 / a);
-            if (cost < best) {
-                best = cost;
-                mx.xcd_a = a;
-            }
-        }
-    }
-#endif
-    hipLaunchKernelGGL((matbatch_q4k_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, mx,
-                       row_bytes(kQ4_K, k), xhl, pq, rscale, b, k, p.kchunk, part);
-    return hipGetLastError();
-}
-
-// Long batches with whole K per work-group (B >= 1024, no split) run the
-// one-product kernel; their activations are q as fp16 in xhl's first B K
-// halves and the blocks' d / s after them (the pairs' space holds both).
-// Measured full calls, two-product against one-product kernel (us): B = 2048
-// 4096 x 4096 183-185 / 176, 4096 -> 12288 515-518 / 497, 12288 -> 4096
-// 534-537 / 473-477, 4096 -> 24576 969-973 / 938-942; but with K split
-// (4096 x 4096 at B = 256 / 512, 4096 -> 14336 at B = 256) 45 / 67 / 100
-// against 57 / 77 / 108, and 4096 -> 14336 at B = 512 (whole K) 165-167
-// against 168: the 16 fmas per tile and block cost more than the halved
-// matrix-core work saves unless the halved activation bytes dominate.
-#ifndef GNCX_Q4K_ONE
-#define GNCX_Q4K_ONE 1
-#endif
-bool q4k_one(const Q4kPlan& p, int32_t b) { return GNCX_Q4K_ONE && p.cfg == 0 && p.splits == 1 && b >= 1024; }
+// the streamed kernel's activations: q as fp16 in xhl's first B K halves and
+// the blocks' d / s after them (the pairs' space holds both)
 float* q4k_dxs(_Float16* xhl, int32_t b, int32_t k) { return reinterpret_cast<float*>(xhl + static_cast<size_t>(b) * k); }
 
 void launch_q4k_act(const float* x, int32_t b, int32_t k, _Float16* xhl, float* rscale, _Float16* pq,
-                    const Q4kPlan& p, hipStream_t stream, const float* up) {
-    if (q4k_one(p, b) || p.cfg == 8) launch_act_q(x, b, k, xhl, q4k_dxs(xhl, b, k), rscale, pq, stream, up);
-    else launch_act_hilo(x, b, k, xhl, rscale, pq, stream, up);
-}
-
-template <int WM, int WN, int MW, int NW>
-hipError_t launch_q4k1_t(const MbMats& m, const _Float16* xq, const float* dxs, const _Float16* pq,
-                         const float* rscale, int32_t b, int32_t k, const Q4kPlan& p, float* part,
-                         hipStream_t stream) {
-    constexpr int BM = 32 * WM * MW, BN = 32 * WN * NW;
-    const int32_t tiles = m.tile0[m.count - 1] + (m.n[m.count - 1] + BN - 1) / BN;
-    const dim3 grid(tiles, (b + BM - 1) / BM, p.splits);
-    MbMats mx = m;
-    mx.xcd_a = 0;
-#if GNCX_MB_XCD
-    // as launch_q4k_t, the activation tile now q alone (2 bytes per value)
-    const double wt = static_cast<double>(BN) * (p.kchunk / 256) * 144.0;
-    const double at = static_cast<double>(BM) * p.kchunk * 2.0;
-    const int gx = static_cast<int>(grid.x), gy = static_cast<int>(grid.y);
-    double best = gx * wt + 8.0 * gy * at;
-    if ((gx * gy) % 8 == 0) {
-        for (int a = 1; a < 8; a *= 2) {
-            if (gx % a != 0 || gy % (8 / a) != 0) continue;
-            const double cost = 8.0 * gx * wt / a + 8.0 * gy * at / (8 / a);
-            if (cost < best) {
-                best = cost;
-                mx.xcd_a = a;
-            }
-        }
-    }
-#endif
-    hipLaunchKernelGGL((matbatch_q4k1_kernel<WM, WN, MW, NW>), grid, dim3(64 * MW * NW), 0, stream, mx,
-                       row_bytes(kQ4_K, k), xq, dxs, pq, rscale, b, k, p.kchunk, part);
-    return hipGetLastError();
+                    hipStream_t stream, const float* up) {
+    launch_act_q(x, b, k, xhl, q4k_dxs(xhl, b, k), rscale, pq, stream, up);
 }
 
 template <int TYPE>
@@ -2215,11 +1395,7 @@ hipError_t launch_q4k_mats(MbMats& m, _Float16* xhl, const _Float16* pq, const f
     }
     m.ntot = rows;
     r.count = m.count;
-    const hipError_t e =
-        p.cfg == 8    ? launch_qs<kQ4_K>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
-        : q4k_one(p, b) ? launch_q4k1_t<2, 2, 2, 4>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream)
-        : p.cfg == 0 ? launch_q4k_t<2, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream)
-                     : launch_q4k_t<1, 2, 2, 4>(m, xhl, pq, rscale, b, k, p, part, stream);
+    const hipError_t e = launch_qs<kQ4_K>(m, xhl, q4k_dxs(xhl, b, k), pq, rscale, b, k, p, part, stream);
     if (e != hipSuccess || p.splits == 1) return e;
     return launch_reduce(part, p.splits, r, stream);
 }
@@ -2227,7 +1403,7 @@ hipError_t launch_q4k_mats(MbMats& m, _Float16* xhl, const _Float16* pq, const f
 hipError_t launch_q4k(const uint8_t* w, const float* x, int32_t b, int32_t k, int32_t n, float* y, _Float16* xhl,
                       _Float16* pq, float* rscale, float* part, hipStream_t stream, const float* up) {
     const Q4kPlan p = q4k_plan(b, k, n);
-    launch_q4k_act(x, b, k, xhl, rscale, pq, p, stream, up);
+    launch_q4k_act(x, b, k, xhl, rscale, pq, stream, up);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
@@ -2254,7 +1430,7 @@ hipError_t launch_t(const uint8_t* w, const float* x, int32_t b, int32_t k, int3
 }  // namespace
 
 // fp16 pairs of the quantised activations [B x K x 2] (or, for the
-// one-product Q4_K kernel, q [B x K] and the blocks' d / s [B x K / 32]),
+// streamed Q4_K / Q6_K kernel, q [B x K] and the blocks' d / s [B x K / 32]),
 // their row scales [B], then the split-K partials [splits x B x N]
 static size_t xh_bytes(int32_t b, int32_t k) {
     return (static_cast<size_t>(b) * k * 2 * sizeof(_Float16) + 255) & ~static_cast<size_t>(255);
@@ -2368,7 +1544,7 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
     float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
     float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
-    launch_q4k_act(x, b, k, xhl, rscale, pq, p, stream, nullptr);
+    launch_q4k_act(x, b, k, xhl, rscale, pq, stream, nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};
