@@ -140,6 +140,7 @@ SIGNATURES = {
          _f32, _fp],
     ),
     "gncx_hip_matvec_multi_addnorm": (None, [_fp, _fp, _vp, _sz, _f32, _fp, _i32, _vp, _vp, _i32, _i32, _vp]),
+    "gncx_hip_matbatch_multi_addnorm": (None, [_fp, _fp, _vp, _sz, _f32, _i32, _vp, _vp, _i32, _i32, _i32, _vp]),
     "gncx_hip_matvec_swiglu": (None, [_vp, _vp, _i32, _fp, _i32, _i32, _fp]),
     "gncx_hip_decode_step": (C.c_int, [_vp, _vp, _i32, _i32, _i32]),
     "gncx_hip_decode_step_noalloc": (C.c_int, [_vp, _vp, _i32, _i32, _i32]),

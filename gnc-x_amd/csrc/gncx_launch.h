@@ -74,6 +74,17 @@ size_t matbatch_multi_workspace_bytes(int32_t type, int32_t count, const int32_t
 hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
                                  const float* x, int32_t b, int32_t k, float* const* ys, void* workspace,
                                  size_t workspace_bytes, hipStream_t stream);
+// launch_matbatch_multi of the RMSNorm (gamma, eps) of the rows h after the
+// optional residual add h += r (r may be null; h is updated in place), the
+// norm and the quantisation in one kernel: the outputs of
+// launch_add_rmsnorm_rows (or launch_rmsnorm) into a buffer followed by
+// launch_matbatch_multi on it.  hipErrorNotSupported where the fused form does
+// not apply (not a one-launch Q4_K plan, K over 16384, unaligned rows): the
+// caller then runs the two steps.
+hipError_t launch_matbatch_multi_norm(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                                      float* h, const float* r, const float* gamma, float eps, int32_t b, int32_t k,
+                                      float* const* ys, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream);
 
 // cos/sin of one RoPE position, computed on the host with the C library's
 // powf/cosf/sinf exactly as the reference does (cpp:1779-1796), passed to

@@ -2445,6 +2445,61 @@ GNCX_API void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* de
     check(launch_gemv_multi(ggml_type, count, ws, out_dims, xn, in_dim, out_vecs, g_rt.stream), where);
 }
 
+// The batch form: hidden += delta over batch_size rows (delta may be NULL:
+// hidden is left as it is), then gncx_hip_matbatch_multi of the rows'
+// RMSNorm, the norm formed inside the activation pass where the plan allows.
+GNCX_API void gncx_hip_matbatch_multi_addnorm(float* hidden, const float* delta, const uint8_t* mmap_base,
+                                              size_t norm_weight_offset, float eps, int32_t count,
+                                              const uint8_t* const* weights, const int32_t* out_dims,
+                                              int32_t ggml_type, int32_t batch_size, int32_t in_dim,
+                                              float* const* out_batches) {
+    std::lock_guard<CallLock> lk(g_mu);
+    const char* where = "gncx_hip_matbatch_multi_addnorm";
+    g_norm_epoch++;
+    if (count <= 0 || count > 4 || !weights || !out_dims || !out_batches || !hidden || in_dim <= 0 ||
+        batch_size <= 0) {
+        set_error(where, "count 1..4 with weights, out_dims, outputs, hidden and positive sizes", -1);
+        return;
+    }
+    if (!type_supported(ggml_type) || !ensure_runtime(where)) return;
+    if (!all_device({hidden, delta})) {
+        set_error(where, "hidden and delta must be device memory", -1);
+        return;
+    }
+    const float* g = reinterpret_cast<const float*>(
+        device_weights(mmap_base + norm_weight_offset, sizeof(float) * static_cast<size_t>(in_dim), where));
+    if (!g) return;
+    const uint8_t* ws[4];
+    for (int32_t i = 0; i < count; ++i) {
+        if (out_dims[i] <= 0 || !weights[i] || !out_batches[i] || !is_device_ptr(out_batches[i])) {
+            set_error(where, "every matrix needs weights, out_dims > 0 and a device output", -1);
+            return;
+        }
+        ws[i] = device_weights(weights[i], row_bytes(ggml_type, in_dim) * static_cast<size_t>(out_dims[i]), where);
+        if (!ws[i]) return;
+    }
+    if (!g_rt.ws.ensure(matbatch_multi_workspace_bytes(ggml_type, count, out_dims, batch_size, in_dim), where))
+        return;
+    const hipError_t e = launch_matbatch_multi_norm(ggml_type, count, ws, out_dims, hidden, delta, g, eps, batch_size,
+                                                    in_dim, out_batches, g_rt.ws.p, g_rt.ws.cap, g_rt.stream);
+    if (e != hipErrorNotSupported) {
+        check(e, where);
+        return;
+    }
+    // the two steps, same values: the normed rows in a staging buffer
+    const size_t n = static_cast<size_t>(batch_size) * in_dim;
+    if (!g_rt.v.ensure(sizeof(float) * n, where)) return;
+    float* xn = g_rt.v.as<float>();
+    if (delta) {
+        if (!check(launch_add_rmsnorm_rows(hidden, delta, g, batch_size, in_dim, eps, xn, g_rt.stream), where)) return;
+    } else if (!check(launch_rmsnorm(hidden, g, batch_size, in_dim, eps, xn, g_rt.stream), where)) {
+        return;
+    }
+    check(launch_matbatch_multi(ggml_type, count, ws, out_dims, xn, batch_size, in_dim, out_batches, g_rt.ws.p,
+                                g_rt.ws.cap, g_rt.stream),
+          where);
+}
+
 GNCX_API void gncx_hip_matvec_swiglu(const uint8_t* gate_weights, const uint8_t* up_weights, int32_t ggml_type,
                                      const float* in_vec, int32_t in_dim, int32_t ffn_dim, float* out_act) {
     std::lock_guard<CallLock> lk(g_mu);

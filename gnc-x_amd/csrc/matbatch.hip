@@ -113,6 +113,37 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // go out instead of the pairs, as fp16 (integers of at most 127, exact):
 // xhl holds 4 of them per task, row-major [B x K], and dxs (set) each
 // 32-block's d / s as fp32 [B x K / 32]; P as above.
+// One task's QX outputs (4 values of row `row`, task t of k / 4, at the
+// row's 1 / s = inv): q as fp16, the block's d / s from its first lane and,
+// with pq, the block's P pair.  Whole 8-lane groups call it together.
+__device__ __forceinline__ void emit_qx(const float4 v, int32_t t, int32_t row, int32_t k, float inv,
+                                        uint2* __restrict xq, float* __restrict dxs, _Float16* __restrict pq) {
+    const int32_t tasks = k / 4;
+    int q0, q1, q2, q3;
+    float d;
+    quantize_values(v, q0, q1, q2, q3, d);
+    auto h2 = [](int a, int b) {
+        return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
+               (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
+    };
+    xq[static_cast<size_t>(row) * tasks + t] = make_uint2(h2(q0, q1), h2(q2, q3));
+    if ((t & 7) == 0) dxs[static_cast<size_t>(row) * (k / 32) + (t >> 3)] = d * inv;
+    if (pq) {
+        // the 8 lanes of block t / 8: quad sums, then lane i adds lane 7 - i
+        const int s4 = quad_sum(q0 + q1 + q2 + q3);
+        const int sum = s4 + __builtin_amdgcn_mov_dpp(s4, 0x141, 0xf, 0xf, false);
+        if ((t & 7) == 0) {
+            const int32_t blk = t >> 3;
+            const float pv = (static_cast<float>(sum) * d) * inv;
+            const _Float16 ph = static_cast<_Float16>(pv);
+            const _Float16 pl = static_cast<_Float16>(pv - static_cast<float>(ph));
+            _Float16* pr = pq + (static_cast<size_t>(row) * (k / 256) + blk / 8) * 16 + (blk & 7);
+            pr[0] = ph;
+            pr[8] = pl;
+        }
+    }
+}
+
 template <int kHiloU, bool SW = false, bool QX = false>
 __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
                                                             uint2* __restrict xhl, float* __restrict rscale,
@@ -159,17 +190,12 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
     if (threadIdx.x == 0) rscale[row] = sc;
     uint2* out = xhl + static_cast<size_t>(row) * tasks * 2;
     auto emit = [&](const float4 v, int32_t t) {
-        int q0, q1, q2, q3;
-        float d;
-        quantize_values(v, q0, q1, q2, q3, d);
         if constexpr (QX) {
-            auto h2 = [](int a, int b) {
-                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a))) |
-                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(b))) << 16);
-            };
-            xhl[static_cast<size_t>(row) * tasks + t] = make_uint2(h2(q0, q1), h2(q2, q3));
-            if ((t & 7) == 0) dxs[static_cast<size_t>(row) * (k / 32) + (t >> 3)] = d * inv;
+            emit_qx(v, t, row, k, inv, xhl, dxs, pq);
         } else {
+            int q0, q1, q2, q3;
+            float d;
+            quantize_values(v, q0, q1, q2, q3, d);
             uint2 hi, lo;
             split2((static_cast<float>(q0) * d) * inv, (static_cast<float>(q1) * d) * inv, hi.x, lo.x);
             split2((static_cast<float>(q2) * d) * inv, (static_cast<float>(q3) * d) * inv, hi.y, lo.y);
@@ -177,19 +203,19 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
             uint2* c = out + 4 * (t >> 1) + (t & 1);
             c[0] = hi;
             c[2] = lo;
-        }
-        if (pq) {
-            // the 8 lanes of block t / 8: quad sums, then lane i adds lane 7 - i
-            const int s4 = quad_sum(q0 + q1 + q2 + q3);
-            const int sum = s4 + __builtin_amdgcn_mov_dpp(s4, 0x141, 0xf, 0xf, false);
-            if ((t & 7) == 0) {
-                const int32_t blk = t >> 3;
-                const float pv = (static_cast<float>(sum) * d) * inv;
-                const _Float16 ph = static_cast<_Float16>(pv);
-                const _Float16 pl = static_cast<_Float16>(pv - static_cast<float>(ph));
-                _Float16* pr = pq + (static_cast<size_t>(row) * (k / 256) + blk / 8) * 16 + (blk & 7);
-                pr[0] = ph;
-                pr[8] = pl;
+            if (pq) {
+                // the 8 lanes of block t / 8: quad sums, then lane i adds lane 7 - i
+                const int s4 = quad_sum(q0 + q1 + q2 + q3);
+                const int sum = s4 + __builtin_amdgcn_mov_dpp(s4, 0x141, 0xf, 0xf, false);
+                if ((t & 7) == 0) {
+                    const int32_t blk = t >> 3;
+                    const float pv = (static_cast<float>(sum) * d) * inv;
+                    const _Float16 ph = static_cast<_Float16>(pv);
+                    const _Float16 pl = static_cast<_Float16>(pv - static_cast<float>(ph));
+                    _Float16* pr = pq + (static_cast<size_t>(row) * (k / 256) + blk / 8) * 16 + (blk & 7);
+                    pr[0] = ph;
+                    pr[8] = pl;
+                }
             }
         }
     };
@@ -222,6 +248,99 @@ void launch_act_q(const float* x, int32_t b, int32_t k, _Float16* xq, float* dxs
         hipLaunchKernelGGL((act_hilo_kernel<16, false, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
                            pq, nullptr, dxs);
     }
+}
+
+// launch_act_q of the RMSNorm of each row, after the optional residual add
+// (h += r, written back), in one launch.  The norm is rmsnorm_kernel's
+// (elementwise.hip) with its thread layout (1024 threads, float4 t = thread +
+// 1024 j, up to 4 per thread), sum order and operation order, so the rows
+// quantised are those gncx_hip_add_rmsnorm_rows / gncx_hip_rmsnorm_rows
+// write; the quantisation is act_hilo_kernel's (a row maximum, then 8
+// consecutive lanes per 32-block).
+constexpr int kNaThreads = 1024;
+constexpr int kNaRegs = 4;
+template <bool ADD>
+__global__ __launch_bounds__(kNaThreads) void norm_act_q_kernel(const float* x, const float* r, float* xo,
+                                                               const float* __restrict g, int32_t k, float eps,
+                                                               uint2* __restrict xq, float* __restrict dxs,
+                                                               float* __restrict rscale, _Float16* __restrict pq) {
+#pragma clang fp contract(off)
+    __shared__ float part[kNaThreads / 64];
+    __shared__ float red[kNaThreads / 64];
+    const int32_t row = blockIdx.x, n4 = k / 4;
+    const int tid = threadIdx.x;
+    const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
+    const float4* r4 = reinterpret_cast<const float4*>(ADD ? r + static_cast<size_t>(row) * k : nullptr);
+    float4* xo4 = reinterpret_cast<float4*>(ADD ? xo + static_cast<size_t>(row) * k : nullptr);
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    float4 xv[kNaRegs], gv[kNaRegs];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNaRegs; ++j) {
+        const int32_t t = tid + kNaThreads * j;
+        if (t < n4) {
+            xv[j] = x4[t];
+            if (ADD) {
+                const float4 b = r4[t];
+                xv[j] = make_float4(xv[j].x + b.x, xv[j].y + b.y, xv[j].z + b.z, xv[j].w + b.w);
+                xo4[t] = xv[j];
+            }
+            gv[j] = g4[t];
+            s += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+        }
+    }
+    s = wave_sum(s);
+    if ((tid & 63) == 0) part[tid >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNaThreads / 64; ++w) tot += part[w];
+    const float inv_rms = 1.0f / sqrtf(tot / static_cast<float>(k) + eps);
+    float4 yv[kNaRegs];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kNaRegs; ++j) {
+        const int32_t t = tid + kNaThreads * j;
+        yv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (t < n4) {
+            yv[j] = make_float4(xv[j].x * inv_rms * gv[j].x, xv[j].y * inv_rms * gv[j].y,
+                                xv[j].z * inv_rms * gv[j].z, xv[j].w * inv_rms * gv[j].w);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(yv[j].x), fabsf(yv[j].y)), fmaxf(fabsf(yv[j].z), fabsf(yv[j].w))));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < kNaThreads / 64; ++w) m = fmaxf(m, red[w]);
+    const float sc = m > 0.0f && m <= 3.0e38f ? ldexpf(1.0f, ilogbf(m) + 1) : 1.0f;  // power of two > m
+    const float inv = 1.0f / sc;                                                     // exact
+    if (tid == 0) rscale[row] = sc;
+#pragma unroll
+    for (int j = 0; j < kNaRegs; ++j) {
+        const int32_t t = tid + kNaThreads * j;
+        if (t < n4) emit_qx(yv[j], t, row, k, inv, xq, dxs, pq);
+    }
+}
+
+// false when the fused form does not apply (then norm and quantise apart)
+bool norm_act_fits(const float* h, const float* r, const float* gamma, int32_t k) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(r) |
+                         reinterpret_cast<uintptr_t>(gamma);
+    return k > 0 && k % 256 == 0 && k / 4 <= kNaThreads * kNaRegs && (al & 15u) == 0;
+}
+
+void launch_norm_act_q(float* h, const float* r, const float* gamma, float eps, int32_t b, int32_t k, _Float16* xq,
+                       float* dxs, float* rscale, _Float16* pq, hipStream_t stream) {
+    uint2* o = reinterpret_cast<uint2*>(xq);
+    if (r)
+        hipLaunchKernelGGL(norm_act_q_kernel<true>, dim3(b), dim3(kNaThreads), 0, stream, h, r, h, gamma, k, eps, o,
+                           dxs, rscale, pq);
+    else
+        hipLaunchKernelGGL(norm_act_q_kernel<false>, dim3(b), dim3(kNaThreads), 0, stream, h, nullptr, nullptr,
+                           gamma, k, eps, o, dxs, rscale, pq);
 }
 
 // up non-null: the rows are SwiGLU(x, up)
@@ -1545,6 +1664,39 @@ hipError_t launch_matbatch_multi(int32_t type, int32_t count, const uint8_t* con
     float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
     if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
     launch_q4k_act(x, b, k, xhl, rscale, pq, stream, nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    MbMats m{};
+    for (int32_t i = 0; i < count; ++i) {
+        m.w[i] = ws[i];
+        m.y[i] = ys[i];
+        m.n[i] = ns[i];
+    }
+    m.count = count;
+    return launch_q4k_mats(m, xhl, pq, rscale, b, k, p, part, stream);
+}
+
+hipError_t launch_matbatch_multi_norm(int32_t type, int32_t count, const uint8_t* const* ws, const int32_t* ns,
+                                      float* h, const float* r, const float* gamma, float eps, int32_t b, int32_t k,
+                                      float* const* ys, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+    if (count <= 0 || count > kMaxMbMats || !ws || !ns || !ys || !h || !gamma) return hipErrorInvalidValue;
+    for (int32_t i = 0; i < count; ++i)
+        if (ns[i] <= 0 || !ws[i] || !ys[i]) return hipErrorInvalidValue;
+    Q4kPlan p;
+    int64_t total;
+    if (!multi_fused(type, count, ns, b, k, p, total) || !norm_act_fits(h, r, gamma, k)) return hipErrorNotSupported;
+    if (workspace_bytes < matbatch_multi_workspace_bytes(type, count, ns, b, k)) return hipErrorInvalidValue;
+    if (k > (1 << 20) || b > 65535 || (row_bytes(kQ4_K, k) & 15u) != 0) return hipErrorInvalidValue;
+    for (int32_t i = 0; i < count; ++i)
+        if ((reinterpret_cast<uintptr_t>(ws[i]) & 15u) != 0) return hipErrorInvalidValue;
+    char* wsp = static_cast<char*>(workspace);
+    _Float16* xhl = reinterpret_cast<_Float16*>(wsp);
+    _Float16* pq = reinterpret_cast<_Float16*>(wsp + xh_bytes(b, k));
+    float* rscale = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k));
+    float* part = reinterpret_cast<float*>(wsp + xh_bytes(b, k) + pq_bytes(kQ4_K, b, k) + rscale_bytes(b));
+    if ((reinterpret_cast<uintptr_t>(xhl) & 255u) != 0) return hipErrorInvalidValue;
+    launch_norm_act_q(h, r, gamma, eps, b, k, xhl, q4k_dxs(xhl, b, k), rscale, pq, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     MbMats m{};

@@ -33,9 +33,10 @@ differences are where the streamer works on host memory:
   results: in decode, gncx_hip_attention_step_fused for the four
   prologue+attention calls, gncx_hip_matvec_multi for Q/K/V and for gate/up
   (one launch each) and gncx_hip_add_rmsnorm for each residual add and the
-  RMSNorm after it; in prefill, gncx_hip_rmsnorm_rows for the per-token
-  RMSNorm loops, gncx_hip_fetch_token_embeddings for the embedding rows,
-  gncx_hip_matbatch_multi for Q/K/V and for gate/up, and
+  RMSNorm after it; in prefill, gncx_hip_fetch_token_embeddings for the
+  embedding rows, gncx_hip_matbatch_multi_addnorm for Q/K/V and for gate/up
+  with the per-token residual add + RMSNorm loops before them folded in,
+  gncx_hip_swiglu_matbatch for the down projection, and
   gncx_hip_attention_prefill for the per-token prologue + attention loop
   (one causal batch).
 
@@ -573,30 +574,25 @@ class Decoder:
         return self._lm_head()
 
     def _prefill_fused(self, B, bh, bn, bq, bk, bv, ba, bp, bg, bu, bf):
-        """prefill's layers with the extensions: every token's RMSNorm in one
-        launch (with the residual add before it), the per-token prologue +
+        """prefill's layers with the extensions: every token's RMSNorm (with
+        the residual add before it) inside the next matbatch's activation
+        pass (gncx_hip_matbatch_multi_addnorm), the per-token prologue +
         attention loop as one causal batch (gncx_hip_attention_prefill), and
         the SwiGLU inside the down projection's matbatch."""
         s, L, m = self.s, self.lib, self.m
+        self._norm_rows = bn
         for l in range(s.n_layers):
             p = f"blk.{l}"
-            # the previous layer's residual add goes into this layer's first norm
-            if l == 0:
-                L.gncx_hip_rmsnorm_rows(bh.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"), s.embed, s.eps,
-                                        bn.data_ptr())
-            else:
-                L.gncx_hip_add_rmsnorm_rows(bh.data_ptr(), bp.data_ptr(), B, m.base, m.off(f"{p}.attn_norm.weight"),
-                                            s.embed, s.eps, bn.data_ptr())
-            self._matbatch_multi(p, "qkv", bn.data_ptr(), B, s.embed, (s.q_dim, s.kv_dim, s.kv_dim),
-                                 (bq, bk, bv))
+            # the previous layer's residual add and this layer's first norm go
+            # into the Q/K/V matbatch's activation pass
+            self._matbatch_multi_addnorm(p, "qkv", "attn_norm", bh, None if l == 0 else bp, B,
+                                         (s.q_dim, s.kv_dim, s.kv_dim), (bq, bk, bv))
             L.gncx_hip_attention_prefill(bq.data_ptr(), bk.data_ptr(), bv.data_ptr(), self.kc[l].data_ptr(),
                                          self.vc[l].data_ptr(), 0, B, s.n_heads, s.n_kv, s.head_dim, self.scale, 0,
                                          m.base, m.off(f"{p}.attn_q_norm.weight"), m.off(f"{p}.attn_k_norm.weight"),
                                          1, s.eps, 0, 0, s.rope_base, ba.data_ptr())
             self._matbatch(f"{p}.attn_output.weight", ba.data_ptr(), B, s.q_dim, s.embed, bp.data_ptr())
-            L.gncx_hip_add_rmsnorm_rows(bh.data_ptr(), bp.data_ptr(), B, m.base, m.off(f"{p}.ffn_norm.weight"),
-                                        s.embed, s.eps, bn.data_ptr())
-            self._matbatch_multi(p, ("ffn_gate", "ffn_up"), bn.data_ptr(), B, s.embed, (s.ffn, s.ffn), (bg, bu))
+            self._matbatch_multi_addnorm(p, ("ffn_gate", "ffn_up"), "ffn_norm", bh, bp, B, (s.ffn, s.ffn), (bg, bu))
             # SwiGLU formed by the down projection's activation pass
             L.gncx_hip_swiglu_matbatch(m.base, m.off(f"{p}.ffn_down.weight"), s.layer_type, bg.data_ptr(),
                                        bu.data_ptr(), B, s.ffn, s.embed, bp.data_ptr())
@@ -604,16 +600,31 @@ class Decoder:
         self.hidden.copy_(bh[B - 1])
         return self._lm_head()
 
-    def _matbatch_multi(self, p, names, x, b, in_dim, out_dims, outs):
-        """gncx_hip_matbatch_multi over tensors {p}.{name}.weight (names "qkv"
-        stands for attn_q, attn_k, attn_v)."""
+    def _matbatch_multi_addnorm(self, p, names, norm, hidden, delta, b, out_dims, outs):
+        """gncx_hip_matbatch_multi_addnorm: hidden += delta (None: no add), then
+        the matrices {p}.{name}.weight applied to the RMSNorm ({p}.{norm}.weight)
+        of the rows; on host buffers the two calls it fuses, the rows normed
+        into the prefill's norm buffer."""
         P, I = C.c_void_p, C.c_int32
         if names == "qkv":
             names = ("attn_q", "attn_k", "attn_v")
         n = len(names)
         w = (P * n)(*(self.m.base + self.m.off(f"{p}.{nm}.weight") for nm in names))
         y = (P * n)(*(t.data_ptr() for t in outs))
-        self.lib.gncx_hip_matbatch_multi(n, w, (I * n)(*out_dims), self.s.layer_type, x, b, in_dim, y)
+        if not hidden.is_cuda:
+            # host buffers (the entry takes device memory): the two calls it fuses
+            L, g, bn = self.lib, self.m.off(f"{p}.{norm}.weight"), self._norm_rows
+            if delta is None:
+                L.gncx_hip_rmsnorm_rows(hidden.data_ptr(), b, self.m.base, g, self.s.embed, self.s.eps,
+                                        bn.data_ptr())
+            else:
+                L.gncx_hip_add_rmsnorm_rows(hidden.data_ptr(), delta.data_ptr(), b, self.m.base, g, self.s.embed,
+                                            self.s.eps, bn.data_ptr())
+            L.gncx_hip_matbatch_multi(n, w, (I * n)(*out_dims), self.s.layer_type, bn.data_ptr(), b, self.s.embed, y)
+            return
+        self.lib.gncx_hip_matbatch_multi_addnorm(hidden.data_ptr(), None if delta is None else delta.data_ptr(),
+                                                 self.m.base, self.m.off(f"{p}.{norm}.weight"), self.s.eps, n, w,
+                                                 (I * n)(*out_dims), self.s.layer_type, b, self.s.embed, y)
 
     def greedy(self, logits) -> int:
         return int(self.torch.argmax(logits).item())

@@ -350,6 +350,17 @@ void gncx_hip_matvec_multi_addnorm(const float* hidden, const float* delta, cons
                                    size_t norm_weight_offset, float eps, float* hidden_out, int32_t count,
                                    const uint8_t* const* weights, const int32_t* out_dims, int32_t ggml_type,
                                    int32_t in_dim, float* const* out_vecs);
+/* The prefill's form over batch_size rows (device memory): hidden += delta
+ * (delta may be NULL, leaving hidden as it is), then out_batches[i] = W_i . x
+ * with x the rows' RMSNorm, formed inside the matbatch's activation pass where
+ * its plan allows (Q4_K matrices of one launch, in_dim up to 16384).  The
+ * same values as gncx_hip_add_rmsnorm_rows (or gncx_hip_rmsnorm_rows) into a
+ * buffer followed by gncx_hip_matbatch_multi of it (lua/gncx_streamer.lua
+ * 1122 then 1126-1132 and 1135-1136; 1059-1065 then 1068-1071). */
+void gncx_hip_matbatch_multi_addnorm(float* hidden, const float* delta, const uint8_t* mmap_base,
+                                     size_t norm_weight_offset, float eps, int32_t count,
+                                     const uint8_t* const* weights, const int32_t* out_dims, int32_t ggml_type,
+                                     int32_t batch_size, int32_t in_dim, float* const* out_batches);
 /* out_act = SiLU(W_gate . x) * (W_up . x) in one launch: the values of two
  * gncx_xfold_universal_matvec calls followed by gncx_swiglu_activation
  * (lua/gncx_streamer.lua:890-894). */

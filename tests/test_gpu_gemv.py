@@ -388,6 +388,58 @@ def test_matbatch_multi_matches_single_calls(lib, oracle, ns, k, b):
             lib.gncx_hip_weight_forget(ptr(w))
 
 
+# gncx_hip_matbatch_multi_addnorm against its two steps, add+RMSNorm (or
+# RMSNorm alone) into a buffer and gncx_hip_matbatch_multi of it: bit for bit,
+# residual rows included.  Q4_K groups of whole 256-row tiles form the norm
+# inside the activation pass; (4096, 1000) and Q6_K run the two steps.
+ADDNORM_CASES = [(Q4_K, (4096, 1024, 1024), 4096, 64, True), (Q4_K, (4096, 1024, 1024), 4096, 2048, False),
+                 (Q4_K, (2048, 2048), 4096, 300, True), (Q4_K, (1536, 512), 5120, 77, True),
+                 (Q4_K, (4096, 1000), 2048, 129, True), (Q6_K, (512, 256), 1024, 40, True)]
+
+
+@pytest.mark.parametrize("t,ns,k,b,add", ADDNORM_CASES)
+def test_matbatch_multi_addnorm_matches_two_steps(lib, oracle, torch_mod, t, ns, k, b, add):
+    torch = torch_mod
+    ws = [synth.make_weights(t, n, k, seed=7300 + 3 * i + n) for i, n in enumerate(ns)]
+    rng = np.random.default_rng(7400 + b + k)
+    h0 = (rng.standard_normal((b, k)) * 3.0).astype(np.float32)
+    d0 = rng.standard_normal((b, k)).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    eps = 1e-6
+    dev = lambda a: torch.from_numpy(a).cuda()
+    h1, h2, dd = dev(h0), dev(h0), dev(d0)
+    xn = torch.zeros(b, k, dtype=torch.float32, device="cuda")
+    y1 = [torch.full((b, n), float("nan"), device="cuda") for n in ns]
+    y2 = [torch.full((b, n), float("nan"), device="cuda") for n in ns]
+    P, I = C.c_void_p * len(ns), C.c_int32 * len(ns)
+    wp = P(*(w.ctypes.data for w in ws))
+    torch.cuda.synchronize()
+    print(f"matbatch multi addnorm type={t} {ns} k={k} b={b} add={add}", flush=True)
+    try:
+        lib.gncx_hip_matbatch_multi_addnorm(h1.data_ptr(), dd.data_ptr() if add else None, gamma.ctypes.data, 0,
+                                            eps, len(ns), wp, I(*ns), t, b, k, P(*(y.data_ptr() for y in y1)))
+        gncx.check(lib)
+        if add:
+            lib.gncx_hip_add_rmsnorm_rows(h2.data_ptr(), dd.data_ptr(), b, gamma.ctypes.data, 0, k, eps,
+                                          xn.data_ptr())
+        else:
+            lib.gncx_hip_rmsnorm_rows(h2.data_ptr(), b, gamma.ctypes.data, 0, k, eps, xn.data_ptr())
+        gncx.check(lib)
+        lib.gncx_hip_matbatch_multi(len(ns), wp, I(*ns), t, xn.data_ptr(), b, k, P(*(y.data_ptr() for y in y2)))
+        gncx.check(lib)
+        assert lib.gncx_hip_synchronize() == 0
+    finally:
+        for w in ws:
+            lib.gncx_hip_weight_forget(ptr(w))
+    assert torch.equal(h1, h2)
+    assert np.array_equal(h1.cpu().numpy(), h0 + d0 if add else h0)
+    x = xn.cpu().numpy()
+    for w, n, a, c in zip(ws, ns, y1, y2):
+        a, c = a.cpu().numpy(), c.cpu().numpy()
+        assert np.array_equal(a, c)
+        assert rel_l2(a, oracle.matbatch(t, w, x, b, k, n)) < TOL_MATBATCH
+
+
 def test_lm_head_and_softcap(lib, golden):
     w, x = golden["lm_w"].copy(), golden["lm_x"].copy()
     v, k = int(golden["lm_vocab"]), int(golden["lm_k"])
