@@ -92,7 +92,9 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 // max pass to the quantising pass (rows up to 4 kThreads U values): the
 // loads of a row are issued together, and a longer row reads its tail again.
 // U = 4 covers 4096-wide rows at 40-odd registers; wider rows take U = 16
-// (130-odd registers, 3 waves per SIMD).
+// (130-odd registers, 3 waves per SIMD), or, for the SwiGLU rows of the down
+// projection up to 12288 wide, 1024 threads (NT) with U = 3, which keeps more
+// of a row's loads in flight (47.9 -> 45.1 us at 2048 x 12288).
 
 // The reference's per-32 quantisation of row blockIdx.x of x (cpp:955-995),
 // each quantised value a = q * d (one fp32 rounding) scaled by 1 / s, where
@@ -144,12 +146,12 @@ __device__ __forceinline__ void emit_qx(const float4 v, int32_t t, int32_t row, 
     }
 }
 
-template <int kHiloU, bool SW = false, bool QX = false>
-__global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restrict x, int32_t k,
+template <int kHiloU, bool SW = false, bool QX = false, int NT = kThreads>
+__global__ __launch_bounds__(NT) void act_hilo_kernel(const float* __restrict x, int32_t k,
                                                             uint2* __restrict xhl, float* __restrict rscale,
                                                             _Float16* __restrict pq, const float* __restrict up,
                                                             float* __restrict dxs = nullptr) {
-    __shared__ float red[kThreads / 64];
+    __shared__ float red[NT / 64];
     const int32_t row = blockIdx.x, tasks = k / 4;
     const float4* xg = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
     const float4* xu = SW ? reinterpret_cast<const float4*>(up + static_cast<size_t>(row) * k) : nullptr;
@@ -171,20 +173,20 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
     float4 xv[kHiloU];
 #pragma unroll
     for (int u = 0; u < kHiloU; ++u) {
-        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * kThreads;
+        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * NT;
         xv[u] = t < tasks ? xr[t] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float m = 0.0f;
 #pragma unroll
     for (int u = 0; u < kHiloU; ++u) m = fmaxf(m, amax4(xv[u]));
-    for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) m = fmaxf(m, amax4(xr[t]));
+    for (int32_t t = threadIdx.x + kHiloU * NT; t < tasks; t += NT) m = fmaxf(m, amax4(xr[t]));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = red[0];
 #pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w]);
+    for (int w = 1; w < NT / 64; ++w) m = fmaxf(m, red[w]);
     const float sc = m > 0.0f && m <= 3.0e38f ? ldexpf(1.0f, ilogbf(m) + 1) : 1.0f;  // power of two > m
     const float inv = 1.0f / sc;                                       // exact
     if (threadIdx.x == 0) rscale[row] = sc;
@@ -220,13 +222,13 @@ __global__ __launch_bounds__(kThreads) void act_hilo_kernel(const float* __restr
         }
     };
     // whole 8-lane groups take the same branches and trip counts (tasks and
-    // kThreads are multiples of 8), as the group operations need
+    // NT are multiples of 8), as the group operations need
 #pragma unroll
     for (int u = 0; u < kHiloU; ++u) {
-        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * kThreads;
+        const int32_t t = static_cast<int32_t>(threadIdx.x) + u * NT;
         if (t < tasks) emit(xv[u], t);
     }
-    for (int32_t t = threadIdx.x + kHiloU * kThreads; t < tasks; t += kThreads) emit(xr[t], t);
+    for (int32_t t = threadIdx.x + kHiloU * NT; t < tasks; t += NT) emit(xr[t], t);
 }
 
 // the streamed kernel's activations: q as fp16 [B x K], then the blocks'
@@ -238,6 +240,9 @@ void launch_act_q(const float* x, int32_t b, int32_t k, _Float16* xq, float* dxs
         if (k <= 4 * 4 * kThreads)
             hipLaunchKernelGGL((act_hilo_kernel<4, true, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
                                pq, up, dxs);
+        else if (k <= 3 * 4 * 1024)  // up to 12288-wide rows: 16 waves, 3 float4 pairs each
+            hipLaunchKernelGGL((act_hilo_kernel<3, true, true, 1024>), dim3(b), dim3(1024), 0, stream, x, k, o,
+                               rscale, pq, up, dxs);
         else
             hipLaunchKernelGGL((act_hilo_kernel<16, true, true>), dim3(b), dim3(kThreads), 0, stream, x, k, o, rscale,
                                pq, up, dxs);
