@@ -440,6 +440,28 @@ def test_matbatch_multi_addnorm_matches_two_steps(lib, oracle, torch_mod, t, ns,
         assert rel_l2(a, oracle.matbatch(t, w, x, b, k, n)) < TOL_MATBATCH
 
 
+def test_matbatch_multi_addnorm_rejects_host_rows(lib, torch_mod):
+    """hidden, delta and the outputs must be device memory: host rows are
+    refused with an error before anything runs, and the host rows stay as
+    they were."""
+    torch = torch_mod
+    k, b, ns = 256, 4, (256, 256)
+    ws = [synth.make_weights(Q4_K, n, k, seed=7500 + n + i) for i, n in enumerate(ns)]
+    gamma = np.ones(k, np.float32)
+    h = np.arange(b * k, dtype=np.float32)
+    ys = [torch.zeros(b, n, device="cuda") for n in ns]
+    P, I = C.c_void_p * 2, C.c_int32 * 2
+    torch.cuda.synchronize()
+    lib.gncx_hip_matbatch_multi_addnorm(h.ctypes.data, None, gamma.ctypes.data, 0, 1e-6, 2,
+                                        P(*(w.ctypes.data for w in ws)), I(*ns), Q4_K, b, k,
+                                        P(*(y.data_ptr() for y in ys)))
+    with pytest.raises(RuntimeError, match="device memory"):
+        gncx.check(lib)
+    assert np.array_equal(h, np.arange(b * k, dtype=np.float32))
+    for w in ws:
+        lib.gncx_hip_weight_forget(ptr(w))
+
+
 def test_lm_head_and_softcap(lib, golden):
     w, x = golden["lm_w"].copy(), golden["lm_x"].copy()
     v, k = int(golden["lm_vocab"]), int(golden["lm_k"])
